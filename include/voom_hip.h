@@ -1,0 +1,136 @@
+/*
+ * voom_hip.h - C ABI of libvoom_hip.so, the MI355X (gfx950) kernels behind the
+ * paged-KV path: paged GQA decode attention, absorbed-MLA latent decode, the
+ * byte-plane spill codec and the page append/gather/scatter helpers.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise.  The
+ *     caller owns all memory (PyTorch tensors in the Python host layer).
+ *   - bf16 data is passed as raw 16-bit words (uint16_t bit patterns).
+ *   - Every entry point takes a hipStream_t (NULL = legacy default stream) and
+ *     only enqueues work; nothing synchronises.
+ *   - Return value: 0 on success; VOOM_EINVAL (negative) when an argument fails
+ *     validation; a positive hipError_t when a HIP call or launch fails.
+ *     voom_last_error() returns a thread-local message for the last failure.
+ *
+ * Device page layouts (one tensor per layer)
+ *   K pool  [num_slots, num_kv_heads, page_tokens, head_dim]   token-major
+ *   V pool  [num_slots, num_kv_heads, head_dim, page_tokens]   dim-major (V^T)
+ *   latent  [num_slots, page_tokens, latent_dim]               token-major
+ *   block_table [batch, max_pages] int32 slot ids, ctx_lens [batch] int32.
+ *   V is stored transposed inside each page so that the P.V contraction reads
+ *   16 contiguous bytes per lane straight into the MFMA operand.
+ */
+#ifndef VOOM_HIP_H
+#define VOOM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VOOM_OK 0
+#define VOOM_EINVAL (-1)
+
+/* Thread-local message describing the last non-zero return. */
+const char* voom_last_error(void);
+
+/* ABI version, bumped on any signature or layout change. */
+int voom_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Paged GQA decode attention (one query token per sequence).
+ *
+ * Replaces the decode attention of the reference: PagedKVCache.update
+ * concatenating every page (runtime/kv_paged.py:164-181) followed by
+ * mx.fast.scaled_dot_product_attention(q, K, V, scale=hd**-0.5) with the GQA
+ * broadcast inside SDPA (runtime/layer_runner.py:158,179-180), and the
+ * page-table-indirect Metal kernel position_free_paged_attention
+ * (runtime/pic_attention.py:184-232, page index ((blk*NKV+kvh)*BLOCK+off)*D).
+ *
+ *   q        [batch, num_q_heads, head_dim] bf16 (already RoPE-rotated)
+ *   out      [batch, num_q_heads, head_dim] bf16
+ *   lse_out  [batch, num_q_heads] fp32 natural-log sum-exp of the scaled
+ *            scores, or NULL.  Lets two calls over disjoint page sets be merged
+ *            with voom_merge_attn_states.
+ *   num_splits  number of wavefronts sharing the work (0 = library default);
+ *            the workspace must hold voom_paged_gqa_workspace_bytes(...) bytes
+ *            for the same value.
+ * head_dim in {64, 128}; num_q_heads / num_kv_heads <= 16; page_tokens a power
+ * of two >= 32.  Sequences with ctx_len 0 produce zeros (lse = -inf).
+ * ------------------------------------------------------------------------- */
+size_t voom_paged_gqa_workspace_bytes(int batch, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int num_splits);
+int voom_paged_gqa_default_splits(void);
+int voom_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
+                          const int32_t* block_table, const int32_t* ctx_lens,
+                          void* out, float* lse_out, void* workspace, size_t ws_bytes,
+                          int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                          int page_tokens, int max_pages, int num_slots, float scale,
+                          int num_splits, hipStream_t stream);
+
+/* Merge two attention states over disjoint key sets (log-sum-exp combine):
+ * out = (o_a*e^{lse_a} + o_b*e^{lse_b}) / (e^{lse_a} + e^{lse_b}).
+ * o_a/o_b/out [rows, head_dim] bf16, lse_* [rows] fp32; lse_out may be NULL.
+ * Replaces the running (max, sum, acc) merge of the reference's online key
+ * tiles (runtime/glm.py:165-196) and the simdgroup merge of the Metal kernel
+ * (runtime/pic_attention.py:106-129). */
+int voom_merge_attn_states(const void* o_a, const float* lse_a, const void* o_b,
+                           const float* lse_b, void* out, float* lse_out, int rows,
+                           int head_dim, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Page writes and reads.
+ *
+ * voom_append_kv writes L new tokens per sequence into the pools at logical
+ * positions pos[b] .. pos[b]+L-1 through the block table (slot write, no
+ * concatenation).  Replaces the tail concatenation and page close of
+ * PagedKVCache.update (runtime/kv_paged.py:143-158).
+ *   k_new, v_new [batch, num_kv_heads, L, head_dim] bf16 (contiguous)
+ *   positions    [batch] int32 first logical position of the new tokens
+ *
+ * voom_gather_kv materialises the logical K/V [batch, num_kv_heads, S, head_dim]
+ * (positions 0..S-1) from the pools: the reference's concatenated return value
+ * of PagedKVCache.update (runtime/kv_paged.py:176-181).
+ * ------------------------------------------------------------------------- */
+int voom_append_kv(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                   const int32_t* block_table, const int32_t* positions, int batch,
+                   int num_kv_heads, int new_tokens, int head_dim, int page_tokens,
+                   int max_pages, int num_slots, hipStream_t stream);
+int voom_gather_kv(const void* k_pool, const void* v_pool, const int32_t* block_table,
+                   void* k_out, void* v_out, int batch, int num_kv_heads, int seq_len,
+                   int head_dim, int page_tokens, int max_pages, int num_slots,
+                   hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Byte-plane codec (bit-exact).
+ *
+ * A little-endian 16-bit element e splits into lo = e & 0xff and hi = e >> 8;
+ * the planes hold byte 0 resp. byte 1 of every element in element order.
+ * Replaces formats/packed.py:49-50 / 277-282 (lo = raw[0::2], hi = raw[1::2])
+ * and the inverse interleave of packed.py:376-378.
+ *
+ * The _slots variants gather (split) or scatter (merge) whole pool slots of
+ * slot_bytes bytes each: slot i of the plane stream is slot slots[i] of the
+ * pool.  slot_bytes must be a multiple of 64.  `slots` is a device int32
+ * array of n_slots entries, each in [0, num_slots).
+ * ------------------------------------------------------------------------- */
+int voom_byteplane_split(const void* src, void* lo, void* hi, size_t n_elems,
+                         hipStream_t stream);
+int voom_byteplane_merge(const void* lo, const void* hi, void* dst, size_t n_elems,
+                         hipStream_t stream);
+int voom_byteplane_split_slots(const void* pool, const int32_t* slots, int n_slots,
+                               size_t slot_bytes, int num_slots, void* lo, void* hi,
+                               hipStream_t stream);
+int voom_byteplane_merge_slots(const void* lo, const void* hi, void* pool,
+                               const int32_t* slots, int n_slots, size_t slot_bytes,
+                               int num_slots, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOOM_HIP_H */

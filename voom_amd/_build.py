@@ -1,0 +1,62 @@
+"""Compile libvoom_hip.so for gfx950 with hipcc, in-tree.
+
+The library is built next to this file so that it travels with the source
+tree; nothing is installed.  ``build()`` always recompiles.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+LIB_NAME = "libvoom_hip.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+ARCH = "gfx950"
+
+# Packed-fp32 instructions are disabled for every device pass (the flag is
+# unknown to the host pass, which only warns).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libvoom_hip.so")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel source into one shared library and return its path."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, sources())]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,86 @@
+"""ctypes binding of libvoom_hip.so (the C ABI declared in include/voom_hip.h).
+
+There is no fallback: if the library is missing or does not load, every
+operation raises.  Return codes map to exceptions the way the reference's
+kernel wrapper does (runtime/pic_attention.py:195-213): validation failures
+raise ``ValueError`` and device/runtime failures raise ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_size_t, c_void_p
+
+from ._build import LIB_PATH
+
+VOOM_EINVAL = -1
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+_P = c_void_p
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "voom_last_error": (ctypes.c_char_p, []),
+    "voom_abi_version": (c_int, []),
+    "voom_paged_gqa_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "voom_paged_gqa_default_splits": (c_int, []),
+    "voom_paged_gqa_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_size_t,
+                                      c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                      c_float, c_int, _P]),
+    "voom_merge_attn_states": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, _P]),
+    "voom_append_kv": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int,
+                               c_int, c_int, _P]),
+    "voom_gather_kv": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,
+                               c_int, _P]),
+    "voom_byteplane_split": (c_int, [_P, _P, _P, c_size_t, _P]),
+    "voom_byteplane_merge": (c_int, [_P, _P, _P, c_size_t, _P]),
+    "voom_byteplane_split_slots": (c_int, [_P, _P, c_int, c_size_t, c_int, _P, _P, _P]),
+    "voom_byteplane_merge_slots": (c_int, [_P, _P, _P, _P, c_int, c_size_t, c_int, _P]),
+}
+
+
+class VoomLibraryError(RuntimeError):
+    """libvoom_hip.so is missing or failed to load."""
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise if it is unavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise VoomLibraryError(
+                    f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+            try:
+                handle = ctypes.CDLL(str(LIB_PATH))
+            except OSError as exc:  # pragma: no cover - depends on the box
+                raise VoomLibraryError(f"cannot load {LIB_PATH}: {exc}") from exc
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().voom_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero ABI return code."""
+    if rc == 0:
+        return
+    msg = last_error()
+    if rc < 0:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: HIP error {rc}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args), name)

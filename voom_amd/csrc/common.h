@@ -1,0 +1,82 @@
+// Shared helpers for the gfx950 kernels of libvoom_hip.so: vector types, bf16
+// conversion, wave reductions, error reporting and launch checking.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/voom_hip.h"
+
+namespace voom {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950), as bits.
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
+
+__device__ __forceinline__ float bf2f(uint16_t x) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(x) << 16);
+}
+
+// Packs two fp32 values into one dword of two bf16 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+}
+
+__device__ __forceinline__ float wave_max_across_groups(float v) {
+  // Reduces over lanes l, l^16, l^32, l^48 (the four 16-lane groups).
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_across_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Hardware base-2 exponential (v_exp_f32).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---- host side -------------------------------------------------------------
+
+// Records a printf-style message for voom_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Converts a HIP status into the ABI return convention (0 or positive code).
+int check_hip(hipError_t e, const char* what);
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+inline bool is_pow2(long long x) { return x > 0 && (x & (x - 1)) == 0; }
+inline int ilog2(long long x) {
+  int s = 0;
+  while ((1LL << s) < x) ++s;
+  return s;
+}
+
+}  // namespace voom
+
+#define VOOM_REQUIRE(cond, ...)                                   \
+  do {                                                            \
+    if (!(cond)) return ::voom::set_error(VOOM_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+#define VOOM_LAUNCH_CHECK(what) ::voom::check_hip(hipGetLastError(), what)

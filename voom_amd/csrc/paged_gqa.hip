@@ -1,0 +1,524 @@
+// Paged GQA decode attention for gfx950.
+//
+// One query token per sequence attends over its logical KV, which lives in
+// fixed-size pages scattered through a shared device pool and is addressed
+// through a per-sequence block table.  This replaces the reference's decode
+// step, which concatenates every page of the layer (runtime/kv_paged.py:164-181)
+// and then calls MLX SDPA with the GQA broadcast (runtime/layer_runner.py:
+// 179-180); the page indexing follows the reference's Metal paged kernel
+// (runtime/pic_attention.py:60-65) with V stored transposed inside a page.
+//
+// Work decomposition (balanced split-K over 32-token blocks):
+//   A "unit" is one 32-token block of one (sequence, kv-head) segment.  The
+//   units of all segments are laid end to end, (b, kvh, block) in that order,
+//   and wavefront w of W takes units [w*U/W, (w+1)*U/W).  Every wavefront
+//   therefore streams the same number of KV bytes whatever the context
+//   lengths, and it emits one partial softmax state (m, l, o) per segment
+//   piece it touches into slot (segment + w) of the workspace.  The slots of a
+//   segment are contiguous, so the reduce kernel finds them arithmetically.
+//
+// Per 32-token block a wavefront issues 2*(D/32) K loads and D/16 V loads of
+// 16 bytes per lane that land directly in MFMA operand registers:
+//   scores^T[token][head] = K[token][:] . Q^T          v_mfma_f32_16x16x32_bf16
+//   out^T[dim][head]     += V^T[dim][token] . P^T      v_mfma_f32_16x16x32_bf16
+// with the GQA heads of one KV head in the N dimension (<= 16), so each K/V
+// byte is read from HBM once for all heads that share it.  The 16 token rows of
+// the two score tiles are permuted (tile t row 4g+r holds token 8g+4t+r) so
+// that the score accumulators of lane group g are exactly the 8 consecutive
+// tokens that the P^T operand of the same lane needs: no lane shuffles are
+// required between the two products.
+#include "common.h"
+
+namespace voom {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerBlock = kThreads / kWave;
+constexpr int kMaxBatch = 1024;
+constexpr int kBlockTokens = 32;
+
+// Exclusive prefix sum of per-sequence 32-token block counts into seg[0..B].
+// Requires blockDim.x == kThreads; ends with a barrier.
+__device__ void build_block_prefix(const int32_t* __restrict__ ctx_lens, int B,
+                                   int cap_tokens, int* seg, int* wave_tot) {
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wv = t / kWave;
+  int carry = 0;
+  for (int base = 0; base < B; base += kThreads) {
+    const int i = base + t;
+    int n = 0;
+    if (i < B) {
+      int c = ctx_lens[i];
+      c = c < 0 ? 0 : (c > cap_tokens ? cap_tokens : c);
+      n = (c + kBlockTokens - 1) / kBlockTokens;
+    }
+    const int x = wave_inclusive_scan(n, lane);
+    if (lane == kWave - 1) wave_tot[wv] = x;
+    __syncthreads();
+    int pre = carry;
+    for (int k = 0; k < wv; ++k) pre += wave_tot[k];
+    if (i < B) seg[i] = pre + x - n;
+    int chunk = 0;
+    for (int k = 0; k < kWavesPerBlock; ++k) chunk += wave_tot[k];
+    __syncthreads();
+    carry += chunk;
+  }
+  if (t == 0) seg[B] = carry;
+  __syncthreads();
+}
+
+template <int D>
+struct BlockRegs {
+  u32x4 k[2][D / 32];  // two 16-token score tiles x (D/32) k-steps
+  u32x4 v[D / 16];     // D/16 dimension tiles of V^T, 8 tokens per lane
+};
+
+struct SegmentArgs {
+  const uint16_t* __restrict__ k_pool;
+  const uint16_t* __restrict__ v_pool;
+  const int32_t* __restrict__ table_row;
+  int n_pages;   // pages addressable through table_row
+  int kvh;
+  int nkv;
+  int pt_shift;  // log2(page_tokens)
+  int num_slots;
+  int ctx;       // tokens of this sequence (clamped to table capacity)
+};
+
+template <int D>
+__device__ __forceinline__ void load_block(BlockRegs<D>& r, const SegmentArgs& a, int bi,
+                                           int& tab_base, int& tab, int lane) {
+  const int sub_shift = a.pt_shift - 5;
+  const int page = bi >> sub_shift;
+  const int sub = bi & ((1 << sub_shift) - 1);
+  if (page >= tab_base + kWave) {
+    tab_base = page;
+    const int p = tab_base + lane;
+    tab = p < a.n_pages ? a.table_row[p] : 0;
+  }
+  int slot = __builtin_amdgcn_readlane(tab, page - tab_base);
+  if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
+  const size_t head_page = static_cast<size_t>(slot) * a.nkv + a.kvh;
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const uint16_t* kb = a.k_pool + ((head_page << a.pt_shift) + sub * kBlockTokens) * D;
+  const int krow = 8 * (i16 >> 2) + (i16 & 3);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) {
+      r.k[t][s] = *reinterpret_cast<const u32x4*>(kb + (krow + 4 * t) * D + 32 * s + 8 * g);
+    }
+  }
+  const uint16_t* vb = a.v_pool + ((head_page * D) << a.pt_shift) + sub * kBlockTokens;
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) {
+    r.v[n] = *reinterpret_cast<const u32x4*>(vb + ((16 * n + i16) << a.pt_shift) + 8 * g);
+  }
+}
+
+template <int D>
+struct SoftmaxState {
+  f32x4 acc[D / 16];
+  float m;
+  float l;
+};
+
+template <int D>
+__device__ __forceinline__ void compute_block(const BlockRegs<D>& r, const u32x4* qop,
+                                              SoftmaxState<D>& st, int valid,
+                                              float scale_log2e, int lane) {
+  const int g = lane >> 4;
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    const bf16x8 qb = __builtin_bit_cast(bf16x8, qop[s]);
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[0][s]), qb,
+                                                 s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[1][s]), qb,
+                                                 s1, 0, 0, 0);
+  }
+  // Lane (head j, group g) now holds tokens 8g+e, e = 0..7, of this block.
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = s0[e] * scale_log2e;
+    x[4 + e] = s1[e] * scale_log2e;
+  }
+  u32x4 vv[D / 16];
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) vv[n] = r.v[n];
+  if (valid < kBlockTokens) {
+    // Tail block: tokens past the context are garbage (possibly NaN) in the
+    // pool, so they are removed by selection, never by arithmetic.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (8 * g + e >= valid) x[e] = -INFINITY;
+    }
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const bool lo_ok = 8 * g + 2 * w < valid;
+        const bool hi_ok = 8 * g + 2 * w + 1 < valid;
+        const unsigned mask = (lo_ok ? 0x0000ffffu : 0u) | (hi_ok ? 0xffff0000u : 0u);
+        vv[n][w] &= mask;
+      }
+    }
+  }
+  float mb = x[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mb = fmaxf(mb, x[e]);
+  mb = wave_max_across_groups(mb);
+  const float m_new = fmaxf(st.m, mb);
+  const float alpha = fast_exp2(st.m - m_new);
+  float p[8];
+  float psum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = fast_exp2(x[e] - m_new);
+  u32x4 pk;
+  pk[0] = pack_bf16x2(p[0], p[1]);
+  pk[1] = pack_bf16x2(p[2], p[3]);
+  pk[2] = pack_bf16x2(p[4], p[5]);
+  pk[3] = pack_bf16x2(p[6], p[7]);
+  // The normaliser sums the same bf16-rounded weights the MFMA consumes, so
+  // the output is an exact convex combination of V rows up to fp32 rounding.
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    psum += __builtin_bit_cast(float, pk[w] << 16) + __builtin_bit_cast(float, pk[w] & 0xffff0000u);
+  }
+  st.l = st.l * alpha + psum;
+  st.m = m_new;
+  const bf16x8 pb = __builtin_bit_cast(bf16x8, pk);
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) {
+    st.acc[n] *= alpha;
+    st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv[n]), pb,
+                                                        st.acc[n], 0, 0, 0);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void gqa_decode_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
+    float* __restrict__ part_ml, int B, int NKV, int G, int max_pages, int pt_shift,
+    int num_slots, float scale_log2e, int W) {
+  __shared__ int seg[kMaxBatch + 1];
+  __shared__ int wave_tot[kWavesPerBlock];
+  const int cap_tokens = max_pages << pt_shift;
+  build_block_prefix(ctx_lens, B, cap_tokens, seg, wave_tot);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  const long long U = static_cast<long long>(seg[B]) * NKV;
+  // Never more wavefronts than units: every active wavefront then owns at
+  // least one unit, which the reduce kernel relies on.
+  const int We = static_cast<int>(U < W ? U : W);
+  if (w >= We) return;
+  long long u0 = static_cast<long long>(w) * U / We;
+  const long long u1 = static_cast<long long>(w + 1) * U / We;
+
+  // Sequence holding unit u0: the largest b with NKV*seg[b] <= u0.
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (static_cast<long long>(seg[mid]) * NKV <= u0) lo = mid; else hi = mid - 1;
+  }
+  int b = lo;
+  int nb = seg[b + 1] - seg[b];
+  int kvh = static_cast<int>((u0 - static_cast<long long>(seg[b]) * NKV) / nb);
+  long long S = static_cast<long long>(seg[b]) * NKV + static_cast<long long>(kvh) * nb;
+
+  const int NQ = NKV * G;
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const bool head_ok = i16 < G;
+
+  while (true) {
+    const long long send = S + nb;
+    const int blo = static_cast<int>(u0 - S);
+    const int bhi = static_cast<int>((u1 < send ? u1 : send) - S);
+
+    SegmentArgs a;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.table_row = block_table + static_cast<size_t>(b) * max_pages;
+    a.n_pages = max_pages;
+    a.kvh = kvh;
+    a.nkv = NKV;
+    a.pt_shift = pt_shift;
+    a.num_slots = num_slots;
+    int ctx = ctx_lens[b];
+    a.ctx = ctx > cap_tokens ? cap_tokens : ctx;
+
+    // Q^T operand: lane (head j, group g) holds q[j][32s + 8g .. +8].
+    u32x4 qop[D / 32];
+    const uint16_t* qh = q + (static_cast<size_t>(b) * NQ + kvh * G + (head_ok ? i16 : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qop[s] = head_ok ? *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g) : z;
+    }
+
+    SoftmaxState<D> st;
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = -INFINITY;
+    st.l = 0.f;
+
+    int tab_base = -(1 << 30);
+    int tab = 0;
+    BlockRegs<D> r0, r1;
+    int bi = blo;
+    load_block<D>(r0, a, bi, tab_base, tab, lane);
+    while (true) {
+      // The prefetch index is clamped so both register sets are always loaded
+      // unconditionally; the waitcnt for the block being consumed then never
+      // depends on a branch.
+      load_block<D>(r1, a, bi + 1 < bhi ? bi + 1 : bhi - 1, tab_base, tab, lane);
+      compute_block<D>(r0, qop, st, a.ctx - bi * kBlockTokens, scale_log2e, lane);
+      if (++bi >= bhi) break;
+      load_block<D>(r0, a, bi + 1 < bhi ? bi + 1 : bhi - 1, tab_base, tab, lane);
+      compute_block<D>(r1, qop, st, a.ctx - bi * kBlockTokens, scale_log2e, lane);
+      if (++bi >= bhi) break;
+    }
+
+    const float l_tot = wave_sum_across_groups(st.l);
+    const long long pidx = static_cast<long long>(b) * NKV + kvh + w;
+    if (head_ok) {
+      float* po = part_o + (pidx * G + i16) * D;
+#pragma unroll
+      for (int n = 0; n < D / 16; ++n) {
+        *reinterpret_cast<f32x4*>(po + 16 * n + 4 * g) = st.acc[n];
+      }
+      if (g == 0) {
+        part_ml[(pidx * G + i16) * 2 + 0] = st.m;
+        part_ml[(pidx * G + i16) * 2 + 1] = l_tot;
+      }
+    }
+
+    u0 = u1 < send ? u1 : send;
+    if (u0 >= u1) break;
+    S = send;
+    if (++kvh == NKV) {
+      kvh = 0;
+      do {
+        ++b;
+      } while (b < B - 1 && seg[b + 1] == seg[b]);
+      nb = seg[b + 1] - seg[b];
+    }
+  }
+}
+
+// Wavefront of the split holding unit u (the last w with w*U/W <= u).
+__device__ __forceinline__ long long wave_of_unit(long long u, long long U, int W) {
+  return ((u + 1) * W - 1) / U;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void gqa_reduce_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    const int32_t* __restrict__ ctx_lens, uint16_t* __restrict__ out,
+    float* __restrict__ lse_out, int B, int NKV, int G, int max_pages, int pt_shift, int W) {
+  __shared__ int seg[kMaxBatch + 1];
+  __shared__ int wave_tot[kWavesPerBlock];
+  build_block_prefix(ctx_lens, B, max_pages << pt_shift, seg, wave_tot);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int s = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  if (s >= B * NKV) return;
+  const int b = s / NKV;
+  const int kvh = s - b * NKV;
+  const int NQ = NKV * G;
+  const int nb = seg[b + 1] - seg[b];
+  const int n_el = G * D;  // multiple of 64 for D in {64, 128}
+  uint16_t* ob = out + (static_cast<size_t>(b) * NQ + kvh * G) * D;
+  if (nb == 0) {
+    for (int e = lane; e < n_el; e += kWave) ob[e] = 0;
+    if (lse_out != nullptr && lane < G) lse_out[b * NQ + kvh * G + lane] = -INFINITY;
+    return;
+  }
+  const long long U = static_cast<long long>(seg[B]) * NKV;
+  const int We = static_cast<int>(U < W ? U : W);
+  const long long us = static_cast<long long>(seg[b]) * NKV + static_cast<long long>(kvh) * nb;
+  const long long w_lo = wave_of_unit(us, U, We);
+  const long long w_hi = wave_of_unit(us + nb - 1, U, We);
+
+  constexpr int kMaxPerLane = 16 * D / kWave;
+  const int per_lane = n_el / kWave;
+  float M[kMaxPerLane], L[kMaxPerLane], A[kMaxPerLane];
+#pragma unroll
+  for (int k = 0; k < kMaxPerLane; ++k) {
+    M[k] = -INFINITY;
+    L[k] = 0.f;
+    A[k] = 0.f;
+  }
+  for (long long w = w_lo; w <= w_hi; ++w) {
+    const long long p = s + w;
+    const float* po = part_o + p * n_el;
+    const float* pml = part_ml + p * G * 2;
+#pragma unroll
+    for (int k = 0; k < kMaxPerLane; ++k) {
+      if (k < per_lane) {
+        const int e = lane + kWave * k;
+        const int head = e / D;
+        const float m = pml[head * 2];
+        const float l = pml[head * 2 + 1];
+        const float mn = fmaxf(M[k], m);
+        const float ca = fast_exp2(M[k] - mn);
+        const float cb = fast_exp2(m - mn);
+        L[k] = L[k] * ca + l * cb;
+        A[k] = A[k] * ca + po[e] * cb;
+        M[k] = mn;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxPerLane; ++k) {
+    if (k < per_lane) {
+      const int e = lane + kWave * k;
+      ob[e] = f2bf(A[k] / L[k]);
+      if (lse_out != nullptr && (e % D) == 0) {
+        lse_out[b * NQ + kvh * G + e / D] = (M[k] + __log2f(L[k])) * 0.6931471805599453f;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void merge_states_kernel(
+    const uint16_t* __restrict__ oa, const float* __restrict__ la,
+    const uint16_t* __restrict__ ob, const float* __restrict__ lb, uint16_t* __restrict__ out,
+    float* __restrict__ lse_out, int rows, int D) {
+  const long long idx = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= static_cast<long long>(rows) * D) return;
+  const int row = static_cast<int>(idx / D);
+  const float a = la[row];
+  const float c = lb[row];
+  const float m = fmaxf(a, c);
+  float res;
+  float lse;
+  if (m == -INFINITY) {
+    res = 0.f;
+    lse = -INFINITY;
+  } else {
+    const float wa = __expf(a - m);
+    const float wb = __expf(c - m);
+    res = (bf2f(oa[idx]) * wa + bf2f(ob[idx]) * wb) / (wa + wb);
+    lse = m + __logf(wa + wb);
+  }
+  out[idx] = f2bf(res);
+  if (lse_out != nullptr && idx % D == 0) lse_out[row] = lse;
+}
+
+size_t part_slots(int batch, int num_kv_heads, int num_splits) {
+  return static_cast<size_t>(batch) * num_kv_heads + static_cast<size_t>(num_splits);
+}
+
+}  // namespace
+}  // namespace voom
+
+using namespace voom;
+
+extern "C" int voom_paged_gqa_default_splits(void) { return device_cu_count() * 8; }
+
+extern "C" size_t voom_paged_gqa_workspace_bytes(int batch, int num_q_heads, int num_kv_heads,
+                                                 int head_dim, int num_splits) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
+  if (num_splits <= 0) num_splits = voom_paged_gqa_default_splits();
+  const size_t G = static_cast<size_t>(num_q_heads / num_kv_heads);
+  const size_t slots = part_slots(batch, num_kv_heads, num_splits);
+  const size_t o_bytes = slots * G * head_dim * sizeof(float);
+  const size_t ml_bytes = slots * G * 2 * sizeof(float);
+  return ((o_bytes + 255) & ~size_t(255)) + ml_bytes;
+}
+
+extern "C" int voom_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
+                                     const int32_t* block_table, const int32_t* ctx_lens,
+                                     void* out, float* lse_out, void* workspace,
+                                     size_t ws_bytes, int batch, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int page_tokens,
+                                     int max_pages, int num_slots, float scale,
+                                     int num_splits, hipStream_t stream) {
+  VOOM_REQUIRE(q && k_pool && v_pool && block_table && ctx_lens && out && workspace,
+               "paged_gqa_decode: null pointer argument");
+  VOOM_REQUIRE(batch > 0 && batch <= kMaxBatch, "paged_gqa_decode: batch %d not in [1, %d]",
+               batch, kMaxBatch);
+  VOOM_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0,
+               "paged_gqa_decode: num_q_heads %d not a multiple of num_kv_heads %d",
+               num_q_heads, num_kv_heads);
+  const int G = num_q_heads / num_kv_heads;
+  VOOM_REQUIRE(G <= 16, "paged_gqa_decode: GQA group %d exceeds 16", G);
+  VOOM_REQUIRE(head_dim == 64 || head_dim == 128,
+               "paged_gqa_decode: head_dim %d unsupported (64 or 128)", head_dim);
+  VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens >= 32 && page_tokens <= 4096,
+               "paged_gqa_decode: page_tokens %d must be a power of two in [32, 4096]",
+               page_tokens);
+  VOOM_REQUIRE(max_pages > 0 && num_slots > 0, "paged_gqa_decode: empty table or pool");
+  VOOM_REQUIRE(static_cast<long long>(max_pages) * page_tokens < (1LL << 30),
+               "paged_gqa_decode: table capacity too large");
+  if (num_splits <= 0) num_splits = voom_paged_gqa_default_splits();
+  VOOM_REQUIRE(num_splits <= (1 << 22), "paged_gqa_decode: num_splits %d too large",
+               num_splits);
+  const size_t need = voom_paged_gqa_workspace_bytes(batch, num_q_heads, num_kv_heads,
+                                                      head_dim, num_splits);
+  VOOM_REQUIRE(ws_bytes >= need, "paged_gqa_decode: workspace %zu bytes < required %zu",
+               ws_bytes, need);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(k_pool) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(v_pool) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "paged_gqa_decode: q, pools and workspace must be 16-byte aligned");
+
+  const size_t slots = part_slots(batch, num_kv_heads, num_splits);
+  float* part_o = static_cast<float*>(workspace);
+  const size_t o_bytes = slots * G * head_dim * sizeof(float);
+  float* part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                            ((o_bytes + 255) & ~size_t(255)));
+  const int pt_shift = ilog2(page_tokens);
+  const float scale_log2e = scale * 1.4426950408889634f;
+  const dim3 grid_main((num_splits + kWavesPerBlock - 1) / kWavesPerBlock);
+  const dim3 grid_red((batch * num_kv_heads + kWavesPerBlock - 1) / kWavesPerBlock);
+  const auto* qq = static_cast<const uint16_t*>(q);
+  const auto* kp = static_cast<const uint16_t*>(k_pool);
+  const auto* vp = static_cast<const uint16_t*>(v_pool);
+  auto* oo = static_cast<uint16_t*>(out);
+  if (head_dim == 128) {
+    hipLaunchKernelGGL(gqa_decode_kernel<128>, grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
+                       block_table, ctx_lens, part_o, part_ml, batch, num_kv_heads, G,
+                       max_pages, pt_shift, num_slots, scale_log2e, num_splits);
+    int rc = VOOM_LAUNCH_CHECK("paged_gqa_decode: main kernel launch");
+    if (rc) return rc;
+    hipLaunchKernelGGL(gqa_reduce_kernel<128>, grid_red, dim3(kThreads), 0, stream, part_o,
+                       part_ml, ctx_lens, oo, lse_out, batch, num_kv_heads, G, max_pages,
+                       pt_shift, num_splits);
+  } else {
+    hipLaunchKernelGGL(gqa_decode_kernel<64>, grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
+                       block_table, ctx_lens, part_o, part_ml, batch, num_kv_heads, G,
+                       max_pages, pt_shift, num_slots, scale_log2e, num_splits);
+    int rc = VOOM_LAUNCH_CHECK("paged_gqa_decode: main kernel launch");
+    if (rc) return rc;
+    hipLaunchKernelGGL(gqa_reduce_kernel<64>, grid_red, dim3(kThreads), 0, stream, part_o,
+                       part_ml, ctx_lens, oo, lse_out, batch, num_kv_heads, G, max_pages,
+                       pt_shift, num_splits);
+  }
+  return VOOM_LAUNCH_CHECK("paged_gqa_decode: reduce kernel launch");
+}
+
+extern "C" int voom_merge_attn_states(const void* o_a, const float* lse_a, const void* o_b,
+                                      const float* lse_b, void* out, float* lse_out, int rows,
+                                      int head_dim, hipStream_t stream) {
+  VOOM_REQUIRE(o_a && lse_a && o_b && lse_b && out, "merge_attn_states: null pointer");
+  VOOM_REQUIRE(rows >= 0 && head_dim > 0, "merge_attn_states: bad shape");
+  if (rows == 0) return VOOM_OK;
+  const long long n = static_cast<long long>(rows) * head_dim;
+  const dim3 grid(static_cast<unsigned>((n + kThreads - 1) / kThreads));
+  hipLaunchKernelGGL(merge_states_kernel, grid, dim3(kThreads), 0, stream,
+                     static_cast<const uint16_t*>(o_a), lse_a,
+                     static_cast<const uint16_t*>(o_b), lse_b, static_cast<uint16_t*>(out),
+                     lse_out, rows, head_dim);
+  return VOOM_LAUNCH_CHECK("merge_attn_states: launch");
+}

@@ -1,0 +1,241 @@
+"""Torch-facing wrappers over the libvoom_hip.so C ABI.
+
+Every function validates shapes/dtypes/devices on the host, passes raw device
+pointers plus the current HIP stream, and raises on any non-zero return.  There
+is no CPU path: tensors must live on a ROCm device and the library must be
+built.
+
+Pool layouts (per layer):
+  k_pool  [slots, num_kv_heads, page_tokens, head_dim]  bf16, token-major
+  v_pool  [slots, num_kv_heads, head_dim, page_tokens]  bf16, transposed pages
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _stream(stream: torch.cuda.Stream | None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        _require(t.is_cuda, "voom_amd ops need ROCm device tensors (no CPU fallback exists)")
+        _require(t.is_contiguous(), "voom_amd ops need contiguous tensors")
+        if dev is None:
+            dev = t.device
+        _require(t.device == dev, "all tensors must be on the same device")
+    return dev
+
+
+def workspace(device: torch.device, nbytes: int, tag: int = 0) -> torch.Tensor:
+    """Per-device cached uint8 scratch tensor of at least ``nbytes`` bytes."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), tag)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def default_splits() -> int:
+    return int(_lib.lib().voom_paged_gqa_default_splits())
+
+
+def gqa_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                        num_splits: int) -> int:
+    return int(_lib.lib().voom_paged_gqa_workspace_bytes(batch, num_q_heads, num_kv_heads,
+                                                        head_dim, num_splits))
+
+
+def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                     block_table: torch.Tensor, ctx_lens: torch.Tensor, *,
+                     scale: float | None = None, out: torch.Tensor | None = None,
+                     return_lse: bool = False, num_splits: int | None = None,
+                     ws: torch.Tensor | None = None,
+                     stream: torch.cuda.Stream | None = None):
+    """Decode attention of one query token per sequence over paged K/V.
+
+    q [B, NQ, D] (or [B, NQ, 1, D]) bf16; pools as in the module docstring;
+    block_table [B, max_pages] int32; ctx_lens [B] int32.  Returns out with q's
+    shape (and the fp32 natural-log LSE [B, NQ] when ``return_lse``).
+    Mirrors softmax(q.K^T*scale).V over the concatenated pages
+    (runtime/kv_paged.py:164-181, runtime/layer_runner.py:179-180).
+    """
+    q_shape = q.shape
+    if q.dim() == 4:
+        _require(q.shape[2] == 1, "paged_gqa_decode handles one query token per sequence")
+        q = q.reshape(q.shape[0], q.shape[1], q.shape[3])
+    _require(q.dim() == 3, "q must be [B, NQ, D]")
+    dev = _require_device(q, k_pool, v_pool, block_table, ctx_lens, out)
+    B, NQ, D = q.shape
+    _require(k_pool.dim() == 4 and v_pool.dim() == 4, "pools must be 4-D")
+    slots, NKV, PT, Dk = k_pool.shape
+    _require(Dk == D, f"k_pool head_dim {Dk} != q head_dim {D}")
+    _require(tuple(v_pool.shape) == (slots, NKV, D, PT),
+             f"v_pool must be [slots, NKV, D, PT] = {(slots, NKV, D, PT)}, got {tuple(v_pool.shape)}")
+    _require(q.dtype == k_pool.dtype == v_pool.dtype == torch.bfloat16,
+             "q and pools must be bfloat16")
+    _require(block_table.dtype == torch.int32 and ctx_lens.dtype == torch.int32,
+             "block_table and ctx_lens must be int32")
+    _require(block_table.dim() == 2 and block_table.shape[0] == B,
+             "block_table must be [B, max_pages]")
+    _require(tuple(ctx_lens.shape) == (B,), "ctx_lens must be [B]")
+    _require(NQ % NKV == 0, "num_q_heads must be a multiple of num_kv_heads")
+    max_pages = block_table.shape[1]
+    if scale is None:
+        scale = D ** -0.5
+    if num_splits is None:
+        # Never more wavefronts than 32-token units can exist.
+        bound = max(1, B * NKV * max_pages * max(1, PT // 32))
+        num_splits = min(default_splits(), bound)
+    need = gqa_workspace_bytes(B, NQ, NKV, D, num_splits)
+    if ws is None:
+        ws = workspace(dev, need, tag=1)
+    _require(ws.numel() * ws.element_size() >= need, "workspace too small")
+    if out is None:
+        out = torch.empty((B, NQ, D), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, NQ), dtype=torch.float32, device=dev) if return_lse else None
+    _lib.call("voom_paged_gqa_decode", _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table),
+              _ptr(ctx_lens), _ptr(out), _ptr(lse), _ptr(ws), need, B, NQ, NKV, D, PT,
+              max_pages, slots, float(scale), int(num_splits), _stream(stream))
+    out = out.reshape(q_shape)
+    return (out, lse) if return_lse else out
+
+
+def merge_attn_states(o_a: torch.Tensor, lse_a: torch.Tensor, o_b: torch.Tensor,
+                      lse_b: torch.Tensor, *, stream: torch.cuda.Stream | None = None):
+    """Combine two attention results over disjoint key sets (LSE merge)."""
+    dev = _require_device(o_a, lse_a, o_b, lse_b)
+    _require(o_a.shape == o_b.shape and o_a.dtype == o_b.dtype == torch.bfloat16,
+             "o_a/o_b must be equal-shaped bf16")
+    D = o_a.shape[-1]
+    rows = o_a.numel() // D
+    _require(lse_a.numel() == rows == lse_b.numel(), "lse must have one entry per row")
+    _require(lse_a.dtype == lse_b.dtype == torch.float32, "lse must be float32")
+    out = torch.empty_like(o_a)
+    lse = torch.empty(lse_a.shape, dtype=torch.float32, device=dev)
+    _lib.call("voom_merge_attn_states", _ptr(o_a), _ptr(lse_a), _ptr(o_b), _ptr(lse_b),
+              _ptr(out), _ptr(lse), rows, D, _stream(stream))
+    return out, lse
+
+
+def append_kv(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
+              v_pool: torch.Tensor, block_table: torch.Tensor, positions: torch.Tensor, *,
+              stream: torch.cuda.Stream | None = None) -> None:
+    """Write k_new/v_new [B, NKV, L, D] at logical positions positions[b] + t."""
+    _require_device(k_new, v_new, k_pool, v_pool, block_table, positions)
+    B, NKV, L, D = k_new.shape
+    slots, NKVp, PT, Dp = k_pool.shape
+    _require(v_new.shape == k_new.shape, "k_new and v_new shapes differ")
+    _require(NKVp == NKV and Dp == D, "pool geometry does not match new K/V")
+    _require(tuple(v_pool.shape) == (slots, NKV, D, PT), "v_pool must be [slots, NKV, D, PT]")
+    _require(k_new.dtype == v_new.dtype == k_pool.dtype == v_pool.dtype == torch.bfloat16,
+             "K/V and pools must be bfloat16")
+    _require(block_table.dtype == torch.int32 and positions.dtype == torch.int32,
+             "block_table and positions must be int32")
+    _require(block_table.shape[0] == B and tuple(positions.shape) == (B,),
+             "block_table/positions batch mismatch")
+    _lib.call("voom_append_kv", _ptr(k_new), _ptr(v_new), _ptr(k_pool), _ptr(v_pool),
+              _ptr(block_table), _ptr(positions), B, NKV, L, D, PT, block_table.shape[1],
+              slots, _stream(stream))
+
+
+def gather_kv(k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
+              seq_len: int, *, stream: torch.cuda.Stream | None = None):
+    """Materialise logical K/V [B, NKV, seq_len, D] from the pools."""
+    dev = _require_device(k_pool, v_pool, block_table)
+    slots, NKV, PT, D = k_pool.shape
+    B = block_table.shape[0]
+    _require(tuple(v_pool.shape) == (slots, NKV, D, PT), "v_pool must be [slots, NKV, D, PT]")
+    _require(block_table.dtype == torch.int32, "block_table must be int32")
+    k = torch.empty((B, NKV, seq_len, D), dtype=k_pool.dtype, device=dev)
+    v = torch.empty_like(k)
+    _lib.call("voom_gather_kv", _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(k), _ptr(v),
+              B, NKV, seq_len, D, PT, block_table.shape[1], slots, _stream(stream))
+    return k, v
+
+
+def _u16_view(t: torch.Tensor) -> torch.Tensor:
+    _require(t.element_size() == 2, "byte-plane codec needs a 16-bit dtype")
+    return t
+
+
+def byteplane_split(src: torch.Tensor, lo: torch.Tensor | None = None,
+                    hi: torch.Tensor | None = None, *,
+                    stream: torch.cuda.Stream | None = None):
+    """Split 16-bit elements into (lo, hi) uint8 planes of src.numel() bytes each."""
+    _u16_view(src)
+    dev = _require_device(src, lo, hi)
+    n = src.numel()
+    lo = torch.empty(n, dtype=torch.uint8, device=dev) if lo is None else lo
+    hi = torch.empty(n, dtype=torch.uint8, device=dev) if hi is None else hi
+    _require(lo.numel() >= n and hi.numel() >= n and lo.dtype == hi.dtype == torch.uint8,
+             "planes must be uint8 with >= numel bytes")
+    _lib.call("voom_byteplane_split", _ptr(src), _ptr(lo), _ptr(hi), n, _stream(stream))
+    return lo, hi
+
+
+def byteplane_merge(lo: torch.Tensor, hi: torch.Tensor, out: torch.Tensor, *,
+                    stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Interleave planes back into the 16-bit tensor ``out`` (bit-exact)."""
+    _u16_view(out)
+    _require_device(lo, hi, out)
+    n = out.numel()
+    _require(lo.numel() >= n and hi.numel() >= n and lo.dtype == hi.dtype == torch.uint8,
+             "planes must be uint8 with >= numel bytes")
+    _lib.call("voom_byteplane_merge", _ptr(lo), _ptr(hi), _ptr(out), n, _stream(stream))
+    return out
+
+
+def byteplane_split_slots(pool: torch.Tensor, slots: torch.Tensor, lo: torch.Tensor,
+                          hi: torch.Tensor, *, stream: torch.cuda.Stream | None = None) -> None:
+    """Gather pool[slots[i]] and split it into plane chunk i (slot_bytes/2 bytes each)."""
+    _u16_view(pool)
+    _require_device(pool, slots, lo, hi)
+    _require(slots.dtype == torch.int32 and slots.dim() == 1, "slots must be 1-D int32")
+    num_slots = pool.shape[0]
+    slot_bytes = pool[0].numel() * 2
+    n = slots.numel()
+    _require(lo.numel() >= n * slot_bytes // 2 and hi.numel() >= n * slot_bytes // 2,
+             "plane buffers too small")
+    _lib.call("voom_byteplane_split_slots", _ptr(pool), _ptr(slots), n, slot_bytes, num_slots,
+              _ptr(lo), _ptr(hi), _stream(stream))
+
+
+def byteplane_merge_slots(lo: torch.Tensor, hi: torch.Tensor, pool: torch.Tensor,
+                          slots: torch.Tensor, *, stream: torch.cuda.Stream | None = None) -> None:
+    """Merge plane chunk i back into pool[slots[i]] (scatter, bit-exact)."""
+    _u16_view(pool)
+    _require_device(pool, slots, lo, hi)
+    _require(slots.dtype == torch.int32 and slots.dim() == 1, "slots must be 1-D int32")
+    num_slots = pool.shape[0]
+    slot_bytes = pool[0].numel() * 2
+    n = slots.numel()
+    _require(lo.numel() >= n * slot_bytes // 2 and hi.numel() >= n * slot_bytes // 2,
+             "plane buffers too small")
+    _lib.call("voom_byteplane_merge_slots", _ptr(lo), _ptr(hi), _ptr(pool), _ptr(slots), n,
+              slot_bytes, num_slots, _stream(stream))
+
+
+def slot_codec_supported(pool: torch.Tensor) -> bool:
+    """True when one pool slot is a whole number of 64-byte lines (slot kernels)."""
+    return (pool[0].numel() * 2) % 64 == 0

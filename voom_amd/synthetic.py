@@ -1,0 +1,124 @@
+"""Seeded synthetic inputs for the paged-KV workloads (bench, smoke and tests).
+
+The shapes and seeds follow the BASELINE configurations of this build:
+  gqa_decode_inputs   config 2 -- B=16, 32 q / 8 kv heads, D=128, contexts
+                      U[1024, 32768] (seed 2), K,V ~ N(0,1) (seed 3) with
+                      RoPE(theta=5e5) applied to K at positions U[0, 131072)
+                      (seed 4), 64-token pages at a seeded permutation of pool
+                      slots (seed 5), scale D^-0.5.
+Random tensors are generated on the target device with torch generators; the
+context lengths, positions and slot permutation come from numpy PCG64 so the
+host can rebuild them exactly.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+@dataclass
+class PagedGQAInputs:
+    q: torch.Tensor            # [B, NQ, D] bf16
+    k_pool: torch.Tensor       # [slots, NKV, PT, D] bf16
+    v_pool: torch.Tensor       # [slots, NKV, D, PT] bf16 (transposed pages)
+    block_table: torch.Tensor  # [B, max_pages] int32
+    ctx_lens: torch.Tensor     # [B] int32
+    ctx_host: np.ndarray
+    table_host: np.ndarray
+    scale: float
+    page_tokens: int
+
+    @property
+    def kv_bytes(self) -> int:
+        B, NQ, D = self.q.shape
+        NKV = self.k_pool.shape[1]
+        return int(self.ctx_host.sum()) * NKV * D * 2 * 2
+
+    def algorithmic_bytes(self) -> int:
+        """K/V of every live token + q + out + table entries + lengths."""
+        B, NQ, D = self.q.shape
+        pages = int(np.sum(-(-self.ctx_host // self.page_tokens)))
+        return self.kv_bytes + 2 * B * NQ * D * 2 + pages * 4 + B * 4
+
+    def flops(self) -> int:
+        B, NQ, D = self.q.shape
+        return 4 * NQ * D * int(self.ctx_host.sum())
+
+
+def rope_tables(positions: torch.Tensor, head_dim: int, theta: float):
+    """fp32 cos/sin [n, D/2]: angle = pos / theta^(i/half) (pic_attention.py:150-167)."""
+    half = head_dim // 2
+    inv = theta ** (torch.arange(half, dtype=torch.float32, device=positions.device) / half)
+    ang = positions.to(torch.float32)[:, None] / inv[None, :]
+    return torch.cos(ang), torch.sin(ang)
+
+
+def apply_rope_neox(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE in fp32, x [..., n, D] with tables [n, D/2] (pic_attention.py:170-181)."""
+    half = x.shape[-1] // 2
+    a, b = x[..., :half].float(), x[..., half:].float()
+    return torch.cat((a * cos - b * sin, b * cos + a * sin), dim=-1)
+
+
+def gqa_decode_inputs(*, batch: int = 16, num_q_heads: int = 32, num_kv_heads: int = 8,
+                      head_dim: int = 128, page_tokens: int = 64, ctx_min: int = 1024,
+                      ctx_max: int = 32768, ctx_lens=None, rope_theta: float = 5e5,
+                      slack_pages: int = 0, device="cuda", seed_base: int = 0,
+                      k_scale_outliers: bool = False) -> PagedGQAInputs:
+    dev = torch.device(device)
+    if ctx_lens is None:
+        ctx = np.random.default_rng(2 + seed_base).integers(ctx_min, ctx_max + 1, size=batch)
+    else:
+        ctx = np.asarray(ctx_lens, dtype=np.int64)
+        batch = len(ctx)
+    ctx = ctx.astype(np.int64)
+    pages_per = -(-ctx // page_tokens)
+    total_pages = int(pages_per.sum())
+    slots = max(1, total_pages + slack_pages)
+    max_pages = max(1, int(pages_per.max()) if batch else 1)
+    perm = np.random.default_rng(5 + seed_base).permutation(slots)
+    table = np.zeros((batch, max_pages), dtype=np.int32)
+    cursor = 0
+    for b in range(batch):
+        n = int(pages_per[b])
+        table[b, :n] = perm[cursor:cursor + n]
+        cursor += n
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3 + seed_base)
+    NKV, D, PT = num_kv_heads, head_dim, page_tokens
+    k_pool = torch.empty((slots, NKV, PT, D), dtype=torch.bfloat16, device=dev)
+    v_pool = torch.empty((slots, NKV, D, PT), dtype=torch.bfloat16, device=dev)
+    pos_rng = np.random.default_rng(4 + seed_base)
+    # Fill page by page in slot order, rotating K at random positions.
+    chunk = 256
+    for s0 in range(0, slots, chunk):
+        s1 = min(slots, s0 + chunk)
+        n = s1 - s0
+        kr = torch.randn((n, NKV, PT, D), generator=gen, device=dev, dtype=torch.float32)
+        vr = torch.randn((n, NKV, PT, D), generator=gen, device=dev, dtype=torch.float32)
+        pos = torch.from_numpy(pos_rng.integers(0, 131072, size=n * PT)).to(dev)
+        cos, sin = rope_tables(pos, D, rope_theta)
+        cos = cos.view(n, 1, PT, D // 2)
+        sin = sin.view(n, 1, PT, D // 2)
+        kr = apply_rope_neox(kr, cos, sin)
+        k_pool[s0:s1] = kr.to(torch.bfloat16)
+        v_pool[s0:s1] = vr.to(torch.bfloat16).transpose(2, 3)
+    q = torch.randn((batch, num_q_heads, D), generator=gen, device=dev,
+                    dtype=torch.float32).to(torch.bfloat16)
+    return PagedGQAInputs(
+        q=q, k_pool=k_pool, v_pool=v_pool,
+        block_table=torch.from_numpy(table).to(dev),
+        ctx_lens=torch.from_numpy(ctx.astype(np.int32)).to(dev),
+        ctx_host=ctx, table_host=table, scale=D ** -0.5, page_tokens=PT)
+
+
+def to_reference_layout(inp: PagedGQAInputs):
+    """Host fp32 copies in the reference page layout [P, NKV, PT, D] for K and V."""
+    k = inp.k_pool.float().cpu().numpy()
+    v = inp.v_pool.transpose(2, 3).float().cpu().numpy()
+    q = inp.q.float().cpu().numpy()
+    return q, k, v
