@@ -135,12 +135,33 @@ def bench_gqa(steps: int, warmup: int, cpu_sample: bool) -> dict:
     return res
 
 
+def copy_calibration(nbytes: int = 1 << 30, reps: int = 5) -> None:
+    """A plain device-to-device copy of known size: the scale for PMC byte counters."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    log(f"copy calibration: {nbytes} B read + {nbytes} B written per copy, {ms * 1e3:.1f} us, "
+        f"{2 * nbytes / ms / 1e6:.0f} GB/s (read+write)")
+    del src, dst
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; multi-GPU sharding is design-only "
@@ -152,6 +173,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        copy_calibration()
     gqa = bench_gqa(args.steps, args.warmup, cpu_sample=not args.no_cpu)
     line = {
         "metric": "paged decode-attn HBM GB/s (% peak) + spill/reload GB/s, Llama-3-8B shape",
