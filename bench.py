@@ -36,6 +36,21 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def profiled_traffic(name: str) -> int | None:
+    """HBM bytes per launch recorded by rocprofv3 PMC runs in profiles/<name>.md.
+
+    The figure is FETCH_SIZE + WRITE_SIZE scaled by the counters' reading for
+    a kernel of known size (the summary states the scale and the commands).
+    """
+    path = ROOT / "profiles" / f"{name}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def cpu_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
@@ -102,8 +117,11 @@ def bench_gqa(steps: int, warmup: int, cpu_sample: bool) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel": "paged_gqa_decode (gqa_decode_kernel<128> + gqa_reduce_kernel<128>)",
+            "traffic": profiled_traffic("gqa_decode_config2"),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, calibrated; "
+                              "profiles/gqa_decode_config2.md",
+            "kernel": "paged_gqa_decode op = gqa_decode_kernel<128,3,1> + gqa_reduce_kernel<128>, "
+                      "timed together with HIP events on the launch stream",
         },
         "context_tokens": int(inp.ctx_host.sum()),
         "num_splits": splits,
@@ -136,22 +154,29 @@ def bench_gqa(steps: int, warmup: int, cpu_sample: bool) -> dict:
 
 
 def copy_calibration(nbytes: int = 1 << 30, reps: int = 5) -> None:
-    """A plain device-to-device copy of known size: the scale for PMC byte counters."""
+    """A plain streaming kernel of known size, the scale for PMC byte counters.
+
+    voom's contiguous byte-plane split (kernel ``split_kernel``) over ``nbytes``
+    of 16-bit data reads exactly ``nbytes`` and writes exactly ``nbytes``.
+    """
     import torch
 
-    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
-    dst = torch.empty_like(src)
+    from voom_amd import ops
+
+    src = torch.ones(nbytes // 2, dtype=torch.int16, device="cuda")
+    lo = torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")
+    hi = torch.empty_like(lo)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
-        dst.copy_(src)
+        ops.byteplane_split(src, lo, hi)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    log(f"copy calibration: {nbytes} B read + {nbytes} B written per copy, {ms * 1e3:.1f} us, "
-        f"{2 * nbytes / ms / 1e6:.0f} GB/s (read+write)")
-    del src, dst
+    log(f"copy calibration (split_kernel): {nbytes} B read + {nbytes} B written per launch, "
+        f"{ms * 1e3:.1f} us, {2 * nbytes / ms / 1e6:.0f} GB/s (read+write)")
+    del src, lo, hi
 
 
 def main() -> int:
@@ -161,7 +186,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run a plain 1 GiB device copy (PMC byte-counter calibration)")
+                    help="also run a known-size 1 GiB streaming kernel (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; multi-GPU sharding is design-only "

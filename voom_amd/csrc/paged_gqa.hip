@@ -37,6 +37,25 @@ constexpr int kWavesPerBlock = kThreads / kWave;
 constexpr int kMaxBatch = 1024;
 constexpr int kBlockTokens = 32;
 
+// Pipeline depth (32-token blocks in flight per wavefront) and the occupancy
+// target handed to the register allocator, per head_dim.
+#ifndef VOOM_GQA_NBUF_128
+#define VOOM_GQA_NBUF_128 3
+#endif
+#ifndef VOOM_GQA_WAVES_PER_EU_128
+#define VOOM_GQA_WAVES_PER_EU_128 1
+#endif
+#ifndef VOOM_GQA_CACHE_POLICY
+#define VOOM_GQA_CACHE_POLICY 0
+#endif
+#ifndef VOOM_GQA_SPLITS_PER_CU
+#define VOOM_GQA_SPLITS_PER_CU 4
+#endif
+constexpr int kNbuf128 = VOOM_GQA_NBUF_128;
+constexpr int kWavesPerEu128 = VOOM_GQA_WAVES_PER_EU_128;
+constexpr int kNbuf64 = 3;
+constexpr int kWavesPerEu64 = 2;
+
 // Exclusive prefix sum of per-sequence 32-token block counts into seg[0..B].
 // Requires blockDim.x == kThreads; ends with a barrier.
 __device__ void build_block_prefix(const int32_t* __restrict__ ctx_lens, int B,
@@ -86,9 +105,29 @@ struct SegmentArgs {
   int ctx;       // tokens of this sequence (clamped to table capacity)
 };
 
+// Buffer resource covering one head-page: out-of-range offsets read as zero,
+// so no load of a well-formed call can leave the page.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint16_t* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), static_cast<short>(0),
+                                           bytes, 0x00020000);
+}
+
+// Lane-constant byte offsets of the MFMA operand loads inside a 32-token block.
+struct LaneOffsets {
+  int k;  // K row (8*(i16/4) + i16%4) x D + 8g, in bytes
+  int v;  // V^T row i16 x PT + 8g, in bytes
+};
+
+// Loads block bi of the segment into r.  A block past the end of the piece
+// (bi >= bhi) is issued against an empty descriptor: the loads complete with
+// zeros and move no bytes, which keeps the pipeline's wait counts
+// branch-free without re-reading memory.
 template <int D>
 __device__ __forceinline__ void load_block(BlockRegs<D>& r, const SegmentArgs& a, int bi,
-                                           int& tab_base, int& tab, int lane) {
+                                           int bhi, int& tab_base, int& tab, int lane,
+                                           const LaneOffsets& lo) {
+  const bool live = bi < bhi;
+  if (!live) bi = bhi - 1;
   const int sub_shift = a.pt_shift - 5;
   const int page = bi >> sub_shift;
   const int sub = bi & ((1 << sub_shift) - 1);
@@ -100,21 +139,25 @@ __device__ __forceinline__ void load_block(BlockRegs<D>& r, const SegmentArgs& a
   int slot = __builtin_amdgcn_readlane(tab, page - tab_base);
   if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
   const size_t head_page = static_cast<size_t>(slot) * a.nkv + a.kvh;
-  const int i16 = lane & 15;
-  const int g = lane >> 4;
-  const uint16_t* kb = a.k_pool + ((head_page << a.pt_shift) + sub * kBlockTokens) * D;
-  const int krow = 8 * (i16 >> 2) + (i16 & 3);
+  const int page_elems = D << a.pt_shift;
+  const int page_bytes = live ? page_elems * 2 : 0;
+  const __amdgpu_buffer_rsrc_t kr = page_rsrc(a.k_pool + head_page * page_elems, page_bytes);
+  const __amdgpu_buffer_rsrc_t vr = page_rsrc(a.v_pool + head_page * page_elems, page_bytes);
+  const int k_sub = sub * kBlockTokens * D * 2;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) {
-      r.k[t][s] = *reinterpret_cast<const u32x4*>(kb + (krow + 4 * t) * D + 32 * s + 8 * g);
+      r.k[t][s] = __builtin_amdgcn_raw_buffer_load_b128(kr, lo.k + (4 * t * D + 32 * s) * 2,
+                                                        k_sub, VOOM_GQA_CACHE_POLICY);
     }
   }
-  const uint16_t* vb = a.v_pool + ((head_page * D) << a.pt_shift) + sub * kBlockTokens;
+  const int v_sub = sub * kBlockTokens * 2;
+  const int v_tile = (16 << a.pt_shift) * 2;
 #pragma unroll
   for (int n = 0; n < D / 16; ++n) {
-    r.v[n] = *reinterpret_cast<const u32x4*>(vb + ((16 * n + i16) << a.pt_shift) + 8 * g);
+    r.v[n] = __builtin_amdgcn_raw_buffer_load_b128(vr, lo.v, v_sub + n * v_tile,
+                                                   VOOM_GQA_CACHE_POLICY);
   }
 }
 
@@ -200,8 +243,8 @@ __device__ __forceinline__ void compute_block(const BlockRegs<D>& r, const u32x4
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads, 2) void gqa_decode_kernel(
+template <int D, int NBUF, int WAVES_PER_EU>
+__global__ __launch_bounds__(kThreads, WAVES_PER_EU) void gqa_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ ctx_lens, float* __restrict__ part_o,
@@ -213,8 +256,11 @@ __global__ __launch_bounds__(kThreads, 2) void gqa_decode_kernel(
   build_block_prefix(ctx_lens, B, cap_tokens, seg, wave_tot);
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
-  const long long U = static_cast<long long>(seg[B]) * NKV;
+  // Wave-uniform values are pinned to scalar registers: LDS reads are
+  // per-lane as far as the compiler knows, and the buffer descriptors built
+  // from them must be scalar.
+  const int w = blockIdx.x * kWavesPerBlock + uniform(threadIdx.x / kWave);
+  const long long U = static_cast<long long>(uniform(seg[B])) * NKV;
   // Never more wavefronts than units: every active wavefront then owns at
   // least one unit, which the reduce kernel relies on.
   const int We = static_cast<int>(U < W ? U : W);
@@ -226,17 +272,20 @@ __global__ __launch_bounds__(kThreads, 2) void gqa_decode_kernel(
   int lo = 0, hi = B - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (static_cast<long long>(seg[mid]) * NKV <= u0) lo = mid; else hi = mid - 1;
+    if (static_cast<long long>(uniform(seg[mid])) * NKV <= u0) lo = mid; else hi = mid - 1;
   }
   int b = lo;
-  int nb = seg[b + 1] - seg[b];
-  int kvh = static_cast<int>((u0 - static_cast<long long>(seg[b]) * NKV) / nb);
-  long long S = static_cast<long long>(seg[b]) * NKV + static_cast<long long>(kvh) * nb;
+  int nb = uniform(seg[b + 1]) - uniform(seg[b]);
+  int kvh = static_cast<int>((u0 - static_cast<long long>(uniform(seg[b])) * NKV) / nb);
+  long long S = static_cast<long long>(uniform(seg[b])) * NKV + static_cast<long long>(kvh) * nb;
 
   const int NQ = NKV * G;
   const int i16 = lane & 15;
   const int g = lane >> 4;
   const bool head_ok = i16 < G;
+  LaneOffsets lofs;
+  lofs.k = ((8 * (i16 >> 2) + (i16 & 3)) * D + 8 * g) * 2;
+  lofs.v = ((i16 << pt_shift) + 8 * g) * 2;
 
   while (true) {
     const long long send = S + nb;
@@ -252,7 +301,7 @@ __global__ __launch_bounds__(kThreads, 2) void gqa_decode_kernel(
     a.nkv = NKV;
     a.pt_shift = pt_shift;
     a.num_slots = num_slots;
-    int ctx = ctx_lens[b];
+    const int ctx = uniform(ctx_lens[b]);
     a.ctx = ctx > cap_tokens ? cap_tokens : ctx;
 
     // Q^T operand: lane (head j, group g) holds q[j][32s + 8g .. +8].
@@ -272,19 +321,27 @@ __global__ __launch_bounds__(kThreads, 2) void gqa_decode_kernel(
 
     int tab_base = -(1 << 30);
     int tab = 0;
-    BlockRegs<D> r0, r1;
+    // NBUF-deep register ring: block bi+NBUF-1 is requested while block bi is
+    // consumed.  Every ring slot is loaded unconditionally (prefetches past
+    // the piece are empty loads), so the waitcnt before each compute never
+    // depends on a branch.
+    BlockRegs<D> ring[NBUF];
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; ++j) {
+      load_block<D>(ring[j], a, blo + j, bhi, tab_base, tab, lane, lofs);
+    }
     int bi = blo;
-    load_block<D>(r0, a, bi, tab_base, tab, lane);
-    while (true) {
-      // The prefetch index is clamped so both register sets are always loaded
-      // unconditionally; the waitcnt for the block being consumed then never
-      // depends on a branch.
-      load_block<D>(r1, a, bi + 1 < bhi ? bi + 1 : bhi - 1, tab_base, tab, lane);
-      compute_block<D>(r0, qop, st, a.ctx - bi * kBlockTokens, scale_log2e, lane);
-      if (++bi >= bhi) break;
-      load_block<D>(r0, a, bi + 1 < bhi ? bi + 1 : bhi - 1, tab_base, tab, lane);
-      compute_block<D>(r1, qop, st, a.ctx - bi * kBlockTokens, scale_log2e, lane);
-      if (++bi >= bhi) break;
+    bool done = false;
+    while (!done) {
+#pragma unroll
+      for (int j = 0; j < NBUF; ++j) {
+        if (!done) {
+          const int pf = bi + NBUF - 1;
+          load_block<D>(ring[(j + NBUF - 1) % NBUF], a, pf, bhi, tab_base, tab, lane, lofs);
+          compute_block<D>(ring[j], qop, st, a.ctx - bi * kBlockTokens, scale_log2e, lane);
+          done = ++bi >= bhi;
+        }
+      }
     }
 
     const float l_tot = wave_sum_across_groups(st.l);
@@ -308,8 +365,8 @@ __global__ __launch_bounds__(kThreads, 2) void gqa_decode_kernel(
       kvh = 0;
       do {
         ++b;
-      } while (b < B - 1 && seg[b + 1] == seg[b]);
-      nb = seg[b + 1] - seg[b];
+      } while (b < B - 1 && uniform(seg[b + 1]) == uniform(seg[b]));
+      nb = uniform(seg[b + 1]) - uniform(seg[b]);
     }
   }
 }
@@ -319,6 +376,8 @@ __device__ __forceinline__ long long wave_of_unit(long long u, long long U, int 
   return ((u + 1) * W - 1) / U;
 }
 
+// One wavefront per (sequence, q-head): merges the partial states of the
+// wavefronts that shared the head's KV segment.
 template <int D>
 __global__ __launch_bounds__(kThreads) void gqa_reduce_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -328,65 +387,83 @@ __global__ __launch_bounds__(kThreads) void gqa_reduce_kernel(
   __shared__ int wave_tot[kWavesPerBlock];
   build_block_prefix(ctx_lens, B, max_pages << pt_shift, seg, wave_tot);
 
+  constexpr int DPL = D / kWave;  // dims per lane
   const int lane = threadIdx.x & (kWave - 1);
-  const int s = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
-  if (s >= B * NKV) return;
-  const int b = s / NKV;
-  const int kvh = s - b * NKV;
+  const int task = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
   const int NQ = NKV * G;
+  if (task >= B * NQ) return;
+  const int b = task / NQ;
+  const int hq = task - b * NQ;
+  const int kvh = hq / G;
+  const int j = hq - kvh * G;
+  const int s = b * NKV + kvh;
   const int nb = seg[b + 1] - seg[b];
-  const int n_el = G * D;  // multiple of 64 for D in {64, 128}
-  uint16_t* ob = out + (static_cast<size_t>(b) * NQ + kvh * G) * D;
+  uint16_t* ob = out + static_cast<size_t>(task) * D;
   if (nb == 0) {
-    for (int e = lane; e < n_el; e += kWave) ob[e] = 0;
-    if (lse_out != nullptr && lane < G) lse_out[b * NQ + kvh * G + lane] = -INFINITY;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) ob[lane * DPL + d] = 0;
+    if (lse_out != nullptr && lane == 0) lse_out[task] = -INFINITY;
     return;
   }
   const long long U = static_cast<long long>(seg[B]) * NKV;
   const int We = static_cast<int>(U < W ? U : W);
   const long long us = static_cast<long long>(seg[b]) * NKV + static_cast<long long>(kvh) * nb;
-  const long long w_lo = wave_of_unit(us, U, We);
-  const long long w_hi = wave_of_unit(us + nb - 1, U, We);
+  const long long p0 = s + wave_of_unit(us, U, We);
+  const int n = static_cast<int>(wave_of_unit(us + nb - 1, U, We) + s - p0) + 1;
 
-  constexpr int kMaxPerLane = 16 * D / kWave;
-  const int per_lane = n_el / kWave;
-  float M[kMaxPerLane], L[kMaxPerLane], A[kMaxPerLane];
+  // Single pass over chunks of 64 partials: lane i holds partial i's (m, l);
+  // the chunk's maximum rescales the running state, then the partial outputs
+  // are accumulated with every load of a group of four in flight.
+  const float2* ml2 = reinterpret_cast<const float2*>(part_ml);
+  float M = -INFINITY;
+  float L = 0.f;
+  float acc[DPL];
 #pragma unroll
-  for (int k = 0; k < kMaxPerLane; ++k) {
-    M[k] = -INFINITY;
-    L[k] = 0.f;
-    A[k] = 0.f;
-  }
-  for (long long w = w_lo; w <= w_hi; ++w) {
-    const long long p = s + w;
-    const float* po = part_o + p * n_el;
-    const float* pml = part_ml + p * G * 2;
+  for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
+  for (int i0 = 0; i0 < n; i0 += kWave) {
+    const int i = i0 + lane;
+    const float2 mi = i < n ? ml2[(p0 + i) * G + j] : make_float2(-INFINITY, 0.f);
+    float Mc = mi.x;
 #pragma unroll
-    for (int k = 0; k < kMaxPerLane; ++k) {
-      if (k < per_lane) {
-        const int e = lane + kWave * k;
-        const int head = e / D;
-        const float m = pml[head * 2];
-        const float l = pml[head * 2 + 1];
-        const float mn = fmaxf(M[k], m);
-        const float ca = fast_exp2(M[k] - mn);
-        const float cb = fast_exp2(m - mn);
-        L[k] = L[k] * ca + l * cb;
-        A[k] = A[k] * ca + po[e] * cb;
-        M[k] = mn;
+    for (int o = 32; o >= 1; o >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, o));
+    const float Mn = fmaxf(M, Mc);
+    const float rescale = fast_exp2(M - Mn);
+    const float wl = i < n ? fast_exp2(mi.x - Mn) : 0.f;
+    float Lc = mi.y * wl;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) Lc += __shfl_xor(Lc, o);
+    L = L * rescale + Lc;
+    M = Mn;
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) acc[d] *= rescale;
+    const int cnt = n - i0 < kWave ? n - i0 : kWave;
+    int k = 0;
+    for (; k + 4 <= cnt; k += 4) {
+      float v[4][DPL];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float* po = part_o + ((p0 + i0 + k + u) * G + j) * D + lane * DPL;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) v[u][d] = po[d];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wk = __shfl(wl, k + u);
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] += v[u][d] * wk;
       }
     }
-  }
+    for (; k < cnt; ++k) {
+      const float wk = __shfl(wl, k);
+      const float* po = part_o + ((p0 + i0 + k) * G + j) * D + lane * DPL;
 #pragma unroll
-  for (int k = 0; k < kMaxPerLane; ++k) {
-    if (k < per_lane) {
-      const int e = lane + kWave * k;
-      ob[e] = f2bf(A[k] / L[k]);
-      if (lse_out != nullptr && (e % D) == 0) {
-        lse_out[b * NQ + kvh * G + e / D] = (M[k] + __log2f(L[k])) * 0.6931471805599453f;
-      }
+      for (int d = 0; d < DPL; ++d) acc[d] += po[d] * wk;
     }
   }
+  const float inv = 1.f / L;
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) ob[lane * DPL + d] = f2bf(acc[d] * inv);
+  if (lse_out != nullptr && lane == 0) lse_out[task] = (M + __log2f(L)) * 0.6931471805599453f;
 }
 
 __global__ __launch_bounds__(kThreads) void merge_states_kernel(
@@ -423,7 +500,9 @@ size_t part_slots(int batch, int num_kv_heads, int num_splits) {
 
 using namespace voom;
 
-extern "C" int voom_paged_gqa_default_splits(void) { return device_cu_count() * 8; }
+extern "C" int voom_paged_gqa_default_splits(void) {
+  return device_cu_count() * VOOM_GQA_SPLITS_PER_CU;
+}
 
 extern "C" size_t voom_paged_gqa_workspace_bytes(int batch, int num_q_heads, int num_kv_heads,
                                                  int head_dim, int num_splits) {
@@ -481,27 +560,27 @@ extern "C" int voom_paged_gqa_decode(const void* q, const void* k_pool, const vo
   const int pt_shift = ilog2(page_tokens);
   const float scale_log2e = scale * 1.4426950408889634f;
   const dim3 grid_main((num_splits + kWavesPerBlock - 1) / kWavesPerBlock);
-  const dim3 grid_red((batch * num_kv_heads + kWavesPerBlock - 1) / kWavesPerBlock);
+  const dim3 grid_red((batch * num_q_heads + kWavesPerBlock - 1) / kWavesPerBlock);
   const auto* qq = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint16_t*>(k_pool);
   const auto* vp = static_cast<const uint16_t*>(v_pool);
   auto* oo = static_cast<uint16_t*>(out);
   if (head_dim == 128) {
-    hipLaunchKernelGGL(gqa_decode_kernel<128>, grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
+    hipLaunchKernelGGL((gqa_decode_kernel<128, kNbuf128, kWavesPerEu128>), grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
                        block_table, ctx_lens, part_o, part_ml, batch, num_kv_heads, G,
                        max_pages, pt_shift, num_slots, scale_log2e, num_splits);
     int rc = VOOM_LAUNCH_CHECK("paged_gqa_decode: main kernel launch");
     if (rc) return rc;
-    hipLaunchKernelGGL(gqa_reduce_kernel<128>, grid_red, dim3(kThreads), 0, stream, part_o,
+    hipLaunchKernelGGL((gqa_reduce_kernel<128>), grid_red, dim3(kThreads), 0, stream, part_o,
                        part_ml, ctx_lens, oo, lse_out, batch, num_kv_heads, G, max_pages,
                        pt_shift, num_splits);
   } else {
-    hipLaunchKernelGGL(gqa_decode_kernel<64>, grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
+    hipLaunchKernelGGL((gqa_decode_kernel<64, kNbuf64, kWavesPerEu64>), grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
                        block_table, ctx_lens, part_o, part_ml, batch, num_kv_heads, G,
                        max_pages, pt_shift, num_slots, scale_log2e, num_splits);
     int rc = VOOM_LAUNCH_CHECK("paged_gqa_decode: main kernel launch");
     if (rc) return rc;
-    hipLaunchKernelGGL(gqa_reduce_kernel<64>, grid_red, dim3(kThreads), 0, stream, part_o,
+    hipLaunchKernelGGL((gqa_reduce_kernel<64>), grid_red, dim3(kThreads), 0, stream, part_o,
                        part_ml, ctx_lens, oo, lse_out, batch, num_kv_heads, G, max_pages,
                        pt_shift, num_splits);
   }

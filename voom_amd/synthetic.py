@@ -67,7 +67,10 @@ def gqa_decode_inputs(*, batch: int = 16, num_q_heads: int = 32, num_kv_heads: i
                       head_dim: int = 128, page_tokens: int = 64, ctx_min: int = 1024,
                       ctx_max: int = 32768, ctx_lens=None, rope_theta: float = 5e5,
                       slack_pages: int = 0, device="cuda", seed_base: int = 0,
-                      k_scale_outliers: bool = False) -> PagedGQAInputs:
+                      data_seed: int | None = None) -> PagedGQAInputs:
+    """Config-2 style inputs.  ``data_seed`` replaces the K/V/q and position
+    seeds only (same lengths and page table), which gives a second input set of
+    identical shape for Infinity-Cache rotation."""
     dev = torch.device(device)
     if ctx_lens is None:
         ctx = np.random.default_rng(2 + seed_base).integers(ctx_min, ctx_max + 1, size=batch)
@@ -88,11 +91,11 @@ def gqa_decode_inputs(*, batch: int = 16, num_q_heads: int = 32, num_kv_heads: i
         cursor += n
 
     gen = torch.Generator(device=dev)
-    gen.manual_seed(3 + seed_base)
+    gen.manual_seed(3 + seed_base if data_seed is None else data_seed)
     NKV, D, PT = num_kv_heads, head_dim, page_tokens
     k_pool = torch.empty((slots, NKV, PT, D), dtype=torch.bfloat16, device=dev)
     v_pool = torch.empty((slots, NKV, D, PT), dtype=torch.bfloat16, device=dev)
-    pos_rng = np.random.default_rng(4 + seed_base)
+    pos_rng = np.random.default_rng(4 + seed_base if data_seed is None else data_seed + 1)
     # Fill page by page in slot order, rotating K at random positions.
     chunk = 256
     for s0 in range(0, slots, chunk):
