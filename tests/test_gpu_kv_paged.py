@@ -1,0 +1,159 @@
+"""GPU tests of the PagedKVCache drop-in (append/spill/reload/attend + the
+reference protocol), mirroring tests/test_kv_spill_compress.py:22-60 of the
+reference and checking attention against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_attention as opa
+from voom_amd.kv_paged import PagedKVCache
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+def rand_bf16(shape, gen):
+    # arbitrary 16-bit patterns: NaN payloads, infinities, subnormals included
+    return torch.randint(-32768, 32768, shape, generator=gen, dtype=torch.int32,
+                         device="cuda").to(torch.int16).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("compress", [False, True])
+def test_spilled_page_round_trips_byte_identical(compress):
+    print(f"[kv] reference unit geometry compress={compress}", flush=True)
+    kv = PagedKVCache(num_layers=2, max_bytes=1, spill_dir=None, page_positions=4,
+                      resident_pages=0, compress_spill=compress)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    ref_k, ref_v = [], []
+    for layer in range(2):
+        k = rand_bf16((1, 2, 4, 8), gen)
+        v = rand_bf16((1, 2, 4, 8), gen)
+        ref_k.append(k)
+        ref_v.append(v)
+        kv.update(layer, k, v)
+    for layer in range(2):
+        kv.update(layer, rand_bf16((1, 2, 1, 8), gen), rand_bf16((1, 2, 1, 8), gen))
+    assert kv.stats.spills > 0
+    page = kv._pages[0][0]
+    assert not page.resident
+    lk, lv = page.load()
+    torch.cuda.synchronize()
+    assert lk.dtype == torch.bfloat16
+    assert torch.equal(bits(lk), bits(ref_k[0])) and torch.equal(bits(lv), bits(ref_v[0]))
+    if compress:
+        assert kv.stats.spill_bytes_compressed > 0 and "compress" in kv.stats.summary()
+    kv.release()
+    assert kv.offset == 0 and kv.nbytes() == 0
+
+
+def test_update_returns_everything_appended_even_after_spills():
+    print("[kv] update() concatenation", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    B, NKV, D, PT = 2, 2, 64, 32
+    kv = PagedKVCache(num_layers=3, max_bytes=3 * B * NKV * D * 4 * PT * 2,
+                      page_positions=PT, resident_pages=1)
+    ks = [[] for _ in range(3)]
+    vs = [[] for _ in range(3)]
+    for chunk in (70, 1, 1, 33, 1, 64, 1):
+        for layer in range(3):
+            k = rand_bf16((B, NKV, chunk, D), gen)
+            v = rand_bf16((B, NKV, chunk, D), gen)
+            ks[layer].append(k)
+            vs[layer].append(v)
+            K, V = kv.update(layer, k, v)
+            torch.cuda.synchronize()
+            assert torch.equal(bits(K), bits(torch.cat(ks[layer], dim=2)))
+            assert torch.equal(bits(V), bits(torch.cat(vs[layer], dim=2)))
+    assert kv.stats.spills > 0 and kv.stats.reloads > 0
+    assert kv.offset == 171
+    # the newest closed page of each layer stays resident
+    for layer in range(3):
+        assert kv._pages[layer][-1].resident
+
+
+def attn_oracle(q, K, V, scale):
+    """Reference decode over the concatenated K/V [B, NKV, S, D]."""
+    B = q.shape[0]
+    out = []
+    for b in range(B):
+        out.append(opa.sdpa_decode(q[b, :, 0].float().cpu().numpy(), K[b].float().cpu().numpy(),
+                                   V[b].float().cpu().numpy(), scale))
+    return np.stack(out)[:, :, None, :]
+
+
+@pytest.mark.parametrize("budget_pages", [None, 3])
+def test_attend_matches_oracle_with_and_without_spills(budget_pages):
+    print(f"[kv] attend budget_pages={budget_pages}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    B, NQ, NKV, D, PT, layers = 3, 16, 4, 128, 64, 2
+    page_bytes = B * NKV * D * 4 * PT
+    max_bytes = 1 << 40 if budget_pages is None else budget_pages * page_bytes
+    kv = PagedKVCache(num_layers=layers, max_bytes=max_bytes, page_positions=PT,
+                      resident_pages=1)
+    ks = [[] for _ in range(layers)]
+    vs = [[] for _ in range(layers)]
+    for chunk in (300, 1, 1, 1, 130, 1):
+        for layer in range(layers):
+            k = torch.randn((B, NKV, chunk, D), generator=gen, device="cuda").to(torch.bfloat16)
+            v = torch.randn((B, NKV, chunk, D), generator=gen, device="cuda").to(torch.bfloat16)
+            ks[layer].append(k)
+            vs[layer].append(v)
+            kv.append(layer, k, v)
+        for layer in range(layers):
+            q = torch.randn((B, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+            out = kv.attend(layer, q)
+            torch.cuda.synchronize()
+            ref = attn_oracle(q, torch.cat(ks[layer], 2), torch.cat(vs[layer], 2), D ** -0.5)
+            np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    if budget_pages is not None:
+        assert kv.stats.spills > 0 and kv.stats.reloads > 0
+        assert any(not p.resident for p in kv._pages[0])
+
+
+def test_reload_restores_pages_bitwise_and_attention():
+    print("[kv] explicit spill + reload", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    B, NQ, NKV, D, PT = 2, 8, 2, 128, 64
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, page_positions=PT, resident_pages=1)
+    k = rand_bf16((B, NKV, 500, D), gen)
+    v = torch.randn((B, NKV, 500, D), generator=gen, device="cuda").to(torch.bfloat16)
+    kf = torch.randn((B, NKV, 500, D), generator=gen, device="cuda").to(torch.bfloat16)
+    kv.append(0, kf, v)
+    q = torch.randn((B, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    before = kv.attend(0, q).clone()
+    originals = [tuple(t.clone() for t in p.load()) for p in kv._pages[0]]
+    n = kv.spill([(0, i) for i in range(0, 7, 2)])
+    assert n == 4 and not kv._pages[0][0].resident
+    spilled_out = kv.attend(0, q)
+    assert kv.reload() == 4
+    assert all(p.resident for p in kv._pages[0])
+    for p, (ko, vo) in zip(kv._pages[0], originals):
+        kl, vl = p.load()
+        assert torch.equal(bits(kl), bits(ko)) and torch.equal(bits(vl), bits(vo))
+    after = kv.attend(0, q)
+    torch.cuda.synchronize()
+    # same logical pages in new slots: the kernel result is bitwise unchanged
+    assert torch.equal(bits(after), bits(before))
+    np.testing.assert_allclose(spilled_out.float().cpu().numpy(), before.float().cpu().numpy(),
+                               atol=ATOL, rtol=RTOL)
+    kv.release()
+    assert kv.nbytes() == 0
+
+
+def test_nbytes_counts_resident_pages_and_tail():
+    print("[kv] nbytes accounting", flush=True)
+    B, NKV, D, PT = 1, 2, 64, 32
+    kv = PagedKVCache(num_layers=2, max_bytes=1 << 40, page_positions=PT)
+    x = torch.zeros((B, NKV, 70, D), dtype=torch.bfloat16, device="cuda")
+    for layer in range(2):
+        kv.append(layer, x, x)
+    tok = B * NKV * D * 2 * 2
+    assert kv.nbytes() == 2 * 70 * tok
+    kv.spill([(0, 0)])
+    assert kv.nbytes() == 2 * 70 * tok - PT * tok
+    assert kv.offset == 70 and kv.layer_length(0) == 70

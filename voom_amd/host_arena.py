@@ -1,0 +1,87 @@
+"""Pinned host memory arena for spilled page planes.
+
+Spilled KV lives in page-locked host memory so that spill (D2H) and reload
+(H2D) run as asynchronous copies on a side stream.  Pinned allocations are
+slow (page locking), so memory is taken in large slabs up front (``reserve``)
+and carved with a first-fit free list; a block is a ``torch.uint8`` view of
+its slab.  Slabs are never returned to the system before ``close``.
+"""
+
+from __future__ import annotations
+
+import bisect
+from dataclasses import dataclass
+
+import torch
+
+ALIGN = 256
+
+
+@dataclass
+class HostBlock:
+    slab: int
+    offset: int
+    nbytes: int
+    view: torch.Tensor  # uint8 pinned view of exactly nbytes
+
+
+class HostArena:
+    def __init__(self, slab_bytes: int = 256 << 20, pin: bool | None = None):
+        self.slab_bytes = int(slab_bytes)
+        # Page-locked whenever a device exists (asynchronous copies need it);
+        # plain host memory otherwise, which keeps the allocator testable.
+        self.pin = torch.cuda.is_available() if pin is None else bool(pin)
+        self._slabs: list[torch.Tensor] = []
+        # per slab: sorted list of (offset, size) free extents
+        self._free: list[list[tuple[int, int]]] = []
+        self.used_bytes = 0
+
+    @property
+    def capacity(self) -> int:
+        return sum(s.numel() for s in self._slabs)
+
+    def _add_slab(self, nbytes: int) -> int:
+        size = max(self.slab_bytes, -(-nbytes // ALIGN) * ALIGN)
+        slab = torch.empty(size, dtype=torch.uint8, pin_memory=self.pin)
+        self._slabs.append(slab)
+        self._free.append([(0, size)])
+        return len(self._slabs) - 1
+
+    def reserve(self, nbytes: int) -> None:
+        """Ensure at least ``nbytes`` of free pinned memory exist."""
+        free = sum(sz for ext in self._free for _, sz in ext)
+        while free < nbytes:
+            idx = self._add_slab(min(self.slab_bytes, nbytes - free))
+            free += self._slabs[idx].numel()
+
+    def alloc(self, nbytes: int) -> HostBlock:
+        need = -(-max(int(nbytes), 1) // ALIGN) * ALIGN
+        for si, ext in enumerate(self._free):
+            for k, (off, sz) in enumerate(ext):
+                if sz >= need:
+                    if sz == need:
+                        ext.pop(k)
+                    else:
+                        ext[k] = (off + need, sz - need)
+                    self.used_bytes += need
+                    return HostBlock(si, off, need, self._slabs[si][off:off + int(nbytes)])
+        si = self._add_slab(need)
+        return self.alloc(nbytes)
+
+    def free(self, block: HostBlock) -> None:
+        ext = self._free[block.slab]
+        i = bisect.bisect_left(ext, (block.offset, 0))
+        ext.insert(i, (block.offset, block.nbytes))
+        # coalesce with neighbours
+        if i + 1 < len(ext) and ext[i][0] + ext[i][1] == ext[i + 1][0]:
+            ext[i] = (ext[i][0], ext[i][1] + ext[i + 1][1])
+            ext.pop(i + 1)
+        if i > 0 and ext[i - 1][0] + ext[i - 1][1] == ext[i][0]:
+            ext[i - 1] = (ext[i - 1][0], ext[i - 1][1] + ext[i][1])
+            ext.pop(i)
+        self.used_bytes -= block.nbytes
+
+    def close(self) -> None:
+        self._slabs.clear()
+        self._free.clear()
+        self.used_bytes = 0
