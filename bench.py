@@ -179,12 +179,232 @@ def copy_calibration(nbytes: int = 1 << 30, reps: int = 5) -> None:
     del src, lo, hi
 
 
+def link_ceiling(nbytes: int = 256 << 20, reps: int = 5) -> dict:
+    """Pinned host <-> device copy bandwidth (hipMemcpyAsync through torch)."""
+    import torch
+
+    host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    dev = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    res = {}
+    for name, dst, src in (("h2d", dev, host), ("d2h", host, dev)):
+        dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        res[name + "_gbs"] = nbytes * reps / (time.perf_counter() - t0) / 1e9
+    return res
+
+
+def bench_spill_reload(cpu_sample: bool) -> dict:
+    """Config 3: 32 layers x 32768 tokens x 8 kv heads x 128, evict the oldest
+    50 % of pages (2 GiB) through the byte-plane split into pinned host memory,
+    reload into free pool slots, compare all 4 GiB bitwise."""
+    import numpy as np
+    import torch
+
+    from voom_amd import ops
+    from voom_amd.kv_paged import PagedKVCache
+
+    L, S, NKV, D, PT = 32, 32768, 8, 128, 64
+    log("config 3: building 32 x 32768-token layers (4 GiB of bf16 K/V)")
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    chans = np.random.default_rng(6).choice(D, size=(NKV, 4), replace=True)
+    for h in range(NKV):
+        chans[h] = np.random.default_rng(6 + h).choice(D, size=4, replace=False)
+    outlier = torch.ones((1, NKV, 1, D), device="cuda")
+    for h in range(NKV):
+        outlier[0, h, 0, torch.from_numpy(chans[h]).cuda()] = 20.0
+    kv = PagedKVCache(num_layers=L, max_bytes=1 << 62, page_positions=PT, resident_pages=1,
+                      initial_slots=S // PT)
+    orig = []
+    for layer in range(L):
+        k = (torch.randn((1, NKV, S, D), generator=gen, device="cuda") * outlier).to(torch.bfloat16)
+        v = (torch.randn((1, NKV, S, D), generator=gen, device="cuda") * 0.5).to(torch.bfloat16)
+        kv.append(layer, k, v)
+        orig.append((k, v))
+    spill_bytes = L * (S // PT // 2) * kv.page_nbytes
+    kv.arena.reserve(spill_bytes + (64 << 20))
+    torch.cuda.synchronize()
+    link = link_ceiling()
+    kv.max_bytes = kv.nbytes() - spill_bytes
+    t0 = time.perf_counter()
+    n_spilled = kv.spill()
+    torch.cuda.synchronize()
+    t_spill = time.perf_counter() - t0
+    assert n_spilled == L * (S // PT // 2), n_spilled
+    assert all(not kv._pages[l][i].resident for l in range(L) for i in range(S // PT // 2))
+    t0 = time.perf_counter()
+    n_reloaded = kv.reload()
+    torch.cuda.synchronize()
+    t_reload = time.perf_counter() - t0
+    exact = True
+    for layer in range(L):
+        k2, v2 = ops.gather_kv(kv._pools[layer].k, kv._pools[layer].v, kv._tables[layer], S)
+        exact &= torch.equal(k2.view(torch.int16), orig[layer][0].view(torch.int16))
+        exact &= torch.equal(v2.view(torch.int16), orig[layer][1].view(torch.int16))
+    torch.cuda.synchronize()
+    res = {
+        "workload": "config 3: 32 layers x 32768 tokens x 8 kv x 128 bf16, evict oldest 50% "
+                    "(8192 pages of 256 KiB) via byte-plane split to pinned host, reload",
+        "spill_bytes": spill_bytes,
+        "spill_gbs": spill_bytes / t_spill / 1e9,
+        "reload_gbs": spill_bytes / t_reload / 1e9,
+        "spill_s": t_spill,
+        "reload_s": t_reload,
+        "pages": n_spilled,
+        "reloaded": n_reloaded,
+        "bit_exact": bool(exact),
+        "link_ceiling": link,
+        "spill_frac_of_link": spill_bytes / t_spill / 1e9 / link["d2h_gbs"],
+        "reload_frac_of_link": spill_bytes / t_reload / 1e9 / link["h2d_gbs"],
+    }
+    log(f"config 3: spill {res['spill_gbs']:.1f} GB/s, reload {res['reload_gbs']:.1f} GB/s, "
+        f"link d2h {link['d2h_gbs']:.1f} / h2d {link['h2d_gbs']:.1f} GB/s, exact={exact}")
+    if cpu_sample:
+        from oracle import byteplane as ob
+
+        lib = ob.load_c()
+        sample = orig[0][0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+        t0 = time.perf_counter()
+        lo, hi = ob.split_c(lib, sample) if lib is not None else ob.split(sample)
+        back = ob.merge_c(lib, lo, hi) if lib is not None else ob.merge(lo, hi)
+        dt = time.perf_counter() - t0
+        assert np.array_equal(back, sample)
+        res["cpu_baseline"] = {
+            "value": 2 * sample.nbytes / dt / 1e9, "unit": "GB/s (split+merge bytes)",
+            "cores": 1, "kind": "port",
+            "sample": "byte-plane split + merge of one layer's K (64 MiB), "
+                      "oracle/byteplane.c single-threaded",
+        }
+        from voom_amd import zstd as vz
+
+        if vz.available():
+            hi_np = hi[: 16 << 20]
+            t0 = time.perf_counter()
+            z = vz.compress(hi_np, 1)
+            dtz = time.perf_counter() - t0
+            res["zstd_hi_plane"] = {"ratio": hi_np.nbytes / z.nbytes,
+                                   "compress_gbs_1core": hi_np.nbytes / dtz / 1e9,
+                                   "sample": "16 MiB of layer-0 K hi plane, level 1"}
+    del orig
+    kv.release()
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_long_context(steps: int, cpu_sample: bool) -> dict:
+    """Config 4: one sequence, 64 q / 8 kv heads, 131072 tokens in 64-token
+    pages, oldest 40 % spilled; each decode step appends a token and attends,
+    reloading the spilled pages on the side stream while the resident pages
+    are attended (reference semantics: reload every call)."""
+    import numpy as np
+    import torch
+
+    from voom_amd import ops, synthetic
+    from voom_amd.kv_paged import PagedKVCache
+
+    NQ, NKV, D, PT, S = 64, 8, 128, 64, 131072
+    log("config 4: building a 131072-token sequence (1 GiB of bf16 K/V)")
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 62, page_positions=PT, resident_pages=1,
+                      initial_slots=S // PT + 8)
+    pos = torch.arange(S, device="cuda")
+    chunk = 16384
+    for c0 in range(0, S, chunk):
+        kr = torch.randn((1, NKV, chunk, D), generator=gen, device="cuda")
+        cos, sin = synthetic.rope_tables(pos[c0:c0 + chunk], D, 5e5)
+        k = synthetic.apply_rope_neox(kr, cos, sin).to(torch.bfloat16)
+        v = torch.randn((1, NKV, chunk, D), generator=gen, device="cuda").to(torch.bfloat16)
+        kv.append(0, k, v)
+    n_spill = int(0.4 * (S // PT))
+    qs = torch.randn((steps, 1, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    new_k = torch.randn((steps, 1, NKV, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    new_v = torch.randn((steps, 1, NKV, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    # attention alone over the fully resident sequence
+    ctx = torch.full((1,), S, dtype=torch.int32, device="cuda")
+    pool = kv._pools[0]
+    for _ in range(3):
+        ops.paged_gqa_decode(qs[0], pool.k, pool.v, kv._tables[0], ctx)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(10):
+        ops.paged_gqa_decode(qs[i % steps], pool.k, pool.v, kv._tables[0], ctx)
+    e1.record()
+    torch.cuda.synchronize()
+    t_attn = e0.elapsed_time(e1) / 10 / 1e3
+    spill_pages = [(0, i) for i in range(n_spill)]
+    kv.arena.reserve(n_spill * kv.page_nbytes + (16 << 20))
+    kv.spill(spill_pages)
+    torch.cuda.synchronize()
+    reload_bytes = n_spill * kv.page_nbytes
+    # reload alone (transient, as inside attend)
+    spilled = [p for p in kv._pages[0] if not p.resident]
+    stage = kv._stage_pool(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    kv._stream_in(0, spilled, stage, lambda chunk, slots: None, transient=True)
+    torch.cuda.synchronize()
+    t_reload = time.perf_counter() - t0
+    # decode steps
+    for i in range(2):
+        kv.append(0, new_k[i], new_v[i])
+        kv.attend(0, qs[i])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        kv.append(0, new_k[i], new_v[i])
+        out = kv.attend(0, qs[i])
+    torch.cuda.synchronize()
+    t_step = (time.perf_counter() - t0) / steps
+    overlap = (t_attn + t_reload - t_step) / t_attn
+    res = {
+        "workload": "config 4: 1 x 131072 tokens, 64q/8kv, D=128, 40% (819 pages) spilled, "
+                    f"{steps} decode steps with per-step reload overlapped with attention",
+        "step_ms": t_step * 1e3,
+        "reload_bytes_per_step": reload_bytes,
+        "reload_gbs": reload_bytes / t_step / 1e9,
+        "reload_only_ms": t_reload * 1e3,
+        "attention_only_ms": t_attn * 1e3,
+        "attention_gbs": S * NKV * D * 4 / t_attn / 1e9,
+        "overlap_frac": overlap,
+        "steps": steps,
+    }
+    log(f"config 4: step {t_step * 1e3:.2f} ms, reload alone {t_reload * 1e3:.2f} ms, "
+        f"attention alone {t_attn * 1e3:.3f} ms, overlap {overlap:.2f}")
+    if cpu_sample:
+        from oracle import paged_attention as opa
+
+        K, V = kv.gather(0)
+        Sn = K.shape[2]
+        k_np = K[0].float().cpu().numpy()
+        v_np = V[0].float().cpu().numpy()
+        q_np = qs[steps - 1][0, :, 0].float().cpu().numpy()
+        t0 = time.perf_counter()
+        ref = opa.sdpa_decode(q_np, k_np, v_np, D ** -0.5)
+        dt = time.perf_counter() - t0
+        err = float(np.abs(out[0, :, 0].float().cpu().numpy() - ref).max())
+        res["cpu_baseline"] = {"value": Sn * NKV * D * 4 / dt / 1e9, "unit": "GB/s",
+                               "cores": cpu_threads(), "kind": "port",
+                               "sample": "one decode step over the 131136 concatenated tokens "
+                                         "(fp32 SDPA, oracle/paged_attention.py), all resident"}
+        res["parity_max_abs_err_vs_oracle"] = err
+    kv.release()
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="gqa,spill,long",
+                    help="comma list of legs: gqa (config 2, headline), spill (config 3), "
+                         "long (config 4)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a known-size 1 GiB streaming kernel (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -228,6 +448,16 @@ def main() -> int:
     }
     if "parity_max_abs_err_vs_oracle" in gqa:
         line["parity_max_abs_err_vs_oracle"] = gqa["parity_max_abs_err_vs_oracle"]
+    legs = set(args.only.split(","))
+    extra = {}
+    if "spill" in legs:
+        extra["spill_reload"] = bench_spill_reload(cpu_sample=not args.no_cpu)
+        line["spill_gbs"] = round(extra["spill_reload"]["spill_gbs"], 2)
+        line["reload_gbs"] = round(extra["spill_reload"]["reload_gbs"], 2)
+    if "long" in legs:
+        extra["long_context"] = bench_long_context(64, cpu_sample=not args.no_cpu)
+    if extra:
+        line["other_configs"] = extra
     print(json.dumps(line), flush=True)
     return 0
 

@@ -30,6 +30,7 @@ Where the reference differs by platform:
 from __future__ import annotations
 
 import time
+from collections import OrderedDict
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -68,25 +69,38 @@ class KVStats:
 class _SpillBlock:
     """Host copy of a batch of pages spilled together from one layer.
 
-    Layout of ``block``: four parts, each ``n_pages * part_bytes`` long --
-    K low plane, V low plane, K high plane, V high plane -- page j at offset
-    ``j * part_bytes`` in each part.  ``ready`` is recorded after the D2H copy.
+    The block is a sequence of records of up to ``chunk`` pages (the staging
+    ring's chunk).  A record is contiguous and laid out as four parts -- K low
+    plane, V low plane, K high plane, V high plane -- each ``m * part_bytes``
+    long for the record's m pages, page j at ``(j % chunk) * part_bytes`` in
+    each part.  A record therefore moves in one copy each way, exactly as it
+    sits in a staging buffer.  ``ready`` is recorded after the last D2H copy.
     """
 
-    __slots__ = ("block", "n_pages", "part_bytes", "ready", "live", "compressed")
+    __slots__ = ("block", "n_pages", "part_bytes", "chunk", "ready", "live", "compressed")
 
-    def __init__(self, block: HostBlock, n_pages: int, part_bytes: int):
+    def __init__(self, block: HostBlock, n_pages: int, part_bytes: int, chunk: int):
         self.block = block
         self.n_pages = n_pages
         self.part_bytes = part_bytes
+        self.chunk = chunk
         self.ready: torch.cuda.Event | None = None
         self.live = n_pages
         # per page: (k_hi_frame, v_hi_frame) when the hi plane is compressed
         self.compressed: list[tuple[np.ndarray, np.ndarray] | None] = [None] * n_pages
 
-    def part(self, which: int, j: int, n: int = 1) -> torch.Tensor:
-        off = which * self.n_pages * self.part_bytes + j * self.part_bytes
-        return self.block.view[off:off + n * self.part_bytes]
+    def record_pages(self, r: int) -> int:
+        return min(self.chunk, self.n_pages - r * self.chunk)
+
+    def record(self, r: int) -> torch.Tensor:
+        off = r * self.chunk * 4 * self.part_bytes
+        return self.block.view[off:off + 4 * self.record_pages(r) * self.part_bytes]
+
+    def part(self, which: int, j: int) -> torch.Tensor:
+        r, i = divmod(j, self.chunk)
+        m = self.record_pages(r)
+        off = r * self.chunk * 4 * self.part_bytes + (which * m + i) * self.part_bytes
+        return self.block.view[off:off + self.part_bytes]
 
 
 class _Page:
@@ -114,6 +128,44 @@ class _Page:
     def load(self) -> tuple[torch.Tensor, torch.Tensor]:
         """The page's K and V as [B, NKV, page_positions, D] (bit-exact)."""
         return self.cache._page_tensors(self)
+
+
+class _StagingRing:
+    """Persistent device staging buffers reused round-robin.
+
+    Each buffer carries the event after which it may be overwritten; the
+    stream that writes it next waits on that event, so the H2D/D2H copies on
+    the side stream and the split/merge kernels on the main stream pipeline
+    without host synchronisation or allocator churn.  Buffers are large
+    (2 x 256 MiB): every copy and every cross-stream event costs on the order
+    of 0.1 ms of engine idle time on MI355X, so fewer, larger transfers keep
+    the host link saturated.
+    """
+
+    def __init__(self, device: torch.device, nbuf: int = 2, nbytes: int = 256 << 20):
+        self.device = device
+        self.nbytes = nbytes
+        self.bufs: list[torch.Tensor | None] = [None] * nbuf
+        self.free_ev: list[torch.cuda.Event | None] = [None] * nbuf
+        self.i = 0
+
+    def acquire(self, writer: torch.cuda.Stream, nbytes: int):
+        idx = self.i
+        self.i = (self.i + 1) % len(self.bufs)
+        buf = self.bufs[idx]
+        if buf is None or buf.numel() < nbytes:
+            if self.free_ev[idx] is not None:
+                self.free_ev[idx].synchronize()
+            buf = torch.empty(max(nbytes, self.nbytes), dtype=torch.uint8, device=self.device)
+            self.bufs[idx] = buf
+        elif self.free_ev[idx] is not None:
+            writer.wait_event(self.free_ev[idx])
+        return idx, buf[:nbytes]
+
+    def release(self, idx: int, last_user: torch.cuda.Stream) -> None:
+        ev = torch.cuda.Event()
+        ev.record(last_user)
+        self.free_ev[idx] = ev
 
 
 def budget_victims(pages: list[list], resident_pages: int, current_bytes: int,
@@ -170,6 +222,8 @@ class PagedKVCache:
         self._own_arena = arena is None
         self.stats = KVStats()
         self._copy_stream: torch.cuda.Stream | None = None
+        self._ring = _StagingRing(self.device)
+        self._i32_cache: OrderedDict = OrderedDict()
         self._reset_state()
 
     # ---- state ------------------------------------------------------------
@@ -220,6 +274,30 @@ class PagedKVCache:
             self._copy_stream = torch.cuda.Stream(device=self.device)
         return self._copy_stream
 
+    def _dev_i32(self, values, cache: bool = False) -> torch.Tensor:
+        """Int32 device tensor through a pinned buffer (asynchronous, no host stall).
+
+        With ``cache`` the tensor is memoised by value: index tensors that
+        repeat every decode step (staging-slot tables, the resident page
+        table) are uploaded once.
+        """
+        arr = np.ascontiguousarray(values, dtype=np.int32)
+        if cache:
+            key = (arr.shape, arr.tobytes())
+            hit = self._i32_cache.get(key)
+            if hit is not None:
+                self._i32_cache.move_to_end(key)
+                return hit
+        host = torch.from_numpy(arr)
+        if self.arena.pin:
+            host = host.pin_memory()
+        dev = host.to(self.device, non_blocking=True)
+        if cache:
+            self._i32_cache[key] = dev
+            if len(self._i32_cache) > 256:
+                self._i32_cache.popitem(last=False)
+        return dev
+
     @property
     def page_nbytes(self) -> int:
         B, NKV, D = self._geom
@@ -240,15 +318,14 @@ class PagedKVCache:
             if host is not None:
                 new[:, :host.shape[1]] = host
             self._tables_host[layer] = host = new
-            self._tables[layer] = torch.from_numpy(new).to(self.device)
             for page, slots in cols.items():
                 host[:, page] = -1 if slots is None else np.asarray(slots, np.int32)
-            self._tables[layer].copy_(torch.from_numpy(host))
+            self._tables[layer] = self._dev_i32(host)
             return
         for page, slots in cols.items():
             host[:, page] = -1 if slots is None else np.asarray(slots, np.int32)
         lo, hi = min(cols), max(cols) + 1
-        self._tables[layer][:, lo:hi].copy_(torch.from_numpy(np.ascontiguousarray(host[:, lo:hi])))
+        self._tables[layer][:, lo:hi].copy_(self._dev_i32(host[:, lo:hi]))
 
     def _set_table(self, layer: int, page_idx: int, slots) -> None:
         self._set_table_cols(layer, {page_idx: slots})
@@ -323,36 +400,22 @@ class PagedKVCache:
         """Logical K/V [B, NKV, S, D] of a layer, spilled pages reloaded transiently."""
         S = self._len[layer]
         pool = self._pool(layer)
+        k_all, v_all = ops.gather_kv(pool.k, pool.v, self._tables[layer], S)
         spilled = [p for p in self._pages[layer] if not p.resident]
-        if not spilled:
-            return ops.gather_kv(pool.k, pool.v, self._tables[layer], S)
-        stage, slots = self._transient_reload(layer, spilled)
-        table = self._tables[layer].clone()
-        # Point spilled pages at their staging slots (a second pool): gather
-        # resident and staged pages separately and interleave by page.
-        k_res, v_res = ops.gather_kv(pool.k, pool.v, self._resident_table(layer, table), S)
-        B, NKV, D = self._geom
-        PT = self.page_positions
-        st_table = torch.full_like(table, -1)
-        for j, p in enumerate(spilled):
-            st_table[:, p.index] = torch.tensor(slots[j * B:(j + 1) * B], dtype=torch.int32,
-                                                device=self.device)
-        torch.cuda.current_stream().wait_stream(self._stream())
-        k_st, v_st = ops.gather_kv(stage.k, stage.v, st_table, S)
-        mask = torch.zeros(S, dtype=torch.bool, device=self.device)
-        for p in spilled:
-            mask[p.index * PT:(p.index + 1) * PT] = True
-        k_all = torch.where(mask[None, None, :, None], k_st, k_res)
-        v_all = torch.where(mask[None, None, :, None], v_st, v_res)
-        self._release_stage(layer, slots)
-        return k_all, v_all
+        if spilled:
+            PT = self.page_positions
+            stage = self._stage_pool(layer)
 
-    def _resident_table(self, layer: int, table: torch.Tensor) -> torch.Tensor:
-        t = table.clone()
-        for p in self._pages[layer]:
-            if not p.resident:
-                t[:, p.index] = -1
-        return t
+            def place(chunk, slots):
+                B = self._geom[0]
+                for j, p in enumerate(chunk):
+                    idx = self._dev_i32(slots[j * B:(j + 1) * B], cache=True).long()
+                    k_all[:, :, p.index * PT:(p.index + 1) * PT] = stage.k.index_select(0, idx)
+                    v_all[:, :, p.index * PT:(p.index + 1) * PT] = \
+                        stage.v.index_select(0, idx).transpose(2, 3)
+
+            self._stream_in(layer, spilled, stage, place, transient=True)
+        return k_all, v_all
 
     def release(self) -> None:
         """Free device slots and host copies; offset and nbytes return to 0."""
@@ -395,51 +458,73 @@ class PagedKVCache:
         for p in pages:
             by_layer.setdefault(p.layer, []).append(p)
         t0 = time.perf_counter()
+        work = []
         for layer, lp in by_layer.items():
-            self._spill_layer(layer, lp)
+            work += self._spill_plan(layer, lp)
+        self._spill_chunks(work)
+        for layer, lp in by_layer.items():
+            pool = self._pool(layer)
+            for p in lp:
+                pool.release(p.slots)
+                p.slots = None
+            self._set_table_cols(layer, {p.index: None for p in lp})
         if self.compress_spill:
             self._compress_spilled(pages)
         self.stats.spills += len(pages)
         self.stats.spill_s += time.perf_counter() - t0
         return len(pages)
 
-    def _spill_layer(self, layer: int, pages: list[_Page]) -> None:
+    def _spill_plan(self, layer: int, pages: list[_Page]):
+        """One host block for the layer's pages; returns its chunk work items."""
         B = self._geom[0]
         pool = self._pool(layer)
-        part = B * pool.slot_bytes // 2            # bytes of one plane of K (or V) of a page
+        part = B * pool.slot_bytes // 2       # one plane of a page's K (or V)
         n = len(pages)
-        block = self.arena.alloc(4 * n * part)
-        sb = _SpillBlock(block, n, part)
-        slots = [s for p in pages for s in p.slots]
-        main = torch.cuda.current_stream()
-        copy = self._stream()
-        slot_t = torch.tensor(slots, dtype=torch.int32, device=self.device)
-        staging = torch.empty(4 * n * part, dtype=torch.uint8, device=self.device)
-        # Split on the main stream (ordered after the writes of the pages), copy
-        # to the host on the side stream.
-        lo_k, lo_v = staging[0:n * part], staging[n * part:2 * n * part]
-        hi_k, hi_v = staging[2 * n * part:3 * n * part], staging[3 * n * part:]
-        if ops.slot_codec_supported(pool.k):
-            ops.byteplane_split_slots(pool.k, slot_t, lo_k, hi_k)
-            ops.byteplane_split_slots(pool.v, slot_t, lo_v, hi_v)
-        else:
-            idx = slot_t.long()
-            ops.byteplane_split(pool.k.index_select(0, idx).contiguous(), lo_k, hi_k)
-            ops.byteplane_split(pool.v.index_select(0, idx).contiguous(), lo_v, hi_v)
-        split_done = torch.cuda.Event()
-        split_done.record(main)
-        copy.wait_event(split_done)
-        with torch.cuda.stream(copy):
-            block.view.copy_(staging, non_blocking=True)
-            staging.record_stream(copy)
-        sb.ready = torch.cuda.Event()
-        sb.ready.record(copy)
+        per_chunk = max(1, self._ring.nbytes // (4 * part))
+        sb = _SpillBlock(self.arena.alloc(4 * n * part), n, part, per_chunk)
         for j, p in enumerate(pages):
-            pool.release(p.slots)
-            p.slots = None
             p.host = sb
             p.host_j = j
-        self._set_table_cols(layer, {p.index: None for p in pages})
+        return [(pool, pages[c0:c0 + per_chunk], sb, c0 // per_chunk)
+                for c0 in range(0, n, per_chunk)]
+
+    def _spill_chunks(self, work) -> None:
+        """Byte-plane split (main stream, ordered after the pages' writes) into
+        staging buffers, then D2H of each staged record (side stream).
+
+        Work is processed in windows of ring size; within a window every split
+        is enqueued before any copy, so copies run back to back even when the
+        two streams share a hardware queue.
+        """
+        main = torch.cuda.current_stream()
+        copy = self._stream()
+        nbuf = len(self._ring.bufs)
+        for w0 in range(0, len(work), nbuf):
+            staged = []
+            for pool, cp, sb, rec in work[w0:w0 + nbuf]:
+                m = len(cp)
+                part = sb.part_bytes
+                slot_t = self._dev_i32([s for p in cp for s in p.slots])
+                idx, buf = self._ring.acquire(main, 4 * m * part)
+                lo_k, lo_v = buf[0:m * part], buf[m * part:2 * m * part]
+                hi_k, hi_v = buf[2 * m * part:3 * m * part], buf[3 * m * part:4 * m * part]
+                if ops.slot_codec_supported(pool.k):
+                    ops.byteplane_split_slots(pool.k, slot_t, lo_k, hi_k)
+                    ops.byteplane_split_slots(pool.v, slot_t, lo_v, hi_v)
+                else:
+                    sel = slot_t.long()
+                    ops.byteplane_split(pool.k.index_select(0, sel).contiguous(), lo_k, hi_k)
+                    ops.byteplane_split(pool.v.index_select(0, sel).contiguous(), lo_v, hi_v)
+                ev = torch.cuda.Event()
+                ev.record(main)
+                staged.append((idx, buf, sb, rec, ev))
+            for idx, buf, sb, rec, ev in staged:
+                copy.wait_event(ev)
+                with torch.cuda.stream(copy):
+                    sb.record(rec).copy_(buf, non_blocking=True)
+                self._ring.release(idx, copy)
+                sb.ready = torch.cuda.Event()
+                sb.ready.record(copy)
 
     def _compress_spilled(self, pages: list[_Page]) -> None:
         for p in pages:
@@ -467,82 +552,112 @@ class PagedKVCache:
         return parts
 
     def _upload_planes(self, pages: list[_Page], staging: torch.Tensor, part: int) -> None:
-        """H2D the planes of ``pages`` into staging laid out [lo_k | lo_v | hi_k | hi_v]."""
+        """H2D the planes of ``pages`` into staging laid out [lo_k | lo_v | hi_k | hi_v].
+
+        A chunk that is exactly one uncompressed host record, in order, moves
+        in a single copy; anything else is assembled page by page.
+        """
         n = len(pages)
-        j = 0
-        while j < n:
-            p = pages[j]
-            sb = p.host
-            # extend a run of consecutive pages of the same spill block
-            r = 1
-            while (j + r < n and pages[j + r].host is sb and pages[j + r].host_j == p.host_j + r
-                   and sb.compressed[p.host_j + r] is None and sb.compressed[p.host_j] is None):
-                r += 1
-            if sb.compressed[p.host_j] is None:
-                for w in range(4):
-                    src = sb.part(w, p.host_j, r)
-                    staging[w * n * part + j * part: w * n * part + (j + r) * part].copy_(
-                        src, non_blocking=True)
-            else:
-                parts = self._host_planes(p)
-                for w in range(4):
-                    staging[w * n * part + j * part: w * n * part + (j + 1) * part].copy_(
-                        parts[w], non_blocking=True)
-            j += r
+        p0 = pages[0]
+        sb = p0.host
+        if (p0.host_j % sb.chunk == 0 and n == sb.record_pages(p0.host_j // sb.chunk)
+                and all(p.host is sb and p.host_j == p0.host_j + j
+                        and sb.compressed[p.host_j] is None for j, p in enumerate(pages))):
+            staging.copy_(sb.record(p0.host_j // sb.chunk), non_blocking=True)
+            return
+        for j, p in enumerate(pages):
+            parts = self._host_planes(p)
+            for w in range(4):
+                staging[(w * n + j) * part:(w * n + j + 1) * part].copy_(parts[w],
+                                                                         non_blocking=True)
 
     def _merge_into(self, pool: DevicePagePool, staging: torch.Tensor, n: int, part: int,
-                    slots: list[int]) -> None:
-        slot_t = torch.tensor(slots, dtype=torch.int32, device=self.device)
+                    slots: list[int], cache: bool = False) -> None:
+        slot_t = self._dev_i32(slots, cache=cache)
         lo_k, lo_v = staging[0:n * part], staging[n * part:2 * n * part]
-        hi_k, hi_v = staging[2 * n * part:3 * n * part], staging[3 * n * part:]
+        hi_k, hi_v = staging[2 * n * part:3 * n * part], staging[3 * n * part:4 * n * part]
         if ops.slot_codec_supported(pool.k):
             ops.byteplane_merge_slots(lo_k, hi_k, pool.k, slot_t)
             ops.byteplane_merge_slots(lo_v, hi_v, pool.v, slot_t)
         else:
-            idx = slot_t.long()
+            sel = slot_t.long()
             kb = torch.empty((len(slots),) + tuple(pool.k.shape[1:]), dtype=pool.k.dtype,
                              device=self.device)
             vb = torch.empty((len(slots),) + tuple(pool.v.shape[1:]), dtype=pool.v.dtype,
                              device=self.device)
             ops.byteplane_merge(lo_k, hi_k, kb)
             ops.byteplane_merge(lo_v, hi_v, vb)
-            pool.k.index_copy_(0, idx, kb)
-            pool.v.index_copy_(0, idx, vb)
+            pool.k.index_copy_(0, sel, kb)
+            pool.v.index_copy_(0, sel, vb)
 
-    def _transient_reload(self, layer: int, pages: list[_Page]):
-        """Stage spilled pages in the layer's staging pool on the side stream.
+    def _stream_in(self, layer: int, pages: list[_Page], target: DevicePagePool, consume,
+                   transient: bool) -> None:
+        """Bring spilled pages of one layer into ``target``, chunk by chunk."""
+        self._pipeline_in([(layer, pages, target, consume, transient)])
 
-        Returns (staging pool, slots); the side stream holds the work, so the
-        caller waits on it before reading the slots.
+    def _pipeline_in(self, jobs) -> None:
+        """Upload spilled pages and merge them into device slots.
+
+        ``jobs``: (layer, pages, target pool, consume(chunk_pages, slots),
+        transient).  Each job is cut into staging-ring chunks.  Per window of
+        ring size: every H2D copy of the window is enqueued on the side stream
+        first, then on the main stream, per chunk, a wait for its copy, the
+        byte-plane merge into target slots, and ``consume``.  Copies thus run
+        back to back and chunk i is merged and consumed while chunk i+1 is in
+        flight.  Transient jobs land in fixed staging slots per ring buffer,
+        so the index tensors of a steady decode loop repeat (and stay cached);
+        the slots are reused safely because merges and the consumers' reads
+        are all on the main stream.
         """
         B = self._geom[0]
-        stage = self._stage_pool(layer)
-        t0 = time.perf_counter()
-        slots = stage.allocate(B * len(pages))
-        part = B * stage.slot_bytes // 2
+        main = torch.cuda.current_stream()
         copy = self._stream()
-        copy.wait_stream(torch.cuda.current_stream())
-        for sb in {id(p.host): p.host for p in pages}.values():
-            copy.wait_event(sb.ready)
-        with torch.cuda.stream(copy):
-            staging = torch.empty(4 * len(pages) * part, dtype=torch.uint8, device=self.device)
-            self._upload_planes(pages, staging, part)
-            self._merge_into(stage, staging, len(pages), part, slots)
-        self.stats.reloads += len(pages)
+        nbuf = len(self._ring.bufs)
+        t0 = time.perf_counter()
+        chunks = []
+        n_pages = 0
+        for layer, pages, target, consume, transient in jobs:
+            part = B * target.slot_bytes // 2
+            per_chunk = max(1, self._ring.nbytes // (4 * part))
+            if transient:
+                target.ensure_capacity(nbuf * per_chunk * B)
+            for sb in {id(p.host): p.host for p in pages}.values():
+                copy.wait_event(sb.ready)
+            for c0 in range(0, len(pages), per_chunk):
+                chunks.append((pages[c0:c0 + per_chunk], target, consume, transient, part,
+                               per_chunk))
+            n_pages += len(pages)
+        for w0 in range(0, len(chunks), nbuf):
+            window = chunks[w0:w0 + nbuf]
+            landed = []
+            for cp, target, consume, transient, part, per_chunk in window:
+                idx, buf = self._ring.acquire(copy, 4 * len(cp) * part)
+                with torch.cuda.stream(copy):
+                    self._upload_planes(cp, buf, part)
+                ev = torch.cuda.Event()
+                ev.record(copy)
+                landed.append((idx, buf, ev))
+            for (cp, target, consume, transient, part, per_chunk), (idx, buf, ev) in zip(window,
+                                                                                      landed):
+                main.wait_event(ev)
+                m = len(cp)
+                if transient:
+                    base = idx * per_chunk * B
+                    slots = list(range(base, base + m * B))
+                else:
+                    slots = target.allocate(B * m)
+                self._merge_into(target, buf, m, part, slots, cache=transient)
+                self._ring.release(idx, main)
+                consume(cp, slots)
+        self.stats.reloads += n_pages
         self.stats.reload_s += time.perf_counter() - t0
-        return stage, slots
-
-    def _release_stage(self, layer: int, slots: list[int]) -> None:
-        # Later staging writes go through the side stream, which first waits
-        # for the main stream (see _transient_reload), so the slots can be
-        # recycled as soon as the reading kernels are enqueued.
-        self._stage_pools[layer].release(slots)
 
     def reload(self, pages=None, stream: torch.cuda.Stream | None = None) -> int:
         """Make spilled pages resident again in fresh pool slots; returns the count.
 
-        The copies and merges run on ``stream`` (default: the cache's side
-        stream); the current stream waits for them before returning.
+        Uploads run on the cache's side stream (or ``stream``), merges on the
+        current stream; nothing blocks the host except compressed pages,
+        which are decompressed on the host first.
         """
         if pages is None:
             pages = [p for layer in self._pages for p in layer if not p.resident]
@@ -550,30 +665,28 @@ class PagedKVCache:
         pages = [p for p in pages if not p.resident]
         if not pages:
             return 0
-        t0 = time.perf_counter()
+        if stream is not None:
+            self._copy_stream = stream
         B = self._geom[0]
-        side = stream if stream is not None else self._stream()
-        side.wait_stream(torch.cuda.current_stream())
         by_layer: dict[int, list[_Page]] = {}
         for p in pages:
             by_layer.setdefault(p.layer, []).append(p)
+        jobs = []
+        done: dict[int, list[_Page]] = {}
         for layer, lp in by_layer.items():
-            pool = self._pool(layer)
-            slots = pool.allocate(B * len(lp))
-            part = B * pool.slot_bytes // 2
-            for sb in {id(p.host): p.host for p in lp}.values():
-                side.wait_event(sb.ready)
-            with torch.cuda.stream(side):
-                staging = torch.empty(4 * len(lp) * part, dtype=torch.uint8, device=self.device)
-                self._upload_planes(lp, staging, part)
-                self._merge_into(pool, staging, len(lp), part, slots)
-            for j, p in enumerate(lp):
-                p.slots = slots[j * B:(j + 1) * B]
-                self._drop_host(p)
+            done[layer] = []
+
+            def adopt(chunk, slots, acc=done[layer]):
+                for j, p in enumerate(chunk):
+                    p.slots = slots[j * B:(j + 1) * B]
+                    acc.append(p)
+
+            jobs.append((layer, lp, self._pool(layer), adopt, False))
+        self._pipeline_in(jobs)
+        for layer, lp in done.items():
             self._set_table_cols(layer, {p.index: p.slots for p in lp})
-        torch.cuda.current_stream().wait_stream(side)
-        self.stats.reloads += len(pages)
-        self.stats.reload_s += time.perf_counter() - t0
+            for p in lp:
+                self._drop_host(p)
         return len(pages)
 
     def _drop_host(self, p: _Page) -> None:
@@ -587,18 +700,21 @@ class PagedKVCache:
 
     def _page_tensors(self, p: _Page):
         B, NKV, D = self._geom
-        pool = self._pool(p.layer)
         if p.resident:
-            idx = torch.tensor(p.slots, dtype=torch.long, device=self.device)
+            pool = self._pool(p.layer)
+            idx = self._dev_i32(p.slots).long()
             return (pool.k.index_select(0, idx),
                     pool.v.index_select(0, idx).transpose(2, 3).contiguous())
-        stage, slots = self._transient_reload(p.layer, [p])
-        torch.cuda.current_stream().wait_stream(self._stream())
-        idx = torch.tensor(slots, dtype=torch.long, device=self.device)
-        k = stage.k.index_select(0, idx)
-        v = stage.v.index_select(0, idx).transpose(2, 3).contiguous()
-        self._release_stage(p.layer, slots)
-        return k, v
+        stage = self._stage_pool(p.layer)
+        out = []
+
+        def grab(chunk, slots):
+            idx = self._dev_i32(slots).long()
+            out.append(stage.k.index_select(0, idx))
+            out.append(stage.v.index_select(0, idx).transpose(2, 3).contiguous())
+
+        self._stream_in(p.layer, [p], stage, grab, transient=True)
+        return out[0], out[1]
 
     # ---- fused decode attention --------------------------------------------
 
@@ -606,9 +722,12 @@ class PagedKVCache:
         """Decode attention of q [B, NQ, 1, D] over the layer's pages.
 
         Replaces kv.update + mx.fast.scaled_dot_product_attention at
-        runtime/layer_runner.py:158,179-180 with one paged kernel; spilled
-        pages are reloaded on the side stream while the resident pages are
-        attended, and the two partial results are merged by log-sum-exp.
+        runtime/layer_runner.py:158,179-180 with the paged kernel.  Spilled
+        pages (reloaded for every call, as the reference does) stream in on
+        the side stream chunk by chunk while the resident pages are attended;
+        each landed chunk is attended in turn and the partial results are
+        merged by log-sum-exp, so only the last chunk's attention is exposed
+        after the transfer.
         """
         B, NKV, D = self._geom
         S = self._len[layer]
@@ -620,29 +739,33 @@ class PagedKVCache:
             ctx = torch.full((B,), S, dtype=torch.int32, device=self.device)
             return ops.paged_gqa_decode(q, pool.k, pool.v, self._tables[layer], ctx, scale=scale)
         PT = self.page_positions
-        stage, slots = self._transient_reload(layer, spilled)
-        # Resident pages in logical order, the open page last (attention over
-        # one query token is order-free; only the partial page must be last).
-        host = self._tables_host[layer]
+        # Resident pages, the open page last (attention of one query token is
+        # order-free; only a partial page has to be the last one).
         res_cols = [p.index for p in self._pages[layer] if p.resident]
         open_len = S - len(self._pages[layer]) * PT
         if open_len > 0:
             res_cols.append(len(self._pages[layer]))
         res_ctx = (len(res_cols) - (1 if open_len > 0 else 0)) * PT + max(open_len, 0)
-        outs = []
+        state: list[tuple[torch.Tensor, torch.Tensor]] = []
+
+        def fold(o_l):
+            if state:
+                state[0] = ops.merge_attn_states(state[0][0], state[0][1], o_l[0], o_l[1])
+            else:
+                state.append(o_l)
+
         if res_cols:
-            t_res = torch.from_numpy(np.ascontiguousarray(host[:, res_cols])).to(self.device)
+            t_res = self._dev_i32(self._tables_host[layer][:, res_cols], cache=True)
             c_res = torch.full((B,), res_ctx, dtype=torch.int32, device=self.device)
-            outs.append(ops.paged_gqa_decode(q, pool.k, pool.v, t_res, c_res, scale=scale,
-                                             return_lse=True))
-        t_sp = torch.tensor(np.asarray(slots, np.int32).reshape(len(spilled), B).T.copy(),
-                            device=self.device)
-        c_sp = torch.full((B,), len(spilled) * PT, dtype=torch.int32, device=self.device)
-        torch.cuda.current_stream().wait_stream(self._stream())
-        outs.append(ops.paged_gqa_decode(q, stage.k, stage.v, t_sp, c_sp, scale=scale,
-                                         return_lse=True))
-        self._release_stage(layer, slots)
-        if len(outs) == 1:
-            return outs[0][0]
-        (o1, l1), (o2, l2) = outs
-        return ops.merge_attn_states(o1, l1, o2, l2)[0]
+            fold(ops.paged_gqa_decode(q, pool.k, pool.v, t_res, c_res, scale=scale,
+                                      return_lse=True))
+        stage = self._stage_pool(layer)
+
+        def attend_chunk(chunk, slots):
+            m = len(chunk)
+            t = self._dev_i32(np.asarray(slots, np.int32).reshape(m, B).T, cache=True)
+            c = torch.full((B,), m * PT, dtype=torch.int32, device=self.device)
+            fold(ops.paged_gqa_decode(q, stage.k, stage.v, t, c, scale=scale, return_lse=True))
+
+        self._stream_in(layer, spilled, stage, attend_chunk, transient=True)
+        return state[0][0]
