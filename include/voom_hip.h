@@ -83,6 +83,31 @@ int voom_merge_attn_states(const void* o_a, const float* lse_a, const void* o_b,
                            int head_dim, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Absorbed-MLA paged decode: the latent contraction.
+ *
+ * Replaces the latent part of _mla_absorbed_attention (runtime/glm.py:133-164):
+ * scores = q_lat . lat^T * scale in fp32, softmax, probabilities rounded to
+ * bf16, weighted_c = p . lat[:, :512] returned in bf16.  The latent cache is
+ * paged: lat_pool [num_slots, page_tokens, latent_dim] bf16, one slot holding
+ * page_tokens consecutive tokens of one sequence (the compressed cache of
+ * glm.py:265-274 / kv_cache.py:99-105, paged).
+ *   q_lat  [batch, num_heads, latent_dim] bf16 = [q_nope . W_UK | q_rope]
+ *   out_c  [batch, num_heads, c_dim] bf16 (weighted_c)
+ *   lse_out [batch, num_heads] fp32 natural-log sum-exp, or NULL
+ * latent_dim 576 with c_dim 512 (kv_lora_rank 512 + rope 64); num_heads a
+ * multiple of 32; page_tokens a power of two >= 64.  num_ranges splits each
+ * sequence's tokens (0 = library default); the workspace must hold
+ * voom_mla_workspace_bytes(batch, num_heads, num_ranges) bytes.
+ * ------------------------------------------------------------------------- */
+size_t voom_mla_workspace_bytes(int batch, int num_heads, int num_ranges);
+int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
+                             const int32_t* block_table, const int32_t* ctx_lens,
+                             void* out_c, float* lse_out, void* workspace, size_t ws_bytes,
+                             int batch, int num_heads, int latent_dim, int c_dim,
+                             int page_tokens, int max_pages, int num_slots, float scale,
+                             int num_ranges, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Page writes and reads.
  *
  * voom_append_kv writes L new tokens per sequence into the pools at logical

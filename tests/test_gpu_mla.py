@@ -1,0 +1,105 @@
+"""GPU parity of the absorbed-MLA paged decode against the CPU oracle
+(oracle/mla.py, a restatement of runtime/glm.py:78-210).
+
+Tolerance 2e-2 abs / 1e-2 rel on bf16 outputs (fp32 accumulation)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mla as omla
+from voom_amd import ops, synthetic
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def q_lat_of(inp):
+    w_uk, w_uv_t = ops.split_kv_b(inp.kv_b, inp.q_nope.shape[1], inp.dn, inp.dv)
+    q_abs = torch.bmm(inp.q_nope.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
+    return torch.cat([q_abs, inp.q_rope], -1).contiguous(), w_uk, w_uv_t
+
+
+def check_latent(inp, num_ranges=0, batches=None):
+    q_lat, _, _ = q_lat_of(inp)
+    wc, lse = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                                    scale=inp.scale, return_lse=True, num_ranges=num_ranges)
+    torch.cuda.synchronize()
+    got = wc.float().cpu().numpy()
+    ql = q_lat.float().cpu().numpy()
+    for b in (batches if batches is not None else range(q_lat.shape[0])):
+        lat = synthetic.mla_logical_latent(inp, b)
+        ref = omla.absorbed_weighted_c(ql[b:b + 1, :, None, :], lat[None], 64, inp.scale,
+                                       bf16=True)[0, :, 0]
+        np.testing.assert_allclose(got[b], ref, atol=ATOL, rtol=RTOL)
+        s = (ql[b].astype(np.float64) @ lat.T.astype(np.float64)) * inp.scale
+        m = s.max(axis=1)
+        ref_lse = m + np.log(np.exp(s - m[:, None]).sum(axis=1))
+        np.testing.assert_allclose(lse[b].cpu().numpy(), ref_lse, atol=1e-2, rtol=1e-3)
+    return wc
+
+
+@pytest.mark.parametrize("ctx", [[1, 64], [63, 65, 200], [300, 1000]])
+def test_latent_contraction_small(ctx):
+    print(f"[mla] latent ctx={ctx}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=len(ctx), heads=32, ctx_lens=ctx, slack_pages=3)
+    check_latent(inp)
+
+
+@pytest.mark.parametrize("nr", [1, 3, 8])
+def test_range_splits_agree(nr):
+    print(f"[mla] ranges={nr}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=2, heads=64, ctx_lens=[777, 2048])
+    check_latent(inp, num_ranges=nr)
+
+
+@pytest.mark.parametrize("pt", [64, 128, 256])
+def test_page_sizes(pt):
+    print(f"[mla] page_tokens={pt}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=2, heads=32, ctx_lens=[pt + 5, 3 * pt],
+                                      page_tokens=pt)
+    check_latent(inp)
+
+
+def test_full_pipeline_matches_absorbed_and_expanded_oracles():
+    print("[mla] full absorbed pipeline", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=2, heads=32, ctx_lens=[500, 130])
+    w_uk, w_uv_t = ops.split_kv_b(inp.kv_b, 32, inp.dn, inp.dv)
+    out = ops.mla_absorbed_decode(inp.q_nope, inp.q_rope, inp.lat_pool, inp.block_table,
+                                  inp.ctx_lens, w_uk, w_uv_t, scale=inp.scale)
+    torch.cuda.synchronize()
+    kv_b = inp.kv_b.float().cpu().numpy()
+    for b in range(2):
+        lat = synthetic.mla_logical_latent(inp, b)
+        qn = inp.q_nope[b:b + 1, :, None].float().cpu().numpy()
+        qr = inp.q_rope[b:b + 1, :, None].float().cpu().numpy()
+        S = lat.shape[0]
+        ref_bf, _ = omla.absorbed(qn, qr, lat[None], kv_b, inp.dn, inp.dv, offset=S - 1,
+                                  bf16=True)
+        ref_exp = omla.expanded(qn, qr, lat[None, :, :512], lat[None, :, 512:], kv_b, inp.dn,
+                                inp.dv, offset=S - 1)
+        got = out[b].float().cpu().numpy()
+        np.testing.assert_allclose(got, ref_bf[0, :, 0], atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(got, ref_exp[0, :, 0], atol=ATOL, rtol=RTOL)
+
+
+def test_paging_invariance_is_bitwise():
+    print("[mla] paging invariance", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=2, heads=32, ctx_lens=[700, 333], slack_pages=7)
+    q_lat, _, _ = q_lat_of(inp)
+    a = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                              scale=inp.scale)
+    slots = inp.lat_pool.shape[0]
+    perm = torch.from_numpy(np.random.default_rng(5).permutation(slots)).cuda()
+    inv = torch.argsort(perm)
+    pool2 = inp.lat_pool[perm].contiguous()
+    table2 = inv[inp.block_table.long()].to(torch.int32).contiguous()
+    b2 = ops.mla_latent_decode(q_lat, pool2, table2, inp.ctx_lens, scale=inp.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b2)
+
+
+def test_config5_full_size_two_sequences():
+    print("[mla] config 5 full size", flush=True)
+    inp = synthetic.mla_decode_inputs()
+    check_latent(inp, batches=[0, 7])

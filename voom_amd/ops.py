@@ -239,3 +239,72 @@ def byteplane_merge_slots(lo: torch.Tensor, hi: torch.Tensor, pool: torch.Tensor
 def slot_codec_supported(pool: torch.Tensor) -> bool:
     """True when one pool slot is a whole number of 64-byte lines (slot kernels)."""
     return (pool[0].numel() * 2) % 64 == 0
+
+
+def mla_workspace_bytes(batch: int, num_heads: int, num_ranges: int = 0) -> int:
+    return int(_lib.lib().voom_mla_workspace_bytes(batch, num_heads, num_ranges))
+
+
+def mla_latent_decode(q_lat: torch.Tensor, lat_pool: torch.Tensor, block_table: torch.Tensor,
+                      ctx_lens: torch.Tensor, *, scale: float, out: torch.Tensor | None = None,
+                      return_lse: bool = False, num_ranges: int = 0,
+                      ws: torch.Tensor | None = None, stream: torch.cuda.Stream | None = None):
+    """Latent contraction of absorbed MLA over a paged latent cache.
+
+    q_lat [B, H, 576] bf16; lat_pool [slots, page_tokens, 576] bf16;
+    block_table [B, max_pages] int32; ctx_lens [B] int32.  Returns
+    weighted_c [B, H, 512] bf16 (runtime/glm.py:133-164, dense path).
+    """
+    dev = _require_device(q_lat, lat_pool, block_table, ctx_lens, out)
+    _require(q_lat.dim() == 3 and lat_pool.dim() == 3, "q_lat [B,H,576], lat_pool [slots,PT,576]")
+    B, H, LD = q_lat.shape
+    slots, PT, LD2 = lat_pool.shape
+    _require(LD == LD2 == 576, "latent width must be 576 (512 + 64)")
+    _require(q_lat.dtype == lat_pool.dtype == torch.bfloat16, "q_lat and lat_pool must be bf16")
+    _require(block_table.dtype == torch.int32 and ctx_lens.dtype == torch.int32,
+             "block_table and ctx_lens must be int32")
+    _require(block_table.dim() == 2 and block_table.shape[0] == B and tuple(ctx_lens.shape) == (B,),
+             "block_table [B, max_pages], ctx_lens [B]")
+    need = mla_workspace_bytes(B, H, num_ranges)
+    if ws is None:
+        ws = workspace(dev, need, tag=2)
+    _require(ws.numel() * ws.element_size() >= need, "workspace too small")
+    if out is None:
+        out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, H), dtype=torch.float32, device=dev) if return_lse else None
+    _lib.call("voom_mla_absorbed_decode", _ptr(q_lat), _ptr(lat_pool), _ptr(block_table),
+              _ptr(ctx_lens), _ptr(out), _ptr(lse), _ptr(ws), need, B, H, LD, 512, PT,
+              block_table.shape[1], slots, float(scale), int(num_ranges), _stream(stream))
+    return (out, lse) if return_lse else out
+
+
+def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
+    """kv_b_proj weight [H*(dn+dv), C] -> (W_UK [H, dn, C], W_UV^T [H, C, dv]), contiguous.
+
+    The split of runtime/glm.py:124-125; W_UV is pre-transposed once so the
+    output projection is a plain batched product.
+    """
+    C = kv_b.shape[-1]
+    w = kv_b.reshape(num_heads, dn + dv, C)
+    return w[:, :dn, :].contiguous(), w[:, dn:, :].transpose(1, 2).contiguous()
+
+
+def mla_absorbed_decode(q_nope: torch.Tensor, q_rope: torch.Tensor, lat_pool: torch.Tensor,
+                        block_table: torch.Tensor, ctx_lens: torch.Tensor, w_uk: torch.Tensor,
+                        w_uv_t: torch.Tensor, *, scale: float, num_ranges: int = 0,
+                        return_weighted_c: bool = False):
+    """Absorbed MLA decode of one query token: runtime/glm.py:78-202.
+
+    q_nope [B, H, dn], q_rope [B, H, 64] bf16; W_UK [H, dn, 512] and W_UV^T
+    [H, 512, dv] from split_kv_b.  q_nope . W_UK and weighted_c . W_UV run
+    as batched GEMMs (hipBLASLt through torch); the latent contraction runs in
+    the HIP kernel.  Returns the per-head output [B, H, dv] bf16 (before o_proj).
+    """
+    B, H, dn = q_nope.shape
+    # [H, B, dn] @ [H, dn, C] -> [H, B, C]; both operands contiguous.
+    q_abs = torch.bmm(q_nope.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
+    q_lat = torch.cat([q_abs, q_rope], dim=-1).contiguous()
+    wc = mla_latent_decode(q_lat, lat_pool, block_table, ctx_lens, scale=scale,
+                           num_ranges=num_ranges)
+    out = torch.bmm(wc.transpose(0, 1).contiguous(), w_uv_t).transpose(0, 1).contiguous()
+    return (out, wc) if return_weighted_c else out

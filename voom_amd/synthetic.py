@@ -125,3 +125,72 @@ def to_reference_layout(inp: PagedGQAInputs):
     v = inp.v_pool.transpose(2, 3).float().cpu().numpy()
     q = inp.q.float().cpu().numpy()
     return q, k, v
+
+
+@dataclass
+class MLAInputs:
+    q_nope: torch.Tensor       # [B, H, dn] bf16
+    q_rope: torch.Tensor       # [B, H, 64] bf16
+    lat_pool: torch.Tensor     # [slots, PT, 576] bf16
+    block_table: torch.Tensor  # [B, max_pages] int32
+    ctx_lens: torch.Tensor     # [B] int32
+    kv_b: torch.Tensor         # [H*(dn+dv), 512] bf16
+    ctx_host: np.ndarray
+    table_host: np.ndarray
+    dn: int
+    dv: int
+    scale: float
+    page_tokens: int
+
+    def latent_bytes(self) -> int:
+        return int(self.ctx_host.sum()) * 576 * 2
+
+    def latent_flops(self) -> int:
+        H = self.q_nope.shape[1]
+        return int(self.ctx_host.sum()) * H * (2 * 576 + 2 * 512)
+
+
+def mla_decode_inputs(*, batch: int = 8, heads: int = 128, ctx: int = 16384, ctx_lens=None,
+                      page_tokens: int = 64, dn: int = 128, dv: int = 128, slack_pages: int = 0,
+                      device="cuda", seed: int = 8) -> MLAInputs:
+    """Config 5: GLM/DeepSeek absorbed-MLA decode, latent [c_kv 512 | k_rope 64]
+    ~ N(0,1) bf16 in 64-token pages at seeded-random slots; q_nope, q_rope
+    ~ N(0,1); kv_b ~ N(0, 0.02) (dn = dv = 128 as in DeepSeek-V3); scale
+    (dn + 64)^-0.5."""
+    dev = torch.device(device)
+    ctx_arr = np.full(batch, ctx, dtype=np.int64) if ctx_lens is None else \
+        np.asarray(ctx_lens, dtype=np.int64)
+    batch = len(ctx_arr)
+    pages_per = -(-ctx_arr // page_tokens)
+    slots = max(1, int(pages_per.sum()) + slack_pages)
+    max_pages = max(1, int(pages_per.max()) if batch else 1)
+    perm = np.random.default_rng(seed + 1).permutation(slots)
+    table = np.zeros((batch, max_pages), dtype=np.int32)
+    cur = 0
+    for b in range(batch):
+        n = int(pages_per[b])
+        table[b, :n] = perm[cur:cur + n]
+        cur += n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    lat = torch.empty((slots, page_tokens, 576), dtype=torch.bfloat16, device=dev)
+    for s0 in range(0, slots, 512):
+        s1 = min(slots, s0 + 512)
+        lat[s0:s1] = torch.randn((s1 - s0, page_tokens, 576), generator=gen, device=dev)
+    q_nope = torch.randn((batch, heads, dn), generator=gen, device=dev).to(torch.bfloat16)
+    q_rope = torch.randn((batch, heads, 64), generator=gen, device=dev).to(torch.bfloat16)
+    kv_b = (torch.randn((heads * (dn + dv), 512), generator=gen, device=dev) * 0.02).to(
+        torch.bfloat16)
+    return MLAInputs(q_nope=q_nope, q_rope=q_rope, lat_pool=lat,
+                     block_table=torch.from_numpy(table).to(dev),
+                     ctx_lens=torch.from_numpy(ctx_arr.astype(np.int32)).to(dev), kv_b=kv_b,
+                     ctx_host=ctx_arr, table_host=table, dn=dn, dv=dv,
+                     scale=(dn + 64) ** -0.5, page_tokens=page_tokens)
+
+
+def mla_logical_latent(inp: MLAInputs, b: int) -> np.ndarray:
+    """Host fp32 latent rows [ctx_b, 576] of sequence b in logical order."""
+    n = -(-int(inp.ctx_host[b]) // inp.page_tokens)
+    ids = torch.from_numpy(inp.table_host[b, :n].astype(np.int64)).to(inp.lat_pool.device)
+    rows = inp.lat_pool[ids].reshape(-1, 576)[: int(inp.ctx_host[b])]
+    return rows.float().cpu().numpy()
