@@ -396,15 +396,100 @@ def bench_long_context(steps: int, cpu_sample: bool) -> dict:
     return res
 
 
+def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
+    """Config 5: absorbed-MLA paged decode, B=8, H=128, ctx 16384, latent 512+64.
+
+    Four input sets (4 x 151 MB > 512 MB) rotate so the 256 MB Infinity Cache
+    cannot hold the working set; the latent kernel (+ its reduce) is timed
+    with HIP events, the absorption GEMMs separately.
+    """
+    import numpy as np
+    import torch
+
+    from voom_amd import ops, synthetic
+
+    log("config 5: building 4 rotating input sets (B=8, H=128, ctx 16384, latent 576)")
+    sets = [synthetic.mla_decode_inputs(seed=8 + 100 * i) for i in range(4)]
+    inp = sets[0]
+    w_uk, w_uv_t = ops.split_kv_b(inp.kv_b, 128, inp.dn, inp.dv)
+    q_lats = []
+    for s_ in sets:
+        q_abs = torch.bmm(s_.q_nope.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
+        q_lats.append(torch.cat([q_abs, s_.q_rope], -1).contiguous())
+    out = torch.empty((8, 128, 512), dtype=torch.bfloat16, device="cuda")
+    ws = ops.workspace(inp.q_nope.device, ops.mla_workspace_bytes(8, 128, 0), tag=8)
+
+    def step(i):
+        s_ = sets[i % 4]
+        ops.mla_latent_decode(q_lats[i % 4], s_.lat_pool, s_.block_table, s_.ctx_lens,
+                              scale=s_.scale, out=out, ws=ws)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / steps / 1e3
+    nbytes = inp.latent_bytes() + 8 * 128 * 576 * 2 + 8 * 128 * 512 * 2
+    flops = inp.latent_flops()
+    # absorption GEMMs (q_nope . W_UK, weighted_c . W_UV) on their own
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record()
+    for i in range(steps):
+        q_abs = torch.bmm(inp.q_nope.transpose(0, 1).contiguous(), w_uk)
+        torch.bmm(out.transpose(0, 1).contiguous(), w_uv_t)
+    g1.record()
+    torch.cuda.synchronize()
+    t_gemm = g0.elapsed_time(g1) / steps / 1e3
+    res = {
+        "workload": "config 5: absorbed MLA decode, B=8, H=128, ctx 16384, latent 512+64 bf16 "
+                    "in 64-token pages, 4 rotating input sets",
+        "latent_kernel_us": t * 1e6,
+        "hbm_gbs": nbytes / t / 1e9,
+        "hbm_frac": nbytes / t / 1e9 / HBM_PEAK_GBS,
+        "mfma_tflops": flops / t / 1e12,
+        "mfma_frac_bf16_dense": flops / t / 1e12 / 2500.0,
+        "bytes_per_call": nbytes,
+        "flops_per_call": flops,
+        "absorption_gemms_us": t_gemm * 1e6,
+    }
+    log(f"config 5: latent kernel {t * 1e6:.1f} us, {res['hbm_gbs']:.0f} GB/s "
+        f"({100 * res['hbm_frac']:.1f}% HBM), {res['mfma_tflops']:.0f} TFLOP/s; "
+        f"absorption GEMMs {t_gemm * 1e6:.1f} us")
+    if cpu_sample:
+        from oracle import mla as omla
+
+        lat = synthetic.mla_logical_latent(inp, 0)
+        ql = q_lats[0][0:1, :, None, :].float().cpu().numpy()
+        t0 = time.perf_counter()
+        ref = omla.absorbed_weighted_c(ql, lat[None], 64, inp.scale, bf16=True)
+        dt = time.perf_counter() - t0
+        step(0)
+        torch.cuda.synchronize()
+        err = float(np.abs(out[0].float().cpu().numpy() - ref[0, :, 0]).max())
+        res["cpu_baseline"] = {"value": lat.nbytes / 2 / dt / 1e9, "unit": "GB/s (bf16 latent)",
+                               "cores": cpu_threads(), "kind": "port",
+                               "sample": "latent contraction of sequence 0 (16384 tokens, "
+                                         "128 heads), numpy, oracle/mla.py"}
+        res["parity_max_abs_err_vs_oracle"] = err
+    del sets
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="gqa,spill,long",
+    ap.add_argument("--only", default="gqa,spill,long,mla",
                     help="comma list of legs: gqa (config 2, headline), spill (config 3), "
-                         "long (config 4)")
+                         "long (config 4), mla (config 5)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a known-size 1 GiB streaming kernel (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -456,6 +541,8 @@ def main() -> int:
         line["reload_gbs"] = round(extra["spill_reload"]["reload_gbs"], 2)
     if "long" in legs:
         extra["long_context"] = bench_long_context(64, cpu_sample=not args.no_cpu)
+    if "mla" in legs:
+        extra["mla"] = bench_mla(args.steps, args.warmup, cpu_sample=not args.no_cpu)
     if extra:
         line["other_configs"] = extra
     print(json.dumps(line), flush=True)

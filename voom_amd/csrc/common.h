@@ -56,6 +56,13 @@ __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
 // Marks a wave-uniform value as such (v_readfirstlane_b32 into an SGPR).
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// operations, then s_barrier.  Unlike __syncthreads() it does not drain
+// outstanding global loads, so register prefetches stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Hardware base-2 exponential (v_exp_f32).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -15,15 +15,18 @@
 // Decomposition: one workgroup (4 wavefronts) per (sequence, token range,
 // group of 32 heads).  The four head groups of a range are placed on the same
 // XCD so the latent tiles they all read are served from that XCD's L2.
-// Per 64-token tile: the tile is staged in LDS (register prefetch of the next
-// tile overlaps the current one's math); wavefront w computes the scores of
-// tokens 16w..16w+15 for all 32 heads, the page maximum is combined through
-// LDS, P is written to LDS in bf16, and wavefront w accumulates dims
-// 128w..128w+127 of out^T for all 32 heads (accumulators stay in registers
-// for the whole range).  The C^T operand is read from the token-major tile
-// with 16-bit LDS reads; lane group g takes tokens g, g+4, ..., g+28 of a
-// 32-token step, which keeps those reads free of bank conflicts, and P is
-// stored in the same token order so its operand is one 16-byte read.
+// Per 64-token tile: buffer loads deliver the tile straight into LDS (no
+// register staging; the next tile streams into the second buffer while the
+// current one is used); wavefront w computes the scores of tokens
+// 16w..16w+15 for all 32 heads, the tile maximum is combined through LDS, P
+// is written to LDS in bf16, and wavefront w accumulates dims 128w..128w+127
+// of out^T for all 32 heads (accumulators stay in registers for the whole
+// range).  The C^T operand comes from the token-major tile through
+// ds_read_b64_tr_b16: in each 16-lane group, lane l receives element l%4 of
+// the 8-byte rows addressed by lanes 4c + l/4 (c = 0..3), so two transposed
+// reads give a lane the 8 tokens of one latent dim.  LDS rows are padded to
+// 73 sixteen-byte chunks, which spreads both the row reads of the score MFMA
+// and the transposed reads over all banks.
 #include "common.h"
 
 namespace voom {
@@ -34,16 +37,16 @@ constexpr int kLat = 576;          // kv_lora_rank 512 + rope dim 64
 constexpr int kC = 512;
 constexpr int kHeadsPerGroup = 32;
 constexpr int kTile = 64;          // tokens per tile
-constexpr int kRow = kLat + 8;     // LDS row stride in bf16 elements (1168 B, 16 B aligned)
 constexpr int kChunksPerRow = kLat * 2 / 16;  // 72 sixteen-byte chunks per token
-constexpr int kChunksPerThread = kTile * kChunksPerRow / kThreads;  // 18
+constexpr int kRowChunks = kChunksPerRow + 1;  // padded LDS row: 73 chunks = 1168 B
+constexpr int kRow = kRowChunks * 8;           // LDS row stride in bf16 elements
+constexpr int kTileChunks = kTile * kRowChunks;  // 4672 = 73 x 64
+constexpr int kLoadsPerTile = kTileChunks / 64;  // 73 wave-wide 16-byte loads
 constexpr int kQSteps = kLat / 32;  // 18 k-steps of the score MFMA
 
-__device__ __forceinline__ int perm_pos(int t) {
-  // Position of token t (0..31 within a 32-token step) in the P row: token
-  // 4e+g is stored at 8g+e, so lane group g reads its 8 tokens contiguously.
-  return 8 * (t & 3) + (t >> 2);
-}
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
 struct MlaArgs {
   const uint16_t* __restrict__ q;        // [B, H, 576]
@@ -57,7 +60,8 @@ struct MlaArgs {
 };
 
 __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[kTile * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t tile_a[kTile * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t tile_b[kTile * kRow];
   __shared__ __attribute__((aligned(16))) uint16_t p_lds[kHeadsPerGroup * kTile];
   __shared__ float pmax[4][kHeadsPerGroup];
   __shared__ float psum[4][kHeadsPerGroup];
@@ -85,10 +89,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
   }
   const int b = task / a.NR;
   const int range = task - b * a.NR;
-  const int tiles_per_page = 1 << (a.pt_shift - 6);
   int ctx = a.ctx_lens[b];
   const int cap = a.max_pages << a.pt_shift;
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  ctx = uniform(ctx < 0 ? 0 : (ctx > cap ? cap : ctx));
   const int n_tiles = (ctx + kTile - 1) / kTile;
   const int per = (n_tiles + a.NR - 1) / a.NR;
   const int t_lo = range * per;
@@ -117,43 +120,57 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
   float m_run[2] = {-INFINITY, -INFINITY};  // per head tile: head 16ht + i16
   float l_run[2] = {0.f, 0.f};
 
-  auto tile_base = [&](int t) -> const uint16_t* {
-    const int page = t / tiles_per_page;
-    const int sub = t - page * tiles_per_page;
-    int slot = trow[page];
+  // Lane-constant source offsets of this wave's direct-to-LDS loads: load i
+  // (i = w, w+4, ...) fills LDS chunks 64i..64i+63 of the padded tile; chunk
+  // (row, col) holds bytes 16*col of token row; the padding chunk of a row
+  // reads past the buffer end and lands as zeros.
+  int src_off[(kLoadsPerTile + 3) / 4];
+#pragma unroll
+  for (int k = 0; k < (kLoadsPerTile + 3) / 4; ++k) {
+    const int j = 64 * (w + 4 * k) + lane;
+    const int row = j / kRowChunks;
+    const int col = j - row * kRowChunks;
+    src_off[k] = col < kChunksPerRow ? (row * kChunksPerRow + col) * 16 : 0x40000000;
+  }
+
+  // Issues the loads of tile t into LDS buffer `buf`; tokens at or past the
+  // context end read as zeros (the descriptor covers only valid rows).
+  // Block-table entries of the range's pages, one per lane, refreshed every 64
+  // pages: slot lookups inside the loop are register reads, not memory trips.
+  const int tile_shift = a.pt_shift - 6;
+  int tab_base = -(1 << 30);
+  int tab = 0;
+  auto load_tile = [&](int t, uint16_t* dst) {
+    const int page = t >> tile_shift;
+    const int sub = t - (page << tile_shift);
+    if (page >= tab_base + 64) {
+      tab_base = page;
+      tab = tab_base + lane < a.max_pages ? trow[tab_base + lane] : 0;
+    }
+    int slot = __builtin_amdgcn_readlane(tab, page - tab_base);
     if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
-    return a.lat + ((static_cast<size_t>(slot) << a.pt_shift) + sub * kTile) * kLat;
-  };
-
-  u32x4 pre[kChunksPerThread];
-  auto prefetch = [&](int t) {
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(tile_base(t)),
-                                          static_cast<short>(0), kTile * kLat * 2, 0x00020000);
+    const uint16_t* base = a.lat + ((static_cast<size_t>(slot) << a.pt_shift) + sub * kTile) * kLat;
+    int valid = ctx - t * kTile;
+    valid = valid > kTile ? kTile : valid;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(base), static_cast<short>(0), valid * kLat * 2, 0x00020000);
 #pragma unroll
-    for (int k = 0; k < kChunksPerThread; ++k) {
-      pre[k] = __builtin_amdgcn_raw_buffer_load_b128(r, (tid + kThreads * k) * 16, 0, 0);
-    }
-  };
-  auto stage = [&](int t) {
-    const int valid = ctx - t * kTile;
-#pragma unroll
-    for (int k = 0; k < kChunksPerThread; ++k) {
-      const int c = tid + kThreads * k;
-      const int tok = c / kChunksPerRow;
-      const int col = c - tok * kChunksPerRow;
-      u32x4 v = pre[k];
-      if (tok >= valid) v = u32x4{0u, 0u, 0u, 0u};  // tokens past the context
-      *reinterpret_cast<u32x4*>(tile + tok * kRow + col * 8) = v;
+    for (int k = 0; k < (kLoadsPerTile + 3) / 4; ++k) {
+      const int i = w + 4 * k;
+      if (i < kLoadsPerTile) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + i * 64 * 8), 16,
+                                                 src_off[k], 0, 0, 0);
+      }
     }
   };
 
-  if (t_lo < t_hi) prefetch(t_lo);
-  for (int t = t_lo; t < t_hi; ++t) {
-    __syncthreads();  // previous tile fully consumed
-    stage(t);
-    if (t + 1 < t_hi) prefetch(t + 1);
-    __syncthreads();
+  // One tile of work on LDS buffer `tile` while tile t+1 streams into `next`.
+  auto step = [&](int t, const uint16_t* tile, uint16_t* next) {
+    // This wave's loads of tile t have landed; after the barrier every wave's
+    // have, and every wave is done with the other buffer (tile t-1).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    if (t + 1 < t_hi) load_tile(t + 1, next);
 
     // ---- scores: tokens 16w..16w+15 x 32 heads ----
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -181,7 +198,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
       mx = wave_max_across_groups(mx);
       if (g == 0) pmax[w][16 * ht + i16] = mx;
     }
-    __syncthreads();
+    lds_barrier();
 
     float alpha[2];
 #pragma unroll
@@ -191,19 +208,19 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
       const float mn = fmaxf(m_run[ht], mp);
       alpha[ht] = fast_exp2(m_run[ht] - mn);
       m_run[ht] = mn;
-      float ps = 0.f;
+      float p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = fast_exp2(x[ht][r] - mn);
-        const uint16_t pb = f2bf(p);
-        ps += bf2f(pb);
-        const int tok = 16 * w + 4 * g + r;  // 0..63
-        p_lds[hh * kTile + 32 * (tok >> 5) + perm_pos(tok & 31)] = pb;
-      }
+      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(x[ht][r] - mn);
+      const uint32_t w0 = pack_bf16x2(p[0], p[1]);
+      const uint32_t w1 = pack_bf16x2(p[2], p[3]);
+      // P row of head hh: tokens 16w+4g .. +3 in natural order
+      *reinterpret_cast<u32x2*>(p_lds + hh * kTile + 16 * w + 4 * g) = u32x2{w0, w1};
+      float ps = __builtin_bit_cast(float, w0 << 16) + __builtin_bit_cast(float, w0 & 0xffff0000u) +
+                 __builtin_bit_cast(float, w1 << 16) + __builtin_bit_cast(float, w1 & 0xffff0000u);
       ps = wave_sum_across_groups(ps);
       if (g == 0) psum[w][hh] = ps;
     }
-    __syncthreads();
+    lds_barrier();
 
 #pragma unroll
     for (int ht = 0; ht < 2; ++ht) {
@@ -217,28 +234,37 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
       acc[dt][0] *= alpha[0];
       acc[dt][1] *= alpha[1];
     }
+    // Transposed-read addresses: lane k of a 16-lane group supplies token row
+    // 8g + (k/4) (+4 for the second read) at dims 4*(k%4) of the dim tile.
+    const int trow_tok = 8 * g + (i16 >> 2);
+    const int tcol = 4 * (i16 & 3);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const bf16x8 pb0 = __builtin_bit_cast(
           bf16x8, *reinterpret_cast<const u32x4*>(p_lds + i16 * kTile + 32 * ks + 8 * g));
       const bf16x8 pb1 = __builtin_bit_cast(
           bf16x8, *reinterpret_cast<const u32x4*>(p_lds + (16 + i16) * kTile + 32 * ks + 8 * g));
+      const uint16_t* trb = tile + (32 * ks + trow_tok) * kRow + 128 * w + tcol;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const int dim = 128 * w + 16 * dt + i16;
-        const uint16_t* col = tile + (32 * ks + g) * kRow + dim;
-        u32x4 cv;
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const uint32_t lo = col[(8 * e2) * kRow];      // token 32ks + 4(2e2) + g
-          const uint32_t hi = col[(8 * e2 + 4) * kRow];  // token 32ks + 4(2e2+1) + g
-          cv[e2] = lo | (hi << 16);
-        }
-        const bf16x8 av = __builtin_bit_cast(bf16x8, cv);
+        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4*)(trb + 16 * dt));
+        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (lds_bf16x4*)(trb + 4 * kRow + 16 * dt));
+        const bf16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb0, acc[dt][0], 0, 0, 0);
         acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb1, acc[dt][1], 0, 0, 0);
       }
     }
+  };
+
+  // The two buffers are distinct LDS objects and the loop is unrolled by two,
+  // so every LDS read provably misses the buffer being filled and the loads
+  // of the next tile stay in flight across the current tile's reads.
+  if (t_lo < t_hi) load_tile(t_lo, tile_a);
+  for (int t = t_lo; t < t_hi; t += 2) {
+    step(t, tile_a, tile_b);
+    if (t + 1 < t_hi) step(t + 1, tile_b, tile_a);
   }
 
   // ---- partial state of this (sequence, range, head group) ----
