@@ -12,16 +12,15 @@
 // 128 heads share one latent row, so the contraction is MFMA work:
 //   scores^T [tokens x heads] = Lat [tokens x 576] . Q^T      v_mfma_f32_16x16x32_bf16
 //   out^T    [dims x heads]  += C^T [dims x tokens] . P^T     v_mfma_f32_16x16x32_bf16
-// Decomposition: one workgroup (4 wavefronts) per (sequence, token range,
-// group of 32 heads).  The four head groups of a range are placed on the same
+// Decomposition: one workgroup (8 wavefronts, 2 per SIMD) per (sequence,
+// token range, group of 32 heads).  The four head groups of a range are placed on the same
 // XCD so the latent tiles they all read are served from that XCD's L2.
 // Per 64-token tile: buffer loads deliver the tile straight into LDS (no
 // register staging; the next tile streams into the second buffer while the
-// current one is used); wavefront w computes the scores of tokens
-// 16w..16w+15 for all 32 heads, the tile maximum is combined through LDS, P
-// is written to LDS in bf16, and wavefront w accumulates dims 128w..128w+127
-// of out^T for all 32 heads (accumulators stay in registers for the whole
-// range).  The C^T operand comes from the token-major tile through
+// current one is used); wavefront w computes the scores of token tile w%4
+// for head tile w/4, the tile maximum is combined through LDS, P is written
+// to LDS in bf16, and wavefront w accumulates dims 64w..64w+63 of out^T for
+// all 32 heads (accumulators stay in registers for the whole range).  The C^T operand comes from the token-major tile through
 // ds_read_b64_tr_b16: in each 16-lane group, lane l receives element l%4 of
 // the 8-byte rows addressed by lanes 4c + l/4 (c = 0..3), so two transposed
 // reads give a lane the 8 tokens of one latent dim.  LDS rows are padded to
@@ -43,6 +42,8 @@ constexpr int kRow = kRowChunks * 8;           // LDS row stride in bf16 element
 constexpr int kTileChunks = kTile * kRowChunks;  // 4672 = 73 x 64
 constexpr int kLoadsPerTile = kTileChunks / 64;  // 73 wave-wide 16-byte loads
 constexpr int kQSteps = kLat / 32;  // 18 k-steps of the score MFMA
+constexpr int kPRow = kTile + 8;    // P row stride (144 B): the 16 head rows of a lane
+                                    // group start on 16 different 4-bank groups
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -59,16 +60,22 @@ struct MlaArgs {
   float scale_log2e;
 };
 
-__global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
+constexpr int kMlaThreads = 512;  // 8 wavefronts, 2 per SIMD
+constexpr int kMlaWaves = kMlaThreads / 64;
+constexpr int kLoadsPerWave = (kLoadsPerTile + kMlaWaves - 1) / kMlaWaves;
+
+__global__ __launch_bounds__(kMlaThreads, 2) void mla_latent_kernel(MlaArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t tile_a[kTile * kRow];
   __shared__ __attribute__((aligned(16))) uint16_t tile_b[kTile * kRow];
-  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kHeadsPerGroup * kTile];
+  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kHeadsPerGroup * kPRow];
   __shared__ float pmax[4][kHeadsPerGroup];
   __shared__ float psum[4][kHeadsPerGroup];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = uniform(tid >> 6);
+  const int w = uniform(tid >> 6);   // 0..7
+  const int tt = w & 3;              // score MFMA: token tile (16 tokens)
+  const int qt = w >> 2;             // score MFMA: head tile (16 heads)
   const int i16 = lane & 15;
   const int g = lane >> 4;
   const int NHG = a.H / kHeadsPerGroup;
@@ -99,21 +106,20 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
   const int head0 = hg * kHeadsPerGroup;
   const int32_t* trow = a.table + static_cast<size_t>(b) * a.max_pages;
 
-  // Q^T operands for both head tiles, all 18 k-steps: lane (head i16, group g)
-  // holds q[head][32s + 8g .. +8].
-  u32x4 qop[2][kQSteps];
-#pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
-    const uint16_t* qh = a.q + (static_cast<size_t>(b) * a.H + head0 + 16 * ht + i16) * kLat;
+  // Q^T operand of this wave's head tile, all 18 k-steps: lane (head i16,
+  // group g) holds q[head][32s + 8g .. +8].
+  u32x4 qop[kQSteps];
+  {
+    const uint16_t* qh = a.q + (static_cast<size_t>(b) * a.H + head0 + 16 * qt + i16) * kLat;
 #pragma unroll
     for (int s = 0; s < kQSteps; ++s) {
-      qop[ht][s] = *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g);
+      qop[s] = *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g);
     }
   }
 
-  f32x4 acc[8][2];
+  f32x4 acc[4][2];  // out^T tiles: dims 64w + 16dt.., head tile ht
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
+  for (int dt = 0; dt < 4; ++dt) {
     acc[dt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     acc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -121,25 +127,25 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
   float l_run[2] = {0.f, 0.f};
 
   // Lane-constant source offsets of this wave's direct-to-LDS loads: load i
-  // (i = w, w+4, ...) fills LDS chunks 64i..64i+63 of the padded tile; chunk
+  // (i = w, w+8, ...) fills LDS chunks 64i..64i+63 of the padded tile; chunk
   // (row, col) holds bytes 16*col of token row; the padding chunk of a row
   // reads past the buffer end and lands as zeros.
-  int src_off[(kLoadsPerTile + 3) / 4];
+  int src_off[kLoadsPerWave];
 #pragma unroll
-  for (int k = 0; k < (kLoadsPerTile + 3) / 4; ++k) {
-    const int j = 64 * (w + 4 * k) + lane;
+  for (int k = 0; k < kLoadsPerWave; ++k) {
+    const int j = 64 * (w + kMlaWaves * k) + lane;
     const int row = j / kRowChunks;
     const int col = j - row * kRowChunks;
     src_off[k] = col < kChunksPerRow ? (row * kChunksPerRow + col) * 16 : 0x40000000;
   }
 
-  // Issues the loads of tile t into LDS buffer `buf`; tokens at or past the
-  // context end read as zeros (the descriptor covers only valid rows).
   // Block-table entries of the range's pages, one per lane, refreshed every 64
   // pages: slot lookups inside the loop are register reads, not memory trips.
   const int tile_shift = a.pt_shift - 6;
   int tab_base = -(1 << 30);
   int tab = 0;
+  // Issues the loads of tile t into LDS buffer dst; tokens at or past the
+  // context end read as zeros (the descriptor covers only valid rows).
   auto load_tile = [&](int t, uint16_t* dst) {
     const int page = t >> tile_shift;
     const int sub = t - (page << tile_shift);
@@ -155,8 +161,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(base), static_cast<short>(0), valid * kLat * 2, 0x00020000);
 #pragma unroll
-    for (int k = 0; k < (kLoadsPerTile + 3) / 4; ++k) {
-      const int i = w + 4 * k;
+    for (int k = 0; k < kLoadsPerWave; ++k) {
+      const int i = w + kMlaWaves * k;
       if (i < kLoadsPerTile) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + i * 64 * 8), 16,
                                                  src_off[k], 0, 0, 0);
@@ -172,31 +178,26 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
     lds_barrier();
     if (t + 1 < t_hi) load_tile(t + 1, next);
 
-    // ---- scores: tokens 16w..16w+15 x 32 heads ----
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-    const uint16_t* arow = tile + (16 * w + i16) * kRow + 8 * g;
+    // ---- scores: tokens 16tt..16tt+15 x heads 16qt..16qt+15 ----
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+    const uint16_t* arow = tile + (16 * tt + i16) * kRow + 8 * g;
 #pragma unroll
     for (int s = 0; s < kQSteps; ++s) {
       const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(arow + 32 * s));
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, qop[0][s]), s0,
-                                                   0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, qop[1][s]), s1,
-                                                   0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, qop[s]), sc, 0,
+                                                   0, 0);
     }
-    // lane (head i16, group g) holds tokens 16w + 4g + r, r = 0..3
+    // lane (head 16qt + i16, group g) holds tokens 16tt + 4g + r, r = 0..3
     const int valid = ctx - t * kTile;
-    float x[2][4];
+    float x[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const bool ok = 16 * w + 4 * g + r < valid;
-      x[0][r] = ok ? s0[r] * a.scale_log2e : -INFINITY;
-      x[1][r] = ok ? s1[r] * a.scale_log2e : -INFINITY;
+      x[r] = 16 * tt + 4 * g + r < valid ? sc[r] * a.scale_log2e : -INFINITY;
     }
-#pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
-      float mx = fmaxf(fmaxf(x[ht][0], x[ht][1]), fmaxf(x[ht][2], x[ht][3]));
+    {
+      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
       mx = wave_max_across_groups(mx);
-      if (g == 0) pmax[w][16 * ht + i16] = mx;
+      if (g == 0) pmax[tt][16 * qt + i16] = mx;
     }
     lds_barrier();
 
@@ -208,17 +209,21 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
       const float mn = fmaxf(m_run[ht], mp);
       alpha[ht] = fast_exp2(m_run[ht] - mn);
       m_run[ht] = mn;
+    }
+    {
+      const int hh = 16 * qt + i16;
+      const float mn = m_run[qt];
       float p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(x[ht][r] - mn);
+      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(x[r] - mn);
       const uint32_t w0 = pack_bf16x2(p[0], p[1]);
       const uint32_t w1 = pack_bf16x2(p[2], p[3]);
-      // P row of head hh: tokens 16w+4g .. +3 in natural order
-      *reinterpret_cast<u32x2*>(p_lds + hh * kTile + 16 * w + 4 * g) = u32x2{w0, w1};
+      // P row of head hh: tokens 16tt+4g .. +3 in natural order
+      *reinterpret_cast<u32x2*>(p_lds + hh * kPRow + 16 * tt + 4 * g) = u32x2{w0, w1};
       float ps = __builtin_bit_cast(float, w0 << 16) + __builtin_bit_cast(float, w0 & 0xffff0000u) +
                  __builtin_bit_cast(float, w1 << 16) + __builtin_bit_cast(float, w1 & 0xffff0000u);
       ps = wave_sum_across_groups(ps);
-      if (g == 0) psum[w][hh] = ps;
+      if (g == 0) psum[tt][hh] = ps;
     }
     lds_barrier();
 
@@ -228,9 +233,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
       l_run[ht] = l_run[ht] * alpha[ht] + (psum[0][hh] + psum[1][hh] + psum[2][hh] + psum[3][hh]);
     }
 
-    // ---- out^T[dims 128w.., heads] += C^T . P^T ----
+    // ---- out^T[dims 64w.., heads] += C^T . P^T ----
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < 4; ++dt) {
       acc[dt][0] *= alpha[0];
       acc[dt][1] *= alpha[1];
     }
@@ -241,12 +246,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const bf16x8 pb0 = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(p_lds + i16 * kTile + 32 * ks + 8 * g));
+          bf16x8, *reinterpret_cast<const u32x4*>(p_lds + i16 * kPRow + 32 * ks + 8 * g));
       const bf16x8 pb1 = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(p_lds + (16 + i16) * kTile + 32 * ks + 8 * g));
-      const uint16_t* trb = tile + (32 * ks + trow_tok) * kRow + 128 * w + tcol;
+          bf16x8, *reinterpret_cast<const u32x4*>(p_lds + (16 + i16) * kPRow + 32 * ks + 8 * g));
+      const uint16_t* trb = tile + (32 * ks + trow_tok) * kRow + 64 * w + tcol;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < 4; ++dt) {
         const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
             (lds_bf16x4*)(trb + 16 * dt));
         const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
@@ -272,9 +277,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_latent_kernel(MlaArgs a) {
 #pragma unroll
   for (int ht = 0; ht < 2; ++ht) {
     const int hh = 16 * ht + i16;
-    float* po = a.part_o + (pbase + hh) * kC + 128 * w + 4 * g;
+    float* po = a.part_o + (pbase + hh) * kC + 64 * w + 4 * g;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < 4; ++dt) {
       *reinterpret_cast<f32x4*>(po + 16 * dt) = acc[dt][ht];
     }
     if (w == 0 && g == 0) {
@@ -388,7 +393,7 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
   a.pt_shift = ilog2(page_tokens);
   a.num_slots = num_slots;
   a.scale_log2e = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(mla_latent_kernel, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0,
+  hipLaunchKernelGGL(mla_latent_kernel, dim3(static_cast<unsigned>(grid)), dim3(kMlaThreads), 0,
                      stream, a);
   int rc = VOOM_LAUNCH_CHECK("mla_absorbed_decode: latent kernel launch");
   if (rc) return rc;
