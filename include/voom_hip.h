@@ -130,6 +130,18 @@ int voom_gather_kv(const void* k_pool, const void* v_pool, const int32_t* block_
                    int head_dim, int page_tokens, int max_pages, int num_slots,
                    hipStream_t stream);
 
+/* Token-row pages (the paged MLA latent cache, pool [num_slots, page_tokens,
+ * row_elems]): voom_append_rows writes src [batch, new_tokens, row_elems] at
+ * positions[b] + t (the latent append of KVCache.update_latent,
+ * runtime/kv_cache.py:99-105, as a slot write); voom_gather_rows materialises
+ * [batch, seq_len, row_elems] in logical order (its concatenated return). */
+int voom_append_rows(const void* src, void* pool, const int32_t* block_table,
+                     const int32_t* positions, int batch, int new_tokens, int row_elems,
+                     int page_tokens, int max_pages, int num_slots, hipStream_t stream);
+int voom_gather_rows(const void* pool, const int32_t* block_table, void* dst, int batch,
+                     int seq_len, int row_elems, int page_tokens, int max_pages, int num_slots,
+                     hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Byte-plane codec (bit-exact).
  *

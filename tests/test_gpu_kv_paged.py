@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from oracle import paged_attention as opa
+from voom_amd import ops
 from voom_amd.kv_paged import PagedKVCache
 
 pytestmark = pytest.mark.gpu
@@ -157,3 +158,83 @@ def test_nbytes_counts_resident_pages_and_tail():
     kv.spill([(0, 0)])
     assert kv.nbytes() == 2 * 70 * tok - PT * tok
     assert kv.offset == 70 and kv.layer_length(0) == 70
+
+
+# ---- latent (absorbed-MLA) cache -------------------------------------------
+
+def test_latent_update_round_trips_through_spills_bitwise():
+    print("[kv-latent] update_latent concatenation + spilled page load", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    B, R, PT, layers = 2, 576, 64, 2
+    kv = PagedKVCache(num_layers=layers, max_bytes=2 * B * R * 2 * PT, page_positions=PT,
+                      resident_pages=1)
+    chunks = [[] for _ in range(layers)]
+    for n in (150, 1, 1, 70, 1):
+        for layer in range(layers):
+            lat = rand_bf16((B, n, R), gen)
+            chunks[layer].append(lat)
+            got = kv.update_latent(layer, lat)
+            torch.cuda.synchronize()
+            assert torch.equal(bits(got), bits(torch.cat(chunks[layer], 1)))
+    assert kv.compressed_mla
+    assert kv.stats.spills > 0 and kv.stats.reloads > 0
+    page = kv._pages[0][0]
+    assert not page.resident
+    (lat0,) = page.load()
+    assert torch.equal(bits(lat0), bits(torch.cat(chunks[0], 1)[:, :PT]))
+    with pytest.raises(ValueError):
+        kv.attend(0, torch.zeros((B, 8, 1, 64), dtype=torch.bfloat16, device="cuda"))
+    kv.release()
+    assert kv.nbytes() == 0 and kv.offset == 0
+
+
+@pytest.mark.parametrize("budget_pages,compress", [(None, False), (2, False), (2, True)])
+def test_attend_mla_matches_oracle_with_spills(budget_pages, compress):
+    from oracle import mla as omla
+    print(f"[kv-latent] attend_mla budget_pages={budget_pages} compress={compress}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    B, H, dn, dv, C, dr, PT = 2, 32, 128, 128, 512, 64, 64
+    kv_b = (torch.randn((H * (dn + dv), C), generator=gen, device="cuda") * C ** -0.5
+            ).to(torch.bfloat16)
+    w_uk, w_uv_t = ops.split_kv_b(kv_b, H, dn, dv)
+    page_bytes = B * (C + dr) * 2 * PT
+    max_bytes = 1 << 40 if budget_pages is None else budget_pages * page_bytes
+    kv = PagedKVCache(num_layers=1, max_bytes=max_bytes, page_positions=PT, resident_pages=1,
+                      compress_spill=compress)
+    lats = []
+    scale = (dn + dr) ** -0.5
+    for n in (260, 1, 90, 1):
+        lat = torch.randn((B, n, C + dr), generator=gen, device="cuda").to(torch.bfloat16)
+        lats.append(lat)
+        kv.append_latent(0, lat)
+        q_nope = torch.randn((B, H, dn), generator=gen, device="cuda").to(torch.bfloat16)
+        q_rope = torch.randn((B, H, dr), generator=gen, device="cuda").to(torch.bfloat16)
+        out, wc = kv.attend_mla(0, q_nope, q_rope, w_uk, w_uv_t, scale, return_weighted_c=True)
+        torch.cuda.synchronize()
+        ref_out, ref_wc = omla.absorbed(
+            q_nope.float().cpu().numpy()[:, :, None], q_rope.float().cpu().numpy()[:, :, None],
+            torch.cat(lats, 1).float().cpu().numpy(), kv_b.float().cpu().numpy(), dn, dv,
+            bf16=True)
+        np.testing.assert_allclose(wc.float().cpu().numpy(), ref_wc[:, :, 0], atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(out.float().cpu().numpy(), ref_out[:, :, 0], atol=ATOL,
+                                   rtol=RTOL)
+    if budget_pages is not None:
+        assert kv.stats.spills > 0 and any(not p.resident for p in kv._pages[0])
+    if compress:
+        assert kv.stats.spill_bytes_compressed > 0
+
+
+def test_latent_reload_restores_pages_bitwise():
+    print("[kv-latent] explicit spill + reload", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    B, R, PT = 3, 576, 64
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, page_positions=PT, resident_pages=1,
+                      compress_spill=True)
+    kv.append_latent(0, rand_bf16((B, 400, R), gen))
+    originals = [p.load()[0].clone() for p in kv._pages[0]]
+    assert kv.spill([(0, 1), (0, 3), (0, 4)]) == 3
+    assert kv.nbytes() == (400 - 3 * PT) * B * R * 2
+    assert kv.reload() == 3
+    for p, o in zip(kv._pages[0], originals):
+        assert p.resident and torch.equal(bits(p.load()[0]), bits(o))
+    torch.cuda.synchronize()

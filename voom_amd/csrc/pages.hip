@@ -88,6 +88,53 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
   *reinterpret_cast<u32x4*>(v_out + dst) = v;
 }
 
+// Token-row pages (the MLA latent cache): pool [slots, PT, W].  One thread per
+// (b, t, 16-byte chunk) of the rows being written or read.
+__global__ __launch_bounds__(kThreads) void append_rows_kernel(
+    const uint16_t* __restrict__ src, uint16_t* __restrict__ pool,
+    const int32_t* __restrict__ table, const int32_t* __restrict__ positions, int B, int L,
+    int W, int pt_shift, int max_pages, int num_slots) {
+  const int chunks = W / 8;
+  const long long total = static_cast<long long>(B) * L * chunks;
+  const long long idx = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= total) return;
+  const int c = static_cast<int>(idx % chunks);
+  const long long rest = idx / chunks;
+  const int t = static_cast<int>(rest % L);
+  const int b = static_cast<int>(rest / L);
+  const int pos = positions[b] + t;
+  if (pos < 0) return;
+  const int page = pos >> pt_shift;
+  if (page >= max_pages) return;
+  const int slot = table[static_cast<size_t>(b) * max_pages + page];
+  if (static_cast<unsigned>(slot) >= static_cast<unsigned>(num_slots)) return;
+  const size_t off = (pos & ((1 << pt_shift) - 1));
+  *reinterpret_cast<u32x4*>(pool + ((static_cast<size_t>(slot) << pt_shift) + off) * W + c * 8) =
+      *reinterpret_cast<const u32x4*>(src + (static_cast<size_t>(b) * L + t) * W + c * 8);
+}
+
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(
+    const uint16_t* __restrict__ pool, const int32_t* __restrict__ table,
+    uint16_t* __restrict__ dst, int B, int S, int W, int pt_shift, int max_pages, int num_slots) {
+  const int chunks = W / 8;
+  const long long total = static_cast<long long>(B) * S * chunks;
+  const long long idx = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= total) return;
+  const int c = static_cast<int>(idx % chunks);
+  const long long rest = idx / chunks;
+  const int pos = static_cast<int>(rest % S);
+  const int b = static_cast<int>(rest / S);
+  const int page = pos >> pt_shift;
+  const int slot = page < max_pages ? table[static_cast<size_t>(b) * max_pages + page] : -1;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (static_cast<unsigned>(slot) < static_cast<unsigned>(num_slots)) {
+    const size_t off = pos & ((1 << pt_shift) - 1);
+    v = *reinterpret_cast<const u32x4*>(pool + ((static_cast<size_t>(slot) << pt_shift) + off) * W +
+                                        c * 8);
+  }
+  *reinterpret_cast<u32x4*>(dst + (static_cast<size_t>(b) * S + pos) * W + c * 8) = v;
+}
+
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 }  // namespace
@@ -144,4 +191,45 @@ extern "C" int voom_gather_kv(const void* k_pool, const void* v_pool, const int3
                      batch, num_kv_heads, seq_len, head_dim, ilog2(page_tokens), max_pages,
                      num_slots);
   return VOOM_LAUNCH_CHECK("gather_kv: launch");
+}
+
+extern "C" int voom_append_rows(const void* src, void* pool, const int32_t* block_table,
+                                const int32_t* positions, int batch, int new_tokens,
+                                int row_elems, int page_tokens, int max_pages, int num_slots,
+                                hipStream_t stream) {
+  VOOM_REQUIRE(src && pool && block_table && positions, "append_rows: null pointer");
+  VOOM_REQUIRE(batch > 0 && new_tokens >= 0 && max_pages > 0 && num_slots > 0,
+               "append_rows: bad geometry");
+  VOOM_REQUIRE(row_elems > 0 && row_elems % 8 == 0,
+               "append_rows: row_elems %d not a multiple of 8", row_elems);
+  VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens <= 4096,
+               "append_rows: page_tokens %d must be a power of two <= 4096", page_tokens);
+  VOOM_REQUIRE(aligned16(src) && aligned16(pool), "append_rows: buffers must be 16-byte aligned");
+  if (new_tokens == 0) return VOOM_OK;
+  const long long total = static_cast<long long>(batch) * new_tokens * (row_elems / 8);
+  hipLaunchKernelGGL(append_rows_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, static_cast<const uint16_t*>(src),
+                     static_cast<uint16_t*>(pool), block_table, positions, batch, new_tokens,
+                     row_elems, ilog2(page_tokens), max_pages, num_slots);
+  return VOOM_LAUNCH_CHECK("append_rows: launch");
+}
+
+extern "C" int voom_gather_rows(const void* pool, const int32_t* block_table, void* dst, int batch,
+                                int seq_len, int row_elems, int page_tokens, int max_pages,
+                                int num_slots, hipStream_t stream) {
+  VOOM_REQUIRE(pool && block_table && dst, "gather_rows: null pointer");
+  VOOM_REQUIRE(batch > 0 && seq_len >= 0 && max_pages > 0 && num_slots > 0,
+               "gather_rows: bad geometry");
+  VOOM_REQUIRE(row_elems > 0 && row_elems % 8 == 0,
+               "gather_rows: row_elems %d not a multiple of 8", row_elems);
+  VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens <= 4096,
+               "gather_rows: page_tokens %d must be a power of two <= 4096", page_tokens);
+  VOOM_REQUIRE(aligned16(pool) && aligned16(dst), "gather_rows: buffers must be 16-byte aligned");
+  if (seq_len == 0) return VOOM_OK;
+  const long long total = static_cast<long long>(batch) * seq_len * (row_elems / 8);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, static_cast<const uint16_t*>(pool), block_table,
+                     static_cast<uint16_t*>(dst), batch, seq_len, row_elems, ilog2(page_tokens),
+                     max_pages, num_slots);
+  return VOOM_LAUNCH_CHECK("gather_rows: launch");
 }

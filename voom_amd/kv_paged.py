@@ -69,38 +69,60 @@ class KVStats:
 class _SpillBlock:
     """Host copy of a batch of pages spilled together from one layer.
 
-    The block is a sequence of records of up to ``chunk`` pages (the staging
-    ring's chunk).  A record is contiguous and laid out as four parts -- K low
-    plane, V low plane, K high plane, V high plane -- each ``m * part_bytes``
-    long for the record's m pages, page j at ``(j % chunk) * part_bytes`` in
-    each part.  A record therefore moves in one copy each way, exactly as it
-    sits in a staging buffer.  ``ready`` is recorded after the last D2H copy.
+    ``parts[t]`` is the byte size of one byte plane of slot tensor t for one
+    page (B slots).  The block is a sequence of records of up to ``chunk``
+    pages (the staging ring's chunk).  A record of m pages is contiguous and
+    laid out as the low planes of every tensor, then the high planes, each
+    ``m * parts[t]`` long, page i of the record at ``i * parts[t]`` inside its
+    part.  A record therefore moves in one copy each way, exactly as it sits
+    in a staging buffer.  ``ready`` is recorded after the last D2H copy.
     """
 
-    __slots__ = ("block", "n_pages", "part_bytes", "chunk", "ready", "live", "compressed")
+    __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "live", "compressed")
 
-    def __init__(self, block: HostBlock, n_pages: int, part_bytes: int, chunk: int):
+    def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int):
         self.block = block
         self.n_pages = n_pages
-        self.part_bytes = part_bytes
+        self.parts = list(parts)
         self.chunk = chunk
         self.ready: torch.cuda.Event | None = None
         self.live = n_pages
-        # per page: (k_hi_frame, v_hi_frame) when the hi plane is compressed
-        self.compressed: list[tuple[np.ndarray, np.ndarray] | None] = [None] * n_pages
+        # per page: zstd frames of the high planes (one per tensor) when compressed
+        self.compressed: list[list[np.ndarray] | None] = [None] * n_pages
+
+    @property
+    def page_bytes(self) -> int:
+        return 2 * sum(self.parts)
 
     def record_pages(self, r: int) -> int:
         return min(self.chunk, self.n_pages - r * self.chunk)
 
     def record(self, r: int) -> torch.Tensor:
-        off = r * self.chunk * 4 * self.part_bytes
-        return self.block.view[off:off + 4 * self.record_pages(r) * self.part_bytes]
+        off = r * self.chunk * self.page_bytes
+        return self.block.view[off:off + self.record_pages(r) * self.page_bytes]
 
     def part(self, which: int, j: int) -> torch.Tensor:
+        """Plane ``which`` (low planes 0..T-1, then high planes) of page j."""
         r, i = divmod(j, self.chunk)
         m = self.record_pages(r)
-        off = r * self.chunk * 4 * self.part_bytes + (which * m + i) * self.part_bytes
-        return self.block.view[off:off + self.part_bytes]
+        off = r * self.chunk * self.page_bytes + part_offset(self.parts, m, which) + \
+            i * self.parts[which % len(self.parts)]
+        return self.block.view[off:off + self.parts[which % len(self.parts)]]
+
+
+def part_offset(parts: list[int], m: int, which: int) -> int:
+    """Offset of plane ``which`` inside an m-page record/staging buffer."""
+    T = len(parts)
+    lo = sum(parts[:which % T]) * m
+    return lo + (sum(parts) * m if which >= T else 0)
+
+
+def _planes(buf: torch.Tensor, parts: list[int], m: int, t: int):
+    """(low, high) plane views of tensor t inside an m-page record/staging buffer."""
+    T = len(parts)
+    lo = part_offset(parts, m, t)
+    hi = part_offset(parts, m, T + t)
+    return buf[lo:lo + m * parts[t]], buf[hi:hi + m * parts[t]]
 
 
 class _Page:
@@ -125,8 +147,9 @@ class _Page:
     def resident(self) -> bool:
         return self.slots is not None
 
-    def load(self) -> tuple[torch.Tensor, torch.Tensor]:
-        """The page's K and V as [B, NKV, page_positions, D] (bit-exact)."""
+    def load(self):
+        """The page's contents, bit-exact: (K, V) as [B, NKV, page_positions, D],
+        or (latent,) as [B, page_positions, latent_dim] for a latent cache."""
         return self.cache._page_tensors(self)
 
 
@@ -239,33 +262,55 @@ class PagedKVCache:
         self._stage_pools: list[DevicePagePool | None] = [None] * L
         self._tables: list[torch.Tensor | None] = [None] * L
         self._tables_host: list[np.ndarray | None] = [None] * L
-        self._geom: tuple[int, int, int] | None = None  # (B, NKV, D)
+        # ("kv", B, NKV, D) or ("latent", B, latent_dim), fixed by the first write
+        self._geom: tuple | None = None
+
+    def _set_geometry(self, geom: tuple, dtype: torch.dtype) -> None:
+        if self._geom is None:
+            if dtype != torch.bfloat16:
+                raise ValueError("PagedKVCache stores bfloat16 pages")
+            self._geom = geom
+        elif self._geom != geom:
+            raise ValueError(f"cache geometry changed: {self._geom} -> {geom}")
 
     def _init_geometry(self, k: torch.Tensor):
         if k.dim() != 4:
             raise ValueError("k/v must be [B, num_kv_heads, L, head_dim]")
         B, NKV, _, D = k.shape
-        if self._geom is None:
-            if k.dtype != torch.bfloat16:
-                raise ValueError("PagedKVCache stores bfloat16 K/V")
-            self._geom = (B, NKV, D)
-        elif self._geom != (B, NKV, D):
-            raise ValueError(f"K/V geometry changed: {self._geom} -> {(B, NKV, D)}")
+        self._set_geometry(("kv", B, NKV, D), k.dtype)
+
+    def _init_latent(self, lat: torch.Tensor):
+        if lat.dim() != 3:
+            raise ValueError("latent must be [B, L, latent_dim]")
+        B, _, R = lat.shape
+        self._set_geometry(("latent", B, R), lat.dtype)
+
+    @property
+    def _batch(self) -> int:
+        return self._geom[1]
+
+    @property
+    def compressed_mla(self) -> bool:
+        """True for a latent (absorbed-MLA) cache (the reference's kv.compressed_mla)."""
+        return self._geom is not None and self._geom[0] == "latent"
+
+    def _new_pool(self, **kw) -> DevicePagePool:
+        if self._geom[0] == "kv":
+            _, _, NKV, D = self._geom
+            return DevicePagePool.kv(NKV, D, self.page_positions, device=self.device, **kw)
+        return DevicePagePool.rows(self.page_positions, self._geom[2], device=self.device, **kw)
 
     def _pool(self, layer: int) -> DevicePagePool:
         pool = self._pools[layer]
         if pool is None:
-            B, NKV, D = self._geom
-            pool = DevicePagePool(NKV, D, self.page_positions, capacity=self.initial_slots,
-                                  device=self.device)
+            pool = self._new_pool(capacity=self.initial_slots)
             self._pools[layer] = pool
         return pool
 
     def _stage_pool(self, layer: int) -> DevicePagePool:
         pool = self._stage_pools[layer]
         if pool is None:
-            B, NKV, D = self._geom
-            pool = DevicePagePool(NKV, D, self.page_positions, device=self.device, min_grow=16)
+            pool = self._new_pool(min_grow=16)
             self._stage_pools[layer] = pool
         return pool
 
@@ -298,18 +343,21 @@ class PagedKVCache:
                 self._i32_cache.popitem(last=False)
         return dev
 
+    def _token_nbytes(self) -> int:
+        """Bytes one token adds to a layer across the batch (K+V, or one latent row)."""
+        if self._geom[0] == "kv":
+            _, B, NKV, D = self._geom
+            return B * NKV * D * 2 * 2
+        _, B, R = self._geom
+        return B * R * 2
+
     @property
     def page_nbytes(self) -> int:
-        B, NKV, D = self._geom
-        return B * NKV * self.page_positions * D * 2 * 2
-
-    def _token_nbytes(self) -> int:
-        B, NKV, D = self._geom
-        return B * NKV * D * 2 * 2
+        return self._token_nbytes() * self.page_positions
 
     def _set_table_cols(self, layer: int, cols: dict[int, list[int] | None]) -> None:
         """Set block-table columns (page index -> B slots, or None = not resident)."""
-        B = self._geom[0]
+        B = self._batch
         host = self._tables_host[layer]
         need = max(cols) + 1
         if host is None or need > host.shape[1]:
@@ -359,8 +407,26 @@ class PagedKVCache:
         self._init_geometry(k)
         if v.shape != k.shape:
             raise ValueError("k and v shapes differ")
-        L = k.shape[2]
-        B = self._geom[0]
+
+        def write(pool, pos):
+            ops.append_kv(k.contiguous(), v.contiguous(), pool.k, pool.v, self._tables[layer],
+                          pos)
+
+        self._append(layer, k.shape[2], write)
+
+    def append_latent(self, layer: int, lat: torch.Tensor) -> None:
+        """Write latent rows lat [B, L, latent_dim] ([c_kv | k_rope]) after the
+        layer's current tokens: the append of KVCache.update_latent
+        (runtime/kv_cache.py:99-105) as a slot write into the latent pool."""
+        self._init_latent(lat)
+
+        def write(pool, pos):
+            ops.append_rows(lat.contiguous(), pool.lat, self._tables[layer], pos)
+
+        self._append(layer, lat.shape[1], write)
+
+    def _append(self, layer: int, L: int, write) -> None:
+        B = self._batch
         pool = self._pool(layer)
         start = self._len[layer]
         end = start + L
@@ -374,9 +440,7 @@ class PagedKVCache:
                 self._open_slots[layer][page] = cols[page]
             self._set_table_cols(layer, cols)
         if L:
-            pos = torch.full((B,), start, dtype=torch.int32, device=self.device)
-            ops.append_kv(k.contiguous(), v.contiguous(), pool.k, pool.v, self._tables[layer],
-                          pos)
+            write(pool, torch.full((B,), start, dtype=torch.int32, device=self.device))
         self._len[layer] = end
         pages = self._pages[layer]
         while (len(pages) + 1) * PT <= end:
@@ -396,26 +460,61 @@ class PagedKVCache:
         self.append(layer, k, v)
         return self.gather(layer)
 
+    def update_latent(self, layer: int, lat: torch.Tensor) -> torch.Tensor:
+        """Append latent rows, then return the layer's latent [B, S, latent_dim]
+        (KVCache.update_latent, runtime/kv_cache.py:99-105); prefer
+        ``attend_mla`` on the decode path."""
+        self.append_latent(layer, lat)
+        return self.gather_latent(layer)
+
     def gather(self, layer: int):
         """Logical K/V [B, NKV, S, D] of a layer, spilled pages reloaded transiently."""
+        self._require_kind(layer, "kv")
         S = self._len[layer]
         pool = self._pool(layer)
         k_all, v_all = ops.gather_kv(pool.k, pool.v, self._tables[layer], S)
-        spilled = [p for p in self._pages[layer] if not p.resident]
-        if spilled:
-            PT = self.page_positions
-            stage = self._stage_pool(layer)
+        PT = self.page_positions
 
-            def place(chunk, slots):
-                B = self._geom[0]
-                for j, p in enumerate(chunk):
-                    idx = self._dev_i32(slots[j * B:(j + 1) * B], cache=True).long()
-                    k_all[:, :, p.index * PT:(p.index + 1) * PT] = stage.k.index_select(0, idx)
-                    v_all[:, :, p.index * PT:(p.index + 1) * PT] = \
-                        stage.v.index_select(0, idx).transpose(2, 3)
+        def place(p, idx, stage):
+            k_all[:, :, p.index * PT:(p.index + 1) * PT] = stage.k.index_select(0, idx)
+            v_all[:, :, p.index * PT:(p.index + 1) * PT] = \
+                stage.v.index_select(0, idx).transpose(2, 3)
 
-            self._stream_in(layer, spilled, stage, place, transient=True)
+        self._place_spilled(layer, place)
         return k_all, v_all
+
+    def gather_latent(self, layer: int) -> torch.Tensor:
+        """Logical latent [B, S, latent_dim] of a layer, spilled pages reloaded transiently."""
+        self._require_kind(layer, "latent")
+        S = self._len[layer]
+        lat_all = ops.gather_rows(self._pool(layer).lat, self._tables[layer], S)
+        PT = self.page_positions
+
+        def place(p, idx, stage):
+            lat_all[:, p.index * PT:(p.index + 1) * PT] = stage.lat.index_select(0, idx)
+
+        self._place_spilled(layer, place)
+        return lat_all
+
+    def _require_kind(self, layer: int, kind: str) -> None:
+        if self._geom is None or self._geom[0] != kind:
+            have = "empty" if self._geom is None else self._geom[0]
+            raise ValueError(f"layer {layer}: this call needs a {kind} cache, the cache is {have}")
+
+    def _place_spilled(self, layer: int, place) -> None:
+        """Stream a layer's spilled pages through staging slots, calling
+        ``place(page, slot_index_tensor, stage_pool)`` for each landed page."""
+        spilled = [p for p in self._pages[layer] if not p.resident]
+        if not spilled:
+            return
+        stage = self._stage_pool(layer)
+        B = self._batch
+
+        def consume(chunk, slots):
+            for j, p in enumerate(chunk):
+                place(p, self._dev_i32(slots[j * B:(j + 1) * B], cache=True).long(), stage)
+
+        self._stream_in(layer, spilled, stage, consume, transient=True)
 
     def release(self) -> None:
         """Free device slots and host copies; offset and nbytes return to 0."""
@@ -474,14 +573,18 @@ class PagedKVCache:
         self.stats.spill_s += time.perf_counter() - t0
         return len(pages)
 
+    def _plane_parts(self, pool: DevicePagePool) -> list[int]:
+        """Bytes of one byte plane of each pool tensor for one page (B slots)."""
+        return [self._batch * pool.tensor_slot_bytes(t) // 2 for t in range(len(pool.tensors))]
+
     def _spill_plan(self, layer: int, pages: list[_Page]):
         """One host block for the layer's pages; returns its chunk work items."""
-        B = self._geom[0]
         pool = self._pool(layer)
-        part = B * pool.slot_bytes // 2       # one plane of a page's K (or V)
+        parts = self._plane_parts(pool)
+        page_bytes = 2 * sum(parts)
         n = len(pages)
-        per_chunk = max(1, self._ring.nbytes // (4 * part))
-        sb = _SpillBlock(self.arena.alloc(4 * n * part), n, part, per_chunk)
+        per_chunk = max(1, self._ring.nbytes // page_bytes)
+        sb = _SpillBlock(self.arena.alloc(n * page_bytes), n, parts, per_chunk)
         for j, p in enumerate(pages):
             p.host = sb
             p.host_j = j
@@ -503,18 +606,15 @@ class PagedKVCache:
             staged = []
             for pool, cp, sb, rec in work[w0:w0 + nbuf]:
                 m = len(cp)
-                part = sb.part_bytes
                 slot_t = self._dev_i32([s for p in cp for s in p.slots])
-                idx, buf = self._ring.acquire(main, 4 * m * part)
-                lo_k, lo_v = buf[0:m * part], buf[m * part:2 * m * part]
-                hi_k, hi_v = buf[2 * m * part:3 * m * part], buf[3 * m * part:4 * m * part]
-                if ops.slot_codec_supported(pool.k):
-                    ops.byteplane_split_slots(pool.k, slot_t, lo_k, hi_k)
-                    ops.byteplane_split_slots(pool.v, slot_t, lo_v, hi_v)
-                else:
-                    sel = slot_t.long()
-                    ops.byteplane_split(pool.k.index_select(0, sel).contiguous(), lo_k, hi_k)
-                    ops.byteplane_split(pool.v.index_select(0, sel).contiguous(), lo_v, hi_v)
+                idx, buf = self._ring.acquire(main, m * sb.page_bytes)
+                for t, tensor in enumerate(pool.tensors):
+                    lo, hi = _planes(buf, sb.parts, m, t)
+                    if ops.slot_codec_supported(tensor):
+                        ops.byteplane_split_slots(tensor, slot_t, lo, hi)
+                    else:
+                        ops.byteplane_split(tensor.index_select(0, slot_t.long()).contiguous(),
+                                            lo, hi)
                 ev = torch.cuda.Event()
                 ev.record(main)
                 staged.append((idx, buf, sb, rec, ev))
@@ -527,32 +627,35 @@ class PagedKVCache:
                 sb.ready.record(copy)
 
     def _compress_spilled(self, pages: list[_Page]) -> None:
+        """zstd level 1 on each high plane; low planes stay raw (formats/packed.py:49-50)."""
         for p in pages:
             sb = p.host
             sb.ready.synchronize()
-            k_hi = sb.part(2, p.host_j).numpy()
-            v_hi = sb.part(3, p.host_j).numpy()
-            kz, vz = _zstd.compress(k_hi, 1), _zstd.compress(v_hi, 1)
-            sb.compressed[p.host_j] = (kz, vz)
+            T = len(sb.parts)
+            frames = [_zstd.compress(sb.part(T + t, p.host_j).numpy(), 1) for t in range(T)]
+            sb.compressed[p.host_j] = frames
             p._compressed = True
             self.stats.spill_bytes_raw += p.nbytes
-            self.stats.spill_bytes_compressed += 2 * sb.part_bytes + kz.nbytes + vz.nbytes
+            self.stats.spill_bytes_compressed += sum(sb.parts) + sum(f.nbytes for f in frames)
 
-    def _host_planes(self, p: _Page, stage: torch.Tensor | None = None):
-        """Pinned (lo_k, lo_v, hi_k, hi_v) host tensors of a spilled page."""
+    def _host_planes(self, p: _Page) -> list[torch.Tensor]:
+        """Pinned host tensors of a spilled page's planes: low planes of every
+        pool tensor, then high planes (decompressed when compressed)."""
         sb = p.host
-        parts = [sb.part(w, p.host_j) for w in range(4)]
-        comp = sb.compressed[p.host_j]
-        if comp is not None:
-            for w, frame in ((2, comp[0]), (3, comp[1])):
-                out = torch.empty(sb.part_bytes, dtype=torch.uint8,
-                                  pin_memory=self.arena.pin)
+        T = len(sb.parts)
+        planes = [sb.part(w, p.host_j) for w in range(2 * T)]
+        frames = sb.compressed[p.host_j]
+        if frames is not None:
+            for t, frame in enumerate(frames):
+                out = torch.empty(sb.parts[t], dtype=torch.uint8, pin_memory=self.arena.pin)
                 _zstd.decompress_into(frame, out.numpy())
-                parts[w] = out
-        return parts
+                planes[T + t] = out
+        return planes
 
-    def _upload_planes(self, pages: list[_Page], staging: torch.Tensor, part: int) -> None:
-        """H2D the planes of ``pages`` into staging laid out [lo_k | lo_v | hi_k | hi_v].
+    def _upload_planes(self, pages: list[_Page], staging: torch.Tensor,
+                       parts: list[int]) -> None:
+        """H2D the planes of ``pages`` into staging, laid out as a host record
+        (low planes of every tensor, then high planes, page-major inside each).
 
         A chunk that is exactly one uncompressed host record, in order, moves
         in a single copy; anything else is assembled page by page.
@@ -565,30 +668,24 @@ class PagedKVCache:
                         and sb.compressed[p.host_j] is None for j, p in enumerate(pages))):
             staging.copy_(sb.record(p0.host_j // sb.chunk), non_blocking=True)
             return
+        T = len(parts)
         for j, p in enumerate(pages):
-            parts = self._host_planes(p)
-            for w in range(4):
-                staging[(w * n + j) * part:(w * n + j + 1) * part].copy_(parts[w],
-                                                                         non_blocking=True)
+            for w, plane in enumerate(self._host_planes(p)):
+                off = part_offset(parts, n, w) + j * parts[w % T]
+                staging[off:off + parts[w % T]].copy_(plane, non_blocking=True)
 
-    def _merge_into(self, pool: DevicePagePool, staging: torch.Tensor, n: int, part: int,
-                    slots: list[int], cache: bool = False) -> None:
+    def _merge_into(self, pool: DevicePagePool, staging: torch.Tensor, n: int,
+                    parts: list[int], slots: list[int], cache: bool = False) -> None:
         slot_t = self._dev_i32(slots, cache=cache)
-        lo_k, lo_v = staging[0:n * part], staging[n * part:2 * n * part]
-        hi_k, hi_v = staging[2 * n * part:3 * n * part], staging[3 * n * part:4 * n * part]
-        if ops.slot_codec_supported(pool.k):
-            ops.byteplane_merge_slots(lo_k, hi_k, pool.k, slot_t)
-            ops.byteplane_merge_slots(lo_v, hi_v, pool.v, slot_t)
-        else:
-            sel = slot_t.long()
-            kb = torch.empty((len(slots),) + tuple(pool.k.shape[1:]), dtype=pool.k.dtype,
-                             device=self.device)
-            vb = torch.empty((len(slots),) + tuple(pool.v.shape[1:]), dtype=pool.v.dtype,
-                             device=self.device)
-            ops.byteplane_merge(lo_k, hi_k, kb)
-            ops.byteplane_merge(lo_v, hi_v, vb)
-            pool.k.index_copy_(0, sel, kb)
-            pool.v.index_copy_(0, sel, vb)
+        for t, tensor in enumerate(pool.tensors):
+            lo, hi = _planes(staging, parts, n, t)
+            if ops.slot_codec_supported(tensor):
+                ops.byteplane_merge_slots(lo, hi, tensor, slot_t)
+            else:
+                staged = torch.empty((len(slots),) + tuple(tensor.shape[1:]), dtype=tensor.dtype,
+                                     device=self.device)
+                ops.byteplane_merge(lo, hi, staged)
+                tensor.index_copy_(0, slot_t.long(), staged)
 
     def _stream_in(self, layer: int, pages: list[_Page], target: DevicePagePool, consume,
                    transient: bool) -> None:
@@ -609,7 +706,7 @@ class PagedKVCache:
         the slots are reused safely because merges and the consumers' reads
         are all on the main stream.
         """
-        B = self._geom[0]
+        B = self._batch
         main = torch.cuda.current_stream()
         copy = self._stream()
         nbuf = len(self._ring.bufs)
@@ -617,28 +714,28 @@ class PagedKVCache:
         chunks = []
         n_pages = 0
         for layer, pages, target, consume, transient in jobs:
-            part = B * target.slot_bytes // 2
-            per_chunk = max(1, self._ring.nbytes // (4 * part))
+            parts = self._plane_parts(target)
+            per_chunk = max(1, self._ring.nbytes // (2 * sum(parts)))
             if transient:
                 target.ensure_capacity(nbuf * per_chunk * B)
             for sb in {id(p.host): p.host for p in pages}.values():
                 copy.wait_event(sb.ready)
             for c0 in range(0, len(pages), per_chunk):
-                chunks.append((pages[c0:c0 + per_chunk], target, consume, transient, part,
+                chunks.append((pages[c0:c0 + per_chunk], target, consume, transient, parts,
                                per_chunk))
             n_pages += len(pages)
         for w0 in range(0, len(chunks), nbuf):
             window = chunks[w0:w0 + nbuf]
             landed = []
-            for cp, target, consume, transient, part, per_chunk in window:
-                idx, buf = self._ring.acquire(copy, 4 * len(cp) * part)
+            for cp, target, consume, transient, parts, per_chunk in window:
+                idx, buf = self._ring.acquire(copy, 2 * len(cp) * sum(parts))
                 with torch.cuda.stream(copy):
-                    self._upload_planes(cp, buf, part)
+                    self._upload_planes(cp, buf, parts)
                 ev = torch.cuda.Event()
                 ev.record(copy)
                 landed.append((idx, buf, ev))
-            for (cp, target, consume, transient, part, per_chunk), (idx, buf, ev) in zip(window,
-                                                                                      landed):
+            for (cp, target, consume, transient, parts, per_chunk), (idx, buf, ev) in zip(
+                    window, landed):
                 main.wait_event(ev)
                 m = len(cp)
                 if transient:
@@ -646,7 +743,7 @@ class PagedKVCache:
                     slots = list(range(base, base + m * B))
                 else:
                     slots = target.allocate(B * m)
-                self._merge_into(target, buf, m, part, slots, cache=transient)
+                self._merge_into(target, buf, m, parts, slots, cache=transient)
                 self._ring.release(idx, main)
                 consume(cp, slots)
         self.stats.reloads += n_pages
@@ -667,7 +764,7 @@ class PagedKVCache:
             return 0
         if stream is not None:
             self._copy_stream = stream
-        B = self._geom[0]
+        B = self._batch
         by_layer: dict[int, list[_Page]] = {}
         for p in pages:
             by_layer.setdefault(p.layer, []).append(p)
@@ -698,23 +795,23 @@ class PagedKVCache:
             sb.ready.synchronize()
             self.arena.free(sb.block)
 
-    def _page_tensors(self, p: _Page):
-        B, NKV, D = self._geom
-        if p.resident:
-            pool = self._pool(p.layer)
-            idx = self._dev_i32(p.slots).long()
+    def _slot_contents(self, pool: DevicePagePool, idx: torch.Tensor):
+        if self._geom[0] == "kv":
             return (pool.k.index_select(0, idx),
                     pool.v.index_select(0, idx).transpose(2, 3).contiguous())
+        return (pool.lat.index_select(0, idx),)
+
+    def _page_tensors(self, p: _Page):
+        if p.resident:
+            return self._slot_contents(self._pool(p.layer), self._dev_i32(p.slots).long())
         stage = self._stage_pool(p.layer)
         out = []
 
         def grab(chunk, slots):
-            idx = self._dev_i32(slots).long()
-            out.append(stage.k.index_select(0, idx))
-            out.append(stage.v.index_select(0, idx).transpose(2, 3).contiguous())
+            out.extend(self._slot_contents(stage, self._dev_i32(slots).long()))
 
         self._stream_in(p.layer, [p], stage, grab, transient=True)
-        return out[0], out[1]
+        return tuple(out)
 
     # ---- fused decode attention --------------------------------------------
 
@@ -729,15 +826,52 @@ class PagedKVCache:
         merged by log-sum-exp, so only the last chunk's attention is exposed
         after the transfer.
         """
-        B, NKV, D = self._geom
-        S = self._len[layer]
-        pool = self._pool(layer)
+        self._require_kind(layer, "kv")
+        D = self._geom[3]
         if scale is None:
             scale = D ** -0.5
+
+        def run(pool, table, ctx, lse):
+            return ops.paged_gqa_decode(q, pool.k, pool.v, table, ctx, scale=scale,
+                                        return_lse=lse)
+
+        return self._attend_pages(layer, run)
+
+    def attend_mla(self, layer: int, q_nope: torch.Tensor, q_rope: torch.Tensor,
+                   w_uk: torch.Tensor, w_uv_t: torch.Tensor, scale: float,
+                   return_weighted_c: bool = False):
+        """Absorbed-MLA decode over the layer's latent pages (runtime/glm.py:78-202).
+
+        q_nope [B, H, dn], q_rope [B, H, 64] bf16 (one query token); W_UK
+        [H, dn, 512] and W_UV^T [H, 512, dv] as from ops.split_kv_b; ``scale``
+        is the reference's (dn + dr) ** -0.5.  q_lat = [q_nope . W_UK | q_rope]
+        is contracted with the paged latent in the HIP kernel (resident pages
+        first, spilled pages chunk by chunk as they land, LSE-merged), and
+        weighted_c . W_UV gives the per-head output [B, H, dv] before o_proj.
+        """
+        self._require_kind(layer, "latent")
+        q_lat = ops.mla_absorb_query(q_nope, q_rope, w_uk)
+
+        def run(pool, table, ctx, lse):
+            return ops.mla_latent_decode(q_lat, pool.lat, table, ctx, scale=scale,
+                                         return_lse=lse)
+
+        wc = self._attend_pages(layer, run)
+        out = ops.mla_project_out(wc, w_uv_t)
+        return (out, wc) if return_weighted_c else out
+
+    def _attend_pages(self, layer: int, run) -> torch.Tensor:
+        """Drive ``run(pool, block_table, ctx_lens, return_lse)`` over a layer:
+        one call over the block table when every page is resident, else one
+        over the resident pages plus one per landed chunk of spilled pages,
+        folded by log-sum-exp merges."""
+        B = self._batch
+        S = self._len[layer]
+        pool = self._pool(layer)
         spilled = [p for p in self._pages[layer] if not p.resident]
         if not spilled:
             ctx = torch.full((B,), S, dtype=torch.int32, device=self.device)
-            return ops.paged_gqa_decode(q, pool.k, pool.v, self._tables[layer], ctx, scale=scale)
+            return run(pool, self._tables[layer], ctx, False)
         PT = self.page_positions
         # Resident pages, the open page last (attention of one query token is
         # order-free; only a partial page has to be the last one).
@@ -757,15 +891,14 @@ class PagedKVCache:
         if res_cols:
             t_res = self._dev_i32(self._tables_host[layer][:, res_cols], cache=True)
             c_res = torch.full((B,), res_ctx, dtype=torch.int32, device=self.device)
-            fold(ops.paged_gqa_decode(q, pool.k, pool.v, t_res, c_res, scale=scale,
-                                      return_lse=True))
+            fold(run(pool, t_res, c_res, True))
         stage = self._stage_pool(layer)
 
         def attend_chunk(chunk, slots):
             m = len(chunk)
             t = self._dev_i32(np.asarray(slots, np.int32).reshape(m, B).T, cache=True)
             c = torch.full((B,), m * PT, dtype=torch.int32, device=self.device)
-            fold(ops.paged_gqa_decode(q, stage.k, stage.v, t, c, scale=scale, return_lse=True))
+            fold(run(stage, t, c, True))
 
         self._stream_in(layer, spilled, stage, attend_chunk, transient=True)
         return state[0][0]

@@ -289,6 +289,21 @@ def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
     return w[:, :dn, :].contiguous(), w[:, dn:, :].transpose(1, 2).contiguous()
 
 
+def mla_absorb_query(q_nope: torch.Tensor, q_rope: torch.Tensor, w_uk: torch.Tensor):
+    """q_lat = [q_nope . W_UK | q_rope] [B, H, 576] (runtime/glm.py:129-132).
+
+    q_nope [B, H, dn], q_rope [B, H, 64] bf16, W_UK [H, dn, 512]; a batched
+    GEMM over heads with both operands contiguous.
+    """
+    q_abs = torch.bmm(q_nope.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
+    return torch.cat([q_abs, q_rope], dim=-1).contiguous()
+
+
+def mla_project_out(wc: torch.Tensor, w_uv_t: torch.Tensor) -> torch.Tensor:
+    """weighted_c [B, H, 512] . W_UV -> [B, H, dv] (runtime/glm.py:200-202)."""
+    return torch.bmm(wc.transpose(0, 1).contiguous(), w_uv_t).transpose(0, 1).contiguous()
+
+
 def mla_absorbed_decode(q_nope: torch.Tensor, q_rope: torch.Tensor, lat_pool: torch.Tensor,
                         block_table: torch.Tensor, ctx_lens: torch.Tensor, w_uk: torch.Tensor,
                         w_uv_t: torch.Tensor, *, scale: float, num_ranges: int = 0,
@@ -300,11 +315,36 @@ def mla_absorbed_decode(q_nope: torch.Tensor, q_rope: torch.Tensor, lat_pool: to
     as batched GEMMs (hipBLASLt through torch); the latent contraction runs in
     the HIP kernel.  Returns the per-head output [B, H, dv] bf16 (before o_proj).
     """
-    B, H, dn = q_nope.shape
-    # [H, B, dn] @ [H, dn, C] -> [H, B, C]; both operands contiguous.
-    q_abs = torch.bmm(q_nope.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
-    q_lat = torch.cat([q_abs, q_rope], dim=-1).contiguous()
+    q_lat = mla_absorb_query(q_nope, q_rope, w_uk)
     wc = mla_latent_decode(q_lat, lat_pool, block_table, ctx_lens, scale=scale,
                            num_ranges=num_ranges)
-    out = torch.bmm(wc.transpose(0, 1).contiguous(), w_uv_t).transpose(0, 1).contiguous()
+    out = mla_project_out(wc, w_uv_t)
     return (out, wc) if return_weighted_c else out
+
+
+def append_rows(src: torch.Tensor, pool: torch.Tensor, block_table: torch.Tensor,
+                positions: torch.Tensor, *, stream: torch.cuda.Stream | None = None) -> None:
+    """Write token rows src [B, L, W] into a row pool [slots, PT, W] at positions[b] + t."""
+    _require_device(src, pool, block_table, positions)
+    B, L, W = src.shape
+    slots, PT, W2 = pool.shape
+    _require(W == W2 and src.dtype == pool.dtype and src.element_size() == 2,
+             "src and pool must be 16-bit with the same row width")
+    _require(block_table.dtype == torch.int32 and positions.dtype == torch.int32
+             and block_table.shape[0] == B and tuple(positions.shape) == (B,),
+             "block_table [B, max_pages] and positions [B] must be int32")
+    _lib.call("voom_append_rows", _ptr(src), _ptr(pool), _ptr(block_table), _ptr(positions), B, L,
+              W, PT, block_table.shape[1], slots, _stream(stream))
+
+
+def gather_rows(pool: torch.Tensor, block_table: torch.Tensor, seq_len: int, *,
+                stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Logical rows [B, seq_len, W] of a row pool [slots, PT, W]."""
+    dev = _require_device(pool, block_table)
+    slots, PT, W = pool.shape
+    B = block_table.shape[0]
+    _require(block_table.dtype == torch.int32, "block_table must be int32")
+    out = torch.empty((B, seq_len, W), dtype=pool.dtype, device=dev)
+    _lib.call("voom_gather_rows", _ptr(pool), _ptr(block_table), _ptr(out), B, seq_len, W, PT,
+              block_table.shape[1], slots, _stream(stream))
+    return out

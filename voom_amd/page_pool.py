@@ -1,8 +1,10 @@
-"""Device page pool: per-layer K/V slot storage plus a free list of slot ids.
+"""Device page pool: per-layer slot storage plus a free list of slot ids.
 
-One slot holds one page of one sequence for one layer:
-  k [capacity, num_kv_heads, page_tokens, head_dim]   token-major
-  v [capacity, num_kv_heads, head_dim, page_tokens]   transposed page (V^T)
+A slot holds one page of one sequence for one layer, as one or more tensors
+that share the slot index:
+  KV pool      k [capacity, num_kv_heads, page_tokens, head_dim]   token-major
+               v [capacity, num_kv_heads, head_dim, page_tokens]   transposed (V^T)
+  latent pool  lat [capacity, page_tokens, latent_dim]             token-major
 Allocation, recycling and 25 % geometric growth follow the reference's
 PositionFreePagePool (runtime/kv_cache.py:316-414), with page_tokens-wide slots
 instead of one-token pages.  Growth reallocates and copies the pool, so slot
@@ -11,38 +13,53 @@ ids stay valid while tensor addresses change.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 
 class DevicePagePool:
-    def __init__(self, num_kv_heads: int, head_dim: int, page_tokens: int, *,
-                 capacity: int = 0, dtype=torch.bfloat16, device=None, min_grow: int = 64):
-        if num_kv_heads <= 0 or head_dim <= 0 or page_tokens <= 0:
+    def __init__(self, slot_shapes: list[tuple[int, ...]], *, capacity: int = 0,
+                 dtype=torch.bfloat16, device=None, min_grow: int = 64):
+        if not slot_shapes or any(d <= 0 for shp in slot_shapes for d in shp):
             raise ValueError("page pool geometry must be positive")
-        self.num_kv_heads = int(num_kv_heads)
-        self.head_dim = int(head_dim)
-        self.page_tokens = int(page_tokens)
+        self.slot_shapes = [tuple(int(d) for d in shp) for shp in slot_shapes]
         self.dtype = dtype
         self.device = torch.device(device) if device is not None else torch.device("cuda")
         self.min_grow = int(min_grow)
-        self.k = self._empty_k(0)
-        self.v = self._empty_v(0)
+        self.tensors = [self._empty(shp, 0) for shp in self.slot_shapes]
         self._free: list[int] = []
         self._live = 0
         if capacity:
             self.ensure_capacity(capacity)
 
-    def _empty_k(self, n):
-        return torch.empty((n, self.num_kv_heads, self.page_tokens, self.head_dim),
-                           dtype=self.dtype, device=self.device)
+    @classmethod
+    def kv(cls, num_kv_heads: int, head_dim: int, page_tokens: int, **kw) -> "DevicePagePool":
+        return cls([(num_kv_heads, page_tokens, head_dim), (num_kv_heads, head_dim, page_tokens)],
+                   **kw)
 
-    def _empty_v(self, n):
-        return torch.empty((n, self.num_kv_heads, self.head_dim, self.page_tokens),
-                           dtype=self.dtype, device=self.device)
+    @classmethod
+    def rows(cls, page_tokens: int, row_elems: int, **kw) -> "DevicePagePool":
+        return cls([(page_tokens, row_elems)], **kw)
+
+    def _empty(self, shp, n):
+        return torch.empty((n,) + shp, dtype=self.dtype, device=self.device)
+
+    @property
+    def k(self) -> torch.Tensor:
+        return self.tensors[0]
+
+    @property
+    def v(self) -> torch.Tensor:
+        return self.tensors[1]
+
+    @property
+    def lat(self) -> torch.Tensor:
+        return self.tensors[0]
 
     @property
     def capacity(self) -> int:
-        return self.k.shape[0]
+        return self.tensors[0].shape[0]
 
     @property
     def live_slots(self) -> int:
@@ -52,21 +69,25 @@ class DevicePagePool:
     def free_slots(self) -> int:
         return len(self._free)
 
+    def tensor_slot_bytes(self, i: int) -> int:
+        """Bytes of one slot of tensor i."""
+        return math.prod(self.slot_shapes[i]) * self.tensors[i].element_size()
+
     @property
     def slot_bytes(self) -> int:
-        """Bytes of one K slot (the same for V)."""
-        return self.num_kv_heads * self.page_tokens * self.head_dim * self.k.element_size()
+        """Bytes of one slot across all tensors."""
+        return sum(self.tensor_slot_bytes(i) for i in range(len(self.tensors)))
 
     def ensure_capacity(self, required: int) -> None:
         cap = self.capacity
         if required <= cap:
             return
         target = max(required, cap + max(self.min_grow, cap // 4))
-        k, v = self._empty_k(target), self._empty_v(target)
+        new = [self._empty(shp, target) for shp in self.slot_shapes]
         if cap:
-            k[:cap].copy_(self.k)
-            v[:cap].copy_(self.v)
-        self.k, self.v = k, v
+            for dst, src in zip(new, self.tensors):
+                dst[:cap].copy_(src)
+        self.tensors = new
         # new ids are handed out lowest first
         self._free.extend(range(target - 1, cap - 1, -1))
 
