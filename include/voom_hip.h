@@ -72,6 +72,25 @@ int voom_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                           int page_tokens, int max_pages, int num_slots, float scale,
                           int num_splits, hipStream_t stream);
 
+/* The two halves of voom_paged_gqa_decode, for callers that time or schedule
+ * them separately (same arguments, same workspace, same num_splits):
+ *   voom_paged_gqa_partials  streams the pages once and leaves one partial
+ *                            softmax state (m, l, o) per split piece in the
+ *                            workspace (the main, HBM-bound kernel);
+ *   voom_paged_gqa_combine   merges each head's partial states into out and
+ *                            lse_out (the online-softmax merge of
+ *                            runtime/pic_attention.py:106-129).
+ * voom_paged_gqa_decode(...) is exactly partials followed by combine. */
+int voom_paged_gqa_partials(const void* q, const void* k_pool, const void* v_pool,
+                            const int32_t* block_table, const int32_t* ctx_lens,
+                            void* workspace, size_t ws_bytes, int batch, int num_q_heads,
+                            int num_kv_heads, int head_dim, int page_tokens, int max_pages,
+                            int num_slots, float scale, int num_splits, hipStream_t stream);
+int voom_paged_gqa_combine(const int32_t* ctx_lens, void* out, float* lse_out,
+                           void* workspace, size_t ws_bytes, int batch, int num_q_heads,
+                           int num_kv_heads, int head_dim, int page_tokens, int max_pages,
+                           int num_splits, hipStream_t stream);
+
 /* Merge two attention states over disjoint key sets (log-sum-exp combine):
  * out = (o_a*e^{lse_a} + o_b*e^{lse_b}) / (e^{lse_a} + e^{lse_b}).
  * o_a/o_b/out [rows, head_dim] bf16, lse_* [rows] fp32; lse_out may be NULL.

@@ -26,7 +26,9 @@ def test_header_declares_expected_entry_points():
     names = declared_symbols()
     for required in ("voom_paged_gqa_decode", "voom_byteplane_split", "voom_byteplane_merge",
                      "voom_byteplane_split_slots", "voom_byteplane_merge_slots",
-                     "voom_append_kv", "voom_gather_kv", "voom_merge_attn_states"):
+                     "voom_append_kv", "voom_gather_kv", "voom_merge_attn_states",
+                     "voom_paged_gqa_partials", "voom_paged_gqa_combine",
+                     "voom_mla_absorbed_decode", "voom_append_rows", "voom_gather_rows"):
         assert required in names
 
 
@@ -67,6 +69,11 @@ def test_validation_errors_raise_value_error():
     assert rc == _lib.VOOM_EINVAL and "page_tokens" in _lib.last_error()
     rc = lib.voom_paged_gqa_decode(fake, fake, fake, fake, fake, fake, None, fake, 16,
                                    1, 4, 2, 128, 64, 1, 1, 1.0, 64, None)
+    assert rc == _lib.VOOM_EINVAL and "workspace" in _lib.last_error()
+    rc = lib.voom_paged_gqa_partials(fake, fake, fake, fake, None, fake, 1 << 30,
+                                     1, 4, 2, 128, 64, 1, 1, 1.0, 1, None)
+    assert rc == _lib.VOOM_EINVAL and "null pointer" in _lib.last_error()
+    rc = lib.voom_paged_gqa_combine(fake, fake, None, fake, 16, 1, 4, 2, 128, 64, 1, 64, None)
     assert rc == _lib.VOOM_EINVAL and "workspace" in _lib.last_error()
     rc = lib.voom_byteplane_split_slots(fake, fake, 1, 100, 1, fake, fake, None)
     assert rc == _lib.VOOM_EINVAL and "multiple of 64" in _lib.last_error()

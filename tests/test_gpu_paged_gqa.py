@@ -52,6 +52,27 @@ def test_split_counts_agree(splits):
              num_q_heads=32, num_kv_heads=8, head_dim=128, page_tokens=64, num_splits=splits)
 
 
+@pytest.mark.parametrize("D,splits", [(128, None), (64, 5)])
+def test_partials_then_combine_is_the_decode_bitwise(D, splits):
+    print(f"[gqa] case partials+combine D={D} splits={splits}", flush=True)
+    inp = synthetic.gqa_decode_inputs(batch=3, ctx_lens=[0, 700, 2500], num_q_heads=16,
+                                      num_kv_heads=4, head_dim=D, device="cuda")
+    whole, lse = ops.paged_gqa_decode(inp.q, inp.k_pool, inp.v_pool, inp.block_table,
+                                      inp.ctx_lens, scale=inp.scale, return_lse=True,
+                                      num_splits=splits)
+    n = splits if splits is not None else min(ops.default_splits(), 3 * 4 * inp.block_table.shape[1] * 2)
+    ws = torch.empty(ops.gqa_workspace_bytes(3, 16, 4, D, n), dtype=torch.uint8, device="cuda")
+    ops.paged_gqa_partials(inp.q, inp.k_pool, inp.v_pool, inp.block_table, inp.ctx_lens,
+                           scale=inp.scale, num_splits=n, ws=ws)
+    out = torch.empty_like(inp.q)
+    lse2 = torch.empty_like(lse)
+    ops.paged_gqa_combine(inp.ctx_lens, out, ws, num_kv_heads=4, page_tokens=64,
+                          max_pages=inp.block_table.shape[1], num_splits=n, lse=lse2)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), whole.view(torch.int16))
+    assert torch.equal(lse2, lse)
+
+
 def test_empty_sequence_gives_zeros():
     print("[gqa] case empty sequence", flush=True)
     inp = synthetic.gqa_decode_inputs(batch=3, ctx_lens=[0, 40, 0], num_q_heads=8,

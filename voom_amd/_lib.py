@@ -29,6 +29,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_paged_gqa_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_size_t,
                                       c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                       c_float, c_int, _P]),
+    "voom_paged_gqa_partials": (c_int, [_P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int, c_int,
+                                        c_int, c_int, c_int, c_int, c_float, c_int, _P]),
+    "voom_paged_gqa_combine": (c_int, [_P, _P, _P, _P, c_size_t, c_int, c_int, c_int, c_int,
+                                       c_int, c_int, c_int, _P]),
     "voom_merge_attn_states": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, _P]),
     "voom_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "voom_mla_absorbed_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int,

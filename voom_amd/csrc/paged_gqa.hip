@@ -383,10 +383,6 @@ __global__ __launch_bounds__(kThreads) void gqa_reduce_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     const int32_t* __restrict__ ctx_lens, uint16_t* __restrict__ out,
     float* __restrict__ lse_out, int B, int NKV, int G, int max_pages, int pt_shift, int W) {
-  __shared__ int seg[kMaxBatch + 1];
-  __shared__ int wave_tot[kWavesPerBlock];
-  build_block_prefix(ctx_lens, B, max_pages << pt_shift, seg, wave_tot);
-
   constexpr int DPL = D / kWave;  // dims per lane
   const int lane = threadIdx.x & (kWave - 1);
   const int task = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
@@ -397,7 +393,28 @@ __global__ __launch_bounds__(kThreads) void gqa_reduce_kernel(
   const int kvh = hq / G;
   const int j = hq - kvh * G;
   const int s = b * NKV + kvh;
-  const int nb = seg[b + 1] - seg[b];
+
+  // This wavefront's own block prefix (no LDS, no barrier): blocks before
+  // sequence b, blocks of b, and the total, 64 sequences per step.
+  const int cap_tokens = max_pages << pt_shift;
+  int seg_b = 0;
+  int nb = 0;
+  int total = 0;
+  for (int base = 0; base < B; base += kWave) {
+    const int i = base + lane;
+    int nblk = 0;
+    if (i < B) {
+      int c = ctx_lens[i];
+      c = c < 0 ? 0 : (c > cap_tokens ? cap_tokens : c);
+      nblk = (c + kBlockTokens - 1) / kBlockTokens;
+    }
+    const int x = wave_inclusive_scan(nblk, lane);
+    if (b >= base && b < base + kWave) {
+      seg_b = total + __builtin_amdgcn_readlane(x - nblk, b - base);
+      nb = __builtin_amdgcn_readlane(nblk, b - base);
+    }
+    total += __builtin_amdgcn_readlane(x, kWave - 1);
+  }
   uint16_t* ob = out + static_cast<size_t>(task) * D;
   if (nb == 0) {
 #pragma unroll
@@ -405,59 +422,63 @@ __global__ __launch_bounds__(kThreads) void gqa_reduce_kernel(
     if (lse_out != nullptr && lane == 0) lse_out[task] = -INFINITY;
     return;
   }
-  const long long U = static_cast<long long>(seg[B]) * NKV;
+  const long long U = static_cast<long long>(total) * NKV;
   const int We = static_cast<int>(U < W ? U : W);
-  const long long us = static_cast<long long>(seg[b]) * NKV + static_cast<long long>(kvh) * nb;
+  const long long us = static_cast<long long>(seg_b) * NKV + static_cast<long long>(kvh) * nb;
   const long long p0 = s + wave_of_unit(us, U, We);
   const int n = static_cast<int>(wave_of_unit(us + nb - 1, U, We) + s - p0) + 1;
 
-  // Single pass over chunks of 64 partials: lane i holds partial i's (m, l);
-  // the chunk's maximum rescales the running state, then the partial outputs
-  // are accumulated with every load of a group of four in flight.
+  // Single pass over batches of kBatch partials.  Every load of a batch --
+  // lane i's (m, l) of partial i and all kBatch partial rows of this lane's
+  // dims -- is issued before the first use, so a batch costs one memory
+  // round trip; the batch maximum then rescales the running state.  Indices
+  // past n are clamped to the last partial (always written) and weighted 0.
+  constexpr int kBatch = D == 128 ? 32 : 64;
   const float2* ml2 = reinterpret_cast<const float2*>(part_ml);
   float M = -INFINITY;
   float L = 0.f;
   float acc[DPL];
 #pragma unroll
   for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
-  for (int i0 = 0; i0 < n; i0 += kWave) {
+  for (int i0 = 0; i0 < n; i0 += kBatch) {
     const int i = i0 + lane;
-    const float2 mi = i < n ? ml2[(p0 + i) * G + j] : make_float2(-INFINITY, 0.f);
-    float Mc = mi.x;
+    const bool live = lane < kBatch && i < n;
+    const float2 mi = ml2[(p0 + (live ? i : n - 1)) * G + j];
+    float v[kBatch][DPL];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int k = i0 + u < n ? i0 + u : n - 1;
+      const float* po = part_o + ((p0 + k) * G + j) * D + lane * DPL;
+      if constexpr (DPL == 2) {
+        const float2 t = *reinterpret_cast<const float2*>(po);
+        v[u][0] = t.x;
+        v[u][1] = t.y;
+      } else {
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) v[u][d] = po[d];
+      }
+    }
+    // Keep the scheduler from sinking each load next to its use (which would
+    // serialise kBatch round trips): everything above issues first.
+    __builtin_amdgcn_sched_barrier(0);
+    float Mc = live ? mi.x : -INFINITY;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, o));
     const float Mn = fmaxf(M, Mc);
     const float rescale = fast_exp2(M - Mn);
-    const float wl = i < n ? fast_exp2(mi.x - Mn) : 0.f;
-    float Lc = mi.y * wl;
+    const float wl = live ? fast_exp2(mi.x - Mn) : 0.f;
+    float Lc = live ? mi.y * wl : 0.f;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) Lc += __shfl_xor(Lc, o);
     L = L * rescale + Lc;
     M = Mn;
 #pragma unroll
     for (int d = 0; d < DPL; ++d) acc[d] *= rescale;
-    const int cnt = n - i0 < kWave ? n - i0 : kWave;
-    int k = 0;
-    for (; k + 4 <= cnt; k += 4) {
-      float v[4][DPL];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float* po = part_o + ((p0 + i0 + k + u) * G + j) * D + lane * DPL;
+    for (int u = 0; u < kBatch; ++u) {
+      const float wk = __shfl(wl, u);
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) v[u][d] = po[d];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float wk = __shfl(wl, k + u);
-#pragma unroll
-        for (int d = 0; d < DPL; ++d) acc[d] += v[u][d] * wk;
-      }
-    }
-    for (; k < cnt; ++k) {
-      const float wk = __shfl(wl, k);
-      const float* po = part_o + ((p0 + i0 + k) * G + j) * D + lane * DPL;
-#pragma unroll
-      for (int d = 0; d < DPL; ++d) acc[d] += po[d] * wk;
+      for (int d = 0; d < DPL; ++d) acc[d] += v[u][d] * wk;
     }
   }
   const float inv = 1.f / L;
@@ -515,6 +536,112 @@ extern "C" size_t voom_paged_gqa_workspace_bytes(int batch, int num_q_heads, int
   return ((o_bytes + 255) & ~size_t(255)) + ml_bytes;
 }
 
+namespace voom {
+namespace {
+
+// Validated geometry and workspace carving shared by the decode halves.
+struct GqaPlan {
+  int B, NQ, NKV, G, D, max_pages, pt_shift, num_splits;
+  float* part_o;
+  float* part_ml;
+};
+
+int plan_gqa(const char* who, void* workspace, size_t ws_bytes, int batch, int num_q_heads,
+             int num_kv_heads, int head_dim, int page_tokens, int max_pages, int num_splits,
+             GqaPlan* p) {
+  VOOM_REQUIRE(workspace != nullptr, "%s: null workspace", who);
+  VOOM_REQUIRE(batch > 0 && batch <= kMaxBatch, "%s: batch %d not in [1, %d]", who, batch,
+               kMaxBatch);
+  VOOM_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0,
+               "%s: num_q_heads %d not a multiple of num_kv_heads %d", who, num_q_heads,
+               num_kv_heads);
+  const int G = num_q_heads / num_kv_heads;
+  VOOM_REQUIRE(G <= 16, "%s: GQA group %d exceeds 16", who, G);
+  VOOM_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim %d unsupported (64 or 128)",
+               who, head_dim);
+  VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens >= 32 && page_tokens <= 4096,
+               "%s: page_tokens %d must be a power of two in [32, 4096]", who, page_tokens);
+  VOOM_REQUIRE(max_pages > 0, "%s: empty block table", who);
+  VOOM_REQUIRE(static_cast<long long>(max_pages) * page_tokens < (1LL << 30),
+               "%s: table capacity too large", who);
+  if (num_splits <= 0) num_splits = voom_paged_gqa_default_splits();
+  VOOM_REQUIRE(num_splits <= (1 << 22), "%s: num_splits %d too large", who, num_splits);
+  const size_t need = voom_paged_gqa_workspace_bytes(batch, num_q_heads, num_kv_heads,
+                                                      head_dim, num_splits);
+  VOOM_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < required %zu", who, ws_bytes,
+               need);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "%s: workspace must be 16-byte aligned", who);
+  const size_t slots = part_slots(batch, num_kv_heads, num_splits);
+  const size_t o_bytes = slots * G * head_dim * sizeof(float);
+  p->B = batch;
+  p->NQ = num_q_heads;
+  p->NKV = num_kv_heads;
+  p->G = G;
+  p->D = head_dim;
+  p->max_pages = max_pages;
+  p->pt_shift = ilog2(page_tokens);
+  p->num_splits = num_splits;
+  p->part_o = static_cast<float*>(workspace);
+  p->part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                        ((o_bytes + 255) & ~size_t(255)));
+  return VOOM_OK;
+}
+
+int launch_partials(const GqaPlan& p, const void* q, const void* k_pool, const void* v_pool,
+                    const int32_t* block_table, const int32_t* ctx_lens, int num_slots,
+                    float scale, hipStream_t stream) {
+  const float scale_log2e = scale * 1.4426950408889634f;
+  const dim3 grid((p.num_splits + kWavesPerBlock - 1) / kWavesPerBlock);
+  const auto* qq = static_cast<const uint16_t*>(q);
+  const auto* kp = static_cast<const uint16_t*>(k_pool);
+  const auto* vp = static_cast<const uint16_t*>(v_pool);
+  if (p.D == 128) {
+    hipLaunchKernelGGL((gqa_decode_kernel<128, kNbuf128, kWavesPerEu128>), grid,
+                       dim3(kThreads), 0, stream, qq, kp, vp, block_table, ctx_lens, p.part_o,
+                       p.part_ml, p.B, p.NKV, p.G, p.max_pages, p.pt_shift, num_slots,
+                       scale_log2e, p.num_splits);
+  } else {
+    hipLaunchKernelGGL((gqa_decode_kernel<64, kNbuf64, kWavesPerEu64>), grid, dim3(kThreads),
+                       0, stream, qq, kp, vp, block_table, ctx_lens, p.part_o, p.part_ml, p.B,
+                       p.NKV, p.G, p.max_pages, p.pt_shift, num_slots, scale_log2e,
+                       p.num_splits);
+  }
+  return VOOM_LAUNCH_CHECK("paged_gqa: partials kernel launch");
+}
+
+int launch_combine(const GqaPlan& p, const int32_t* ctx_lens, void* out, float* lse_out,
+                   hipStream_t stream) {
+  const dim3 grid((p.B * p.NQ + kWavesPerBlock - 1) / kWavesPerBlock);
+  auto* oo = static_cast<uint16_t*>(out);
+  if (p.D == 128) {
+    hipLaunchKernelGGL((gqa_reduce_kernel<128>), grid, dim3(kThreads), 0, stream, p.part_o,
+                       p.part_ml, ctx_lens, oo, lse_out, p.B, p.NKV, p.G, p.max_pages,
+                       p.pt_shift, p.num_splits);
+  } else {
+    hipLaunchKernelGGL((gqa_reduce_kernel<64>), grid, dim3(kThreads), 0, stream, p.part_o,
+                       p.part_ml, ctx_lens, oo, lse_out, p.B, p.NKV, p.G, p.max_pages,
+                       p.pt_shift, p.num_splits);
+  }
+  return VOOM_LAUNCH_CHECK("paged_gqa: combine kernel launch");
+}
+
+int check_partials_args(const char* who, const void* q, const void* k_pool,
+                        const void* v_pool, const int32_t* block_table,
+                        const int32_t* ctx_lens, int num_slots) {
+  VOOM_REQUIRE(q && k_pool && v_pool && block_table && ctx_lens,
+               "%s: null pointer argument", who);
+  VOOM_REQUIRE(num_slots > 0, "%s: empty page pool", who);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(k_pool) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(v_pool) % 16 == 0,
+               "%s: q and pools must be 16-byte aligned", who);
+  return VOOM_OK;
+}
+
+}  // namespace
+}  // namespace voom
+
 extern "C" int voom_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                                      const int32_t* block_table, const int32_t* ctx_lens,
                                      void* out, float* lse_out, void* workspace,
@@ -522,69 +649,47 @@ extern "C" int voom_paged_gqa_decode(const void* q, const void* k_pool, const vo
                                      int num_kv_heads, int head_dim, int page_tokens,
                                      int max_pages, int num_slots, float scale,
                                      int num_splits, hipStream_t stream) {
-  VOOM_REQUIRE(q && k_pool && v_pool && block_table && ctx_lens && out && workspace,
-               "paged_gqa_decode: null pointer argument");
-  VOOM_REQUIRE(batch > 0 && batch <= kMaxBatch, "paged_gqa_decode: batch %d not in [1, %d]",
-               batch, kMaxBatch);
-  VOOM_REQUIRE(num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0,
-               "paged_gqa_decode: num_q_heads %d not a multiple of num_kv_heads %d",
-               num_q_heads, num_kv_heads);
-  const int G = num_q_heads / num_kv_heads;
-  VOOM_REQUIRE(G <= 16, "paged_gqa_decode: GQA group %d exceeds 16", G);
-  VOOM_REQUIRE(head_dim == 64 || head_dim == 128,
-               "paged_gqa_decode: head_dim %d unsupported (64 or 128)", head_dim);
-  VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens >= 32 && page_tokens <= 4096,
-               "paged_gqa_decode: page_tokens %d must be a power of two in [32, 4096]",
-               page_tokens);
-  VOOM_REQUIRE(max_pages > 0 && num_slots > 0, "paged_gqa_decode: empty table or pool");
-  VOOM_REQUIRE(static_cast<long long>(max_pages) * page_tokens < (1LL << 30),
-               "paged_gqa_decode: table capacity too large");
-  if (num_splits <= 0) num_splits = voom_paged_gqa_default_splits();
-  VOOM_REQUIRE(num_splits <= (1 << 22), "paged_gqa_decode: num_splits %d too large",
-               num_splits);
-  const size_t need = voom_paged_gqa_workspace_bytes(batch, num_q_heads, num_kv_heads,
-                                                      head_dim, num_splits);
-  VOOM_REQUIRE(ws_bytes >= need, "paged_gqa_decode: workspace %zu bytes < required %zu",
-               ws_bytes, need);
-  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(k_pool) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(v_pool) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
-               "paged_gqa_decode: q, pools and workspace must be 16-byte aligned");
+  const char* who = "paged_gqa_decode";
+  int rc = check_partials_args(who, q, k_pool, v_pool, block_table, ctx_lens, num_slots);
+  if (rc) return rc;
+  VOOM_REQUIRE(out != nullptr, "%s: null output", who);
+  GqaPlan p;
+  rc = plan_gqa(who, workspace, ws_bytes, batch, num_q_heads, num_kv_heads, head_dim,
+                page_tokens, max_pages, num_splits, &p);
+  if (rc) return rc;
+  rc = launch_partials(p, q, k_pool, v_pool, block_table, ctx_lens, num_slots, scale, stream);
+  if (rc) return rc;
+  return launch_combine(p, ctx_lens, out, lse_out, stream);
+}
 
-  const size_t slots = part_slots(batch, num_kv_heads, num_splits);
-  float* part_o = static_cast<float*>(workspace);
-  const size_t o_bytes = slots * G * head_dim * sizeof(float);
-  float* part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                            ((o_bytes + 255) & ~size_t(255)));
-  const int pt_shift = ilog2(page_tokens);
-  const float scale_log2e = scale * 1.4426950408889634f;
-  const dim3 grid_main((num_splits + kWavesPerBlock - 1) / kWavesPerBlock);
-  const dim3 grid_red((batch * num_q_heads + kWavesPerBlock - 1) / kWavesPerBlock);
-  const auto* qq = static_cast<const uint16_t*>(q);
-  const auto* kp = static_cast<const uint16_t*>(k_pool);
-  const auto* vp = static_cast<const uint16_t*>(v_pool);
-  auto* oo = static_cast<uint16_t*>(out);
-  if (head_dim == 128) {
-    hipLaunchKernelGGL((gqa_decode_kernel<128, kNbuf128, kWavesPerEu128>), grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
-                       block_table, ctx_lens, part_o, part_ml, batch, num_kv_heads, G,
-                       max_pages, pt_shift, num_slots, scale_log2e, num_splits);
-    int rc = VOOM_LAUNCH_CHECK("paged_gqa_decode: main kernel launch");
-    if (rc) return rc;
-    hipLaunchKernelGGL((gqa_reduce_kernel<128>), grid_red, dim3(kThreads), 0, stream, part_o,
-                       part_ml, ctx_lens, oo, lse_out, batch, num_kv_heads, G, max_pages,
-                       pt_shift, num_splits);
-  } else {
-    hipLaunchKernelGGL((gqa_decode_kernel<64, kNbuf64, kWavesPerEu64>), grid_main, dim3(kThreads), 0, stream, qq, kp, vp,
-                       block_table, ctx_lens, part_o, part_ml, batch, num_kv_heads, G,
-                       max_pages, pt_shift, num_slots, scale_log2e, num_splits);
-    int rc = VOOM_LAUNCH_CHECK("paged_gqa_decode: main kernel launch");
-    if (rc) return rc;
-    hipLaunchKernelGGL((gqa_reduce_kernel<64>), grid_red, dim3(kThreads), 0, stream, part_o,
-                       part_ml, ctx_lens, oo, lse_out, batch, num_kv_heads, G, max_pages,
-                       pt_shift, num_splits);
-  }
-  return VOOM_LAUNCH_CHECK("paged_gqa_decode: reduce kernel launch");
+extern "C" int voom_paged_gqa_partials(const void* q, const void* k_pool, const void* v_pool,
+                                       const int32_t* block_table, const int32_t* ctx_lens,
+                                       void* workspace, size_t ws_bytes, int batch,
+                                       int num_q_heads, int num_kv_heads, int head_dim,
+                                       int page_tokens, int max_pages, int num_slots,
+                                       float scale, int num_splits, hipStream_t stream) {
+  const char* who = "paged_gqa_partials";
+  int rc = check_partials_args(who, q, k_pool, v_pool, block_table, ctx_lens, num_slots);
+  if (rc) return rc;
+  GqaPlan p;
+  rc = plan_gqa(who, workspace, ws_bytes, batch, num_q_heads, num_kv_heads, head_dim,
+                page_tokens, max_pages, num_splits, &p);
+  if (rc) return rc;
+  return launch_partials(p, q, k_pool, v_pool, block_table, ctx_lens, num_slots, scale, stream);
+}
+
+extern "C" int voom_paged_gqa_combine(const int32_t* ctx_lens, void* out, float* lse_out,
+                                      void* workspace, size_t ws_bytes, int batch,
+                                      int num_q_heads, int num_kv_heads, int head_dim,
+                                      int page_tokens, int max_pages, int num_splits,
+                                      hipStream_t stream) {
+  const char* who = "paged_gqa_combine";
+  VOOM_REQUIRE(ctx_lens && out, "%s: null pointer argument", who);
+  GqaPlan p;
+  const int rc = plan_gqa(who, workspace, ws_bytes, batch, num_q_heads, num_kv_heads,
+                          head_dim, page_tokens, max_pages, num_splits, &p);
+  if (rc) return rc;
+  return launch_combine(p, ctx_lens, out, lse_out, stream);
 }
 
 extern "C" int voom_merge_attn_states(const void* o_a, const float* lse_a, const void* o_b,

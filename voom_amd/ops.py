@@ -66,21 +66,8 @@ def gqa_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_di
                                                         head_dim, num_splits))
 
 
-def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
-                     block_table: torch.Tensor, ctx_lens: torch.Tensor, *,
-                     scale: float | None = None, out: torch.Tensor | None = None,
-                     return_lse: bool = False, num_splits: int | None = None,
-                     ws: torch.Tensor | None = None,
-                     stream: torch.cuda.Stream | None = None):
-    """Decode attention of one query token per sequence over paged K/V.
-
-    q [B, NQ, D] (or [B, NQ, 1, D]) bf16; pools as in the module docstring;
-    block_table [B, max_pages] int32; ctx_lens [B] int32.  Returns out with q's
-    shape (and the fp32 natural-log LSE [B, NQ] when ``return_lse``).
-    Mirrors softmax(q.K^T*scale).V over the concatenated pages
-    (runtime/kv_paged.py:164-181, runtime/layer_runner.py:179-180).
-    """
-    q_shape = q.shape
+def _gqa_plan(q, k_pool, v_pool, block_table, ctx_lens, out, scale, num_splits, ws):
+    """Validate a paged GQA decode call; returns (q3, dims tuple, scale, splits, ws, need)."""
     if q.dim() == 4:
         _require(q.shape[2] == 1, "paged_gqa_decode handles one query token per sequence")
         q = q.reshape(q.shape[0], q.shape[1], q.shape[3])
@@ -111,14 +98,65 @@ def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     if ws is None:
         ws = workspace(dev, need, tag=1)
     _require(ws.numel() * ws.element_size() >= need, "workspace too small")
+    return q, (B, NQ, NKV, D, PT, max_pages, slots), float(scale), int(num_splits), ws, need
+
+
+def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                     block_table: torch.Tensor, ctx_lens: torch.Tensor, *,
+                     scale: float | None = None, out: torch.Tensor | None = None,
+                     return_lse: bool = False, num_splits: int | None = None,
+                     ws: torch.Tensor | None = None,
+                     stream: torch.cuda.Stream | None = None):
+    """Decode attention of one query token per sequence over paged K/V.
+
+    q [B, NQ, D] (or [B, NQ, 1, D]) bf16; pools as in the module docstring;
+    block_table [B, max_pages] int32; ctx_lens [B] int32.  Returns out with q's
+    shape (and the fp32 natural-log LSE [B, NQ] when ``return_lse``).
+    Mirrors softmax(q.K^T*scale).V over the concatenated pages
+    (runtime/kv_paged.py:164-181, runtime/layer_runner.py:179-180).
+    """
+    q_shape = q.shape
+    q, (B, NQ, NKV, D, PT, max_pages, slots), scale, num_splits, ws, need = _gqa_plan(
+        q, k_pool, v_pool, block_table, ctx_lens, out, scale, num_splits, ws)
     if out is None:
-        out = torch.empty((B, NQ, D), dtype=torch.bfloat16, device=dev)
-    lse = torch.empty((B, NQ), dtype=torch.float32, device=dev) if return_lse else None
+        out = torch.empty((B, NQ, D), dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty((B, NQ), dtype=torch.float32, device=q.device) if return_lse else None
     _lib.call("voom_paged_gqa_decode", _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table),
               _ptr(ctx_lens), _ptr(out), _ptr(lse), _ptr(ws), need, B, NQ, NKV, D, PT,
-              max_pages, slots, float(scale), int(num_splits), _stream(stream))
+              max_pages, slots, scale, num_splits, _stream(stream))
     out = out.reshape(q_shape)
     return (out, lse) if return_lse else out
+
+
+def paged_gqa_partials(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                       block_table: torch.Tensor, ctx_lens: torch.Tensor, *,
+                       scale: float | None = None, num_splits: int | None = None,
+                       ws: torch.Tensor | None = None,
+                       stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """First half of paged_gqa_decode: the page-streaming kernel, leaving the
+    partial softmax states in ``ws`` (returned).  Pair with paged_gqa_combine
+    using the same geometry, num_splits and workspace."""
+    q, (B, NQ, NKV, D, PT, max_pages, slots), scale, num_splits, ws, need = _gqa_plan(
+        q, k_pool, v_pool, block_table, ctx_lens, None, scale, num_splits, ws)
+    _lib.call("voom_paged_gqa_partials", _ptr(q), _ptr(k_pool), _ptr(v_pool),
+              _ptr(block_table), _ptr(ctx_lens), _ptr(ws), need, B, NQ, NKV, D, PT, max_pages,
+              slots, scale, num_splits, _stream(stream))
+    return ws
+
+
+def paged_gqa_combine(ctx_lens: torch.Tensor, out: torch.Tensor, ws: torch.Tensor, *,
+                      num_kv_heads: int, page_tokens: int, max_pages: int, num_splits: int,
+                      lse: torch.Tensor | None = None,
+                      stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Second half of paged_gqa_decode: merge the partial states in ``ws`` into
+    out [B, NQ, D] bf16 (and lse [B, NQ] fp32 when given)."""
+    _require_device(ctx_lens, out, ws, lse)
+    B, NQ, D = out.shape
+    need = gqa_workspace_bytes(B, NQ, num_kv_heads, D, num_splits)
+    _require(ws.numel() * ws.element_size() >= need, "workspace too small")
+    _lib.call("voom_paged_gqa_combine", _ptr(ctx_lens), _ptr(out), _ptr(lse), _ptr(ws), need, B,
+              NQ, num_kv_heads, D, page_tokens, max_pages, num_splits, _stream(stream))
+    return out
 
 
 def merge_attn_states(o_a: torch.Tensor, lse_a: torch.Tensor, o_b: torch.Tensor,
