@@ -11,6 +11,9 @@ introspection its tests use, and adds the explicit verbs of the paged path:
   attend(layer, q, scale)  fused paged decode attention (HIP kernel); spilled
                            pages are reloaded on a side stream while the
                            resident pages are attended, then LSE-merged
+  attend_prefill(layer, q) causal attention of a prompt through the same kernel
+  append_latent / update_latent / attend_mla
+                           the absorbed-MLA latent cache (runtime/glm.py:265-330)
   spill(pages)             byte-plane split on the GPU -> D2H into the arena
   reload(pages)            H2D -> byte-plane merge into fresh pool slots
 
@@ -258,6 +261,7 @@ class PagedKVCache:
         self._open_slots: list[dict[int, list[int]]] = [{} for _ in range(L)]
         self._len = [0] * L
         self._offset = 0
+        self._resident_closed = 0  # closed pages held in device slots, all layers
         self._pools: list[DevicePagePool | None] = [None] * L
         self._stage_pools: list[DevicePagePool | None] = [None] * L
         self._tables: list[torch.Tensor | None] = [None] * L
@@ -366,14 +370,22 @@ class PagedKVCache:
             if host is not None:
                 new[:, :host.shape[1]] = host
             self._tables_host[layer] = host = new
-            for page, slots in cols.items():
-                host[:, page] = -1 if slots is None else np.asarray(slots, np.int32)
+            self._fill_cols(host, cols)
             self._tables[layer] = self._dev_i32(host)
             return
-        for page, slots in cols.items():
-            host[:, page] = -1 if slots is None else np.asarray(slots, np.int32)
+        self._fill_cols(host, cols)
         lo, hi = min(cols), max(cols) + 1
         self._tables[layer][:, lo:hi].copy_(self._dev_i32(host[:, lo:hi]))
+
+    @staticmethod
+    def _fill_cols(host: np.ndarray, cols: dict) -> None:
+        """Write table columns in two vectorised assignments (cleared, set)."""
+        cleared = [page for page, slots in cols.items() if slots is None]
+        if cleared:
+            host[:, cleared] = -1
+        filled = [page for page, slots in cols.items() if slots is not None]
+        if filled:
+            host[:, filled] = np.asarray([cols[page] for page in filled], np.int32).T
 
     def _set_table(self, layer: int, page_idx: int, slots) -> None:
         self._set_table_cols(layer, {page_idx: slots})
@@ -391,10 +403,9 @@ class PagedKVCache:
         """Resident bytes: resident closed pages plus open-page tokens (kv_paged.py:187-194)."""
         if self._geom is None:
             return 0
-        total = 0
         tok = self._token_nbytes()
+        total = self._resident_closed * self.page_nbytes
         for layer in range(self.num_layers):
-            total += sum(p.nbytes for p in self._pages[layer] if p.resident)
             total += (self._len[layer] - len(self._pages[layer]) * self.page_positions) * tok
         return total
 
@@ -447,6 +458,7 @@ class PagedKVCache:
             idx = len(pages)
             pages.append(_Page(self, layer, idx, self._open_slots[layer].pop(idx),
                                self.page_nbytes))
+            self._resident_closed += 1
         if layer == self.num_layers - 1:
             self._offset += L
             self._enforce_budget()
@@ -563,9 +575,10 @@ class PagedKVCache:
         self._spill_chunks(work)
         for layer, lp in by_layer.items():
             pool = self._pool(layer)
+            pool.release([s for p in lp for s in p.slots])
             for p in lp:
-                pool.release(p.slots)
                 p.slots = None
+            self._resident_closed -= len(lp)
             self._set_table_cols(layer, {p.index: None for p in lp})
         if self.compress_spill:
             self._compress_spilled(pages)
@@ -777,6 +790,7 @@ class PagedKVCache:
                 for j, p in enumerate(chunk):
                     p.slots = slots[j * B:(j + 1) * B]
                     acc.append(p)
+                self._resident_closed += len(chunk)
 
             jobs.append((layer, lp, self._pool(layer), adopt, False))
         self._pipeline_in(jobs)
@@ -836,6 +850,42 @@ class PagedKVCache:
                                         return_lse=lse)
 
         return self._attend_pages(layer, run)
+
+    def attend_prefill(self, layer: int, q: torch.Tensor,
+                       scale: float | None = None) -> torch.Tensor:
+        """Causal attention of the layer's newest L tokens: q [B, NQ, L, D] holds
+        the queries of positions S-L .. S-1, whose K/V were just appended.
+
+        The reference masks a multi-token window explicitly (k_pos <= q_pos,
+        runtime/layer_runner.py:166-177).  Here every query row becomes its own
+        entry of one paged decode call -- the same block-table row, with the
+        context cut at its own position + 1 -- so a prompt runs through the
+        paged kernel in one launch per 1024 query rows.  Spilled pages of the
+        layer are made resident first.
+        """
+        self._require_kind(layer, "kv")
+        B, NQ, L, D = q.shape
+        S = self._len[layer]
+        if L > S:
+            raise ValueError(f"{L} queries but the layer holds {S} tokens")
+        if scale is None:
+            scale = D ** -0.5
+        spilled = [p for p in self._pages[layer] if not p.resident]
+        if spilled:
+            self.reload(spilled)
+        pool = self._pool(layer)
+        rows_q = q.permute(0, 2, 1, 3).reshape(B * L, NQ, D).contiguous()
+        table = self._tables[layer].repeat_interleave(L, dim=0)
+        ctx = (torch.arange(S - L + 1, S + 1, dtype=torch.int32, device=self.device)
+               .repeat(B))
+        out = torch.empty_like(rows_q)
+        step = 1024  # rows per launch (the kernel's batch limit)
+        for r0 in range(0, B * L, step):
+            r1 = min(B * L, r0 + step)
+            out[r0:r1] = ops.paged_gqa_decode(rows_q[r0:r1], pool.k, pool.v,
+                                              table[r0:r1].contiguous(), ctx[r0:r1].contiguous(),
+                                              scale=scale)
+        return out.reshape(B, L, NQ, D).permute(0, 2, 1, 3)
 
     def attend_mla(self, layer: int, q_nope: torch.Tensor, q_rope: torch.Tensor,
                    w_uk: torch.Tensor, w_uv_t: torch.Tensor, scale: float,

@@ -101,11 +101,10 @@ class DevicePagePool:
         return ids
 
     def release(self, ids) -> None:
-        for i in ids:
-            i = int(i)
-            if not 0 <= i < self.capacity:
-                raise RuntimeError(f"slot {i} outside the pool")
-            self._free.append(i)
+        ids = [int(i) for i in ids]
+        if ids and not (0 <= min(ids) and max(ids) < self.capacity):
+            raise RuntimeError(f"slot outside the pool (capacity {self.capacity})")
+        self._free.extend(ids)
         self._live -= len(ids)
         if self._live < 0:
             raise RuntimeError("page pool released more slots than it allocated")
