@@ -238,3 +238,47 @@ def test_latent_reload_restores_pages_bitwise():
     for p, o in zip(kv._pages[0], originals):
         assert p.resident and torch.equal(bits(p.load()[0]), bits(o))
     torch.cuda.synchronize()
+
+
+def test_prefetched_uploads_match_fresh_ones_through_cache_changes():
+    print("[kv] cross-layer prefetch vs no prefetch, with spills and reloads between", flush=True)
+    B, NQ, NKV, D, PT, layers = 2, 8, 2, 128, 64, 3
+    outs = {}
+    for prefetch in (True, False):
+        gen = torch.Generator(device="cuda").manual_seed(7)
+        kv = PagedKVCache(num_layers=layers, max_bytes=1 << 40, page_positions=PT,
+                          resident_pages=1, prefetch=prefetch)
+        ks = [[] for _ in range(layers)]
+        vs = [[] for _ in range(layers)]
+        res = []
+        for step, n in enumerate((400, 1, 1, 70, 1, 1)):
+            for layer in range(layers):
+                k = torch.randn((B, NKV, n, D), generator=gen, device="cuda").to(torch.bfloat16)
+                v = torch.randn((B, NKV, n, D), generator=gen, device="cuda").to(torch.bfloat16)
+                ks[layer].append(k)
+                vs[layer].append(v)
+                kv.append(layer, k, v)
+            if step == 0:
+                kv.spill([(l, i) for l in range(layers) for i in range(0, 5)])
+            if step == 3:
+                kv.reload([(1, 2), (2, 0)])
+                kv.spill([(0, 5), (2, 6)])
+            for layer in range(layers):
+                q = torch.randn((B, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+                out = kv.attend(layer, q)
+                res.append(out.clone())
+                if prefetch:
+                    ref = attn_oracle(q, torch.cat(ks[layer], 2), torch.cat(vs[layer], 2),
+                                      D ** -0.5)
+                    torch.cuda.synchronize()
+                    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL,
+                                               rtol=RTOL)
+        torch.cuda.synchronize()
+        outs[prefetch] = res
+        if prefetch:
+            assert kv.prefetch_hits > 0
+        else:
+            assert kv.prefetch_hits == 0
+        kv.release()
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(bits(a), bits(b))

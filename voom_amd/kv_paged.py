@@ -227,7 +227,7 @@ class PagedKVCache:
     def __init__(self, num_layers: int, max_bytes: int, spill_dir: str | Path | None = None,
                  page_positions: int = 256, resident_pages: int = 1,
                  compress_spill: bool = False, *, device=None, initial_slots: int = 0,
-                 arena: HostArena | None = None):
+                 arena: HostArena | None = None, prefetch: bool = True):
         if num_layers <= 0:
             raise ValueError("num_layers must be positive")
         if page_positions <= 0 or page_positions & (page_positions - 1):
@@ -250,6 +250,11 @@ class PagedKVCache:
         self._copy_stream: torch.cuda.Stream | None = None
         self._ring = _StagingRing(self.device)
         self._i32_cache: OrderedDict = OrderedDict()
+        # attend(layer) starts the upload of the next layer's first spilled
+        # chunk, so host-link time overlaps the compute in between
+        self.prefetch = prefetch
+        self.prefetch_hits = 0
+        self._prefetched: dict = {}
         self._reset_state()
 
     # ---- state ------------------------------------------------------------
@@ -263,7 +268,10 @@ class PagedKVCache:
         self._offset = 0
         self._resident_closed = 0  # closed pages held in device slots, all layers
         self._pools: list[DevicePagePool | None] = [None] * L
-        self._stage_pools: list[DevicePagePool | None] = [None] * L
+        # one transient staging pool shared by all layers: every transient
+        # merge and every read of it is ordered on the main stream
+        self._stage: DevicePagePool | None = None
+        self._drop_prefetch()
         self._tables: list[torch.Tensor | None] = [None] * L
         self._tables_host: list[np.ndarray | None] = [None] * L
         # ("kv", B, NKV, D) or ("latent", B, latent_dim), fixed by the first write
@@ -312,11 +320,9 @@ class PagedKVCache:
         return pool
 
     def _stage_pool(self, layer: int) -> DevicePagePool:
-        pool = self._stage_pools[layer]
-        if pool is None:
-            pool = self._new_pool(min_grow=16)
-            self._stage_pools[layer] = pool
-        return pool
+        if self._stage is None:
+            self._stage = self._new_pool(min_grow=16)
+        return self._stage
 
     def _stream(self) -> torch.cuda.Stream:
         if self._copy_stream is None:
@@ -620,7 +626,7 @@ class PagedKVCache:
             for pool, cp, sb, rec in work[w0:w0 + nbuf]:
                 m = len(cp)
                 slot_t = self._dev_i32([s for p in cp for s in p.slots])
-                idx, buf = self._ring.acquire(main, m * sb.page_bytes)
+                idx, buf = self._acquire(main, m * sb.page_bytes)
                 for t, tensor in enumerate(pool.tensors):
                     lo, hi = _planes(buf, sb.parts, m, t)
                     if ops.slot_codec_supported(tensor):
@@ -700,6 +706,63 @@ class PagedKVCache:
                 ops.byteplane_merge(lo, hi, staged)
                 tensor.index_copy_(0, slot_t.long(), staged)
 
+    @staticmethod
+    def _chunk_sig(pages: list[_Page]) -> tuple:
+        return tuple((id(p.host), p.host_j) for p in pages)
+
+    def _acquire(self, writer: torch.cuda.Stream, nbytes: int):
+        """Next staging buffer; an upload started ahead into it is given up
+        first (the writer then waits for that copy to land)."""
+        idx = self._ring.i
+        for layer, (_, (pidx, _buf, ev)) in list(self._prefetched.items()):
+            if pidx == idx:
+                del self._prefetched[layer]
+                self._ring.free_ev[idx] = ev
+        return self._ring.acquire(writer, nbytes)
+
+    def _drop_prefetch(self) -> None:
+        """Forget uploads started ahead; their buffers free once the copy lands."""
+        for _, (idx, _buf, ev) in getattr(self, "_prefetched", {}).values():
+            self._ring.free_ev[idx] = ev
+        self._prefetched = {}
+
+    def _take_prefetch(self, layer: int, pages: list[_Page]):
+        """(ring idx, buffer, landed event) of an upload of exactly ``pages``
+        started ahead for this layer, or None (a stale one is dropped)."""
+        hit = self._prefetched.pop(layer, None)
+        if hit is None:
+            return None
+        sig, landed = hit
+        if sig == self._chunk_sig(pages):
+            self.prefetch_hits += 1
+            return landed
+        self._ring.free_ev[landed[0]] = landed[2]
+        return None
+
+    def _prefetch(self, layer: int) -> None:
+        """Start uploading the first chunk of ``layer``'s spilled pages into a
+        staging buffer on the side stream; the layer's next transient reload
+        (attend, gather, load) merges it instead of uploading again.  Spilled
+        pages are immutable while spilled, and any spill or reload in between
+        changes the chunk, which discards the upload."""
+        if not self.prefetch or layer in self._prefetched or self._geom is None:
+            return
+        spilled = [p for p in self._pages[layer] if not p.resident]
+        if not spilled:
+            return
+        parts = self._plane_parts(self._stage_pool(layer))
+        per_chunk = max(1, self._ring.nbytes // (2 * sum(parts)))
+        cp = spilled[:per_chunk]
+        copy = self._stream()
+        for sb in {id(p.host): p.host for p in cp}.values():
+            copy.wait_event(sb.ready)
+        idx, buf = self._acquire(copy, 2 * len(cp) * sum(parts))
+        with torch.cuda.stream(copy):
+            self._upload_planes(cp, buf, parts)
+        ev = torch.cuda.Event()
+        ev.record(copy)
+        self._prefetched[layer] = (self._chunk_sig(cp), (idx, buf, ev))
+
     def _stream_in(self, layer: int, pages: list[_Page], target: DevicePagePool, consume,
                    transient: bool) -> None:
         """Bring spilled pages of one layer into ``target``, chunk by chunk."""
@@ -734,20 +797,24 @@ class PagedKVCache:
             for sb in {id(p.host): p.host for p in pages}.values():
                 copy.wait_event(sb.ready)
             for c0 in range(0, len(pages), per_chunk):
-                chunks.append((pages[c0:c0 + per_chunk], target, consume, transient, parts,
-                               per_chunk))
+                cp = pages[c0:c0 + per_chunk]
+                ahead = self._take_prefetch(layer, cp) if transient and c0 == 0 else None
+                chunks.append((cp, target, consume, transient, parts, per_chunk, ahead))
             n_pages += len(pages)
         for w0 in range(0, len(chunks), nbuf):
             window = chunks[w0:w0 + nbuf]
             landed = []
-            for cp, target, consume, transient, parts, per_chunk in window:
-                idx, buf = self._ring.acquire(copy, 2 * len(cp) * sum(parts))
+            for cp, target, consume, transient, parts, per_chunk, ahead in window:
+                if ahead is not None:
+                    landed.append(ahead)
+                    continue
+                idx, buf = self._acquire(copy, 2 * len(cp) * sum(parts))
                 with torch.cuda.stream(copy):
                     self._upload_planes(cp, buf, parts)
                 ev = torch.cuda.Event()
                 ev.record(copy)
                 landed.append((idx, buf, ev))
-            for (cp, target, consume, transient, parts, per_chunk), (idx, buf, ev) in zip(
+            for (cp, target, consume, transient, parts, per_chunk, _), (idx, buf, ev) in zip(
                     window, landed):
                 main.wait_event(ev)
                 m = len(cp)
@@ -921,7 +988,11 @@ class PagedKVCache:
         spilled = [p for p in self._pages[layer] if not p.resident]
         if not spilled:
             ctx = torch.full((B,), S, dtype=torch.int32, device=self.device)
-            return run(pool, self._tables[layer], ctx, False)
+            out = run(pool, self._tables[layer], ctx, False)
+            self._prefetch((layer + 1) % self.num_layers)
+            return out
+        # the first chunk's upload goes first, ahead of the resident attention
+        self._prefetch(layer)
         PT = self.page_positions
         # Resident pages, the open page last (attention of one query token is
         # order-free; only a partial page has to be the last one).
@@ -951,4 +1022,5 @@ class PagedKVCache:
             fold(run(stage, t, c, True))
 
         self._stream_in(layer, spilled, stage, attend_chunk, transient=True)
+        self._prefetch((layer + 1) % self.num_layers)
         return state[0][0]
