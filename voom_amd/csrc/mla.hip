@@ -13,14 +13,20 @@
 //   scores^T [tokens x heads] = Lat [tokens x 576] . Q^T      v_mfma_f32_16x16x32_bf16
 //   out^T    [dims x heads]  += C^T [dims x tokens] . P^T     v_mfma_f32_16x16x32_bf16
 // Decomposition: one workgroup (8 wavefronts, 2 per SIMD) per (sequence,
-// token range, group of 32 heads).  The four head groups of a range are placed on the same
-// XCD so the latent tiles they all read are served from that XCD's L2.
+// token range, group of 64 heads; 32 when the head count is not a multiple of
+// 64).  The head groups of a range are placed on the same XCD so the latent
+// tiles they all read are served from that XCD's L2; with 64 heads a tile
+// pulled into LDS serves twice as many heads as with 32.
 // Per 64-token tile: buffer loads deliver the tile straight into LDS (no
 // register staging; the next tile streams into the second buffer while the
-// current one is used); wavefront w computes the scores of token tile w%4
-// for head tile w/4, the tile maximum is combined through LDS, P is written
-// to LDS in bf16, and wavefront w accumulates dims 64w..64w+63 of out^T for
-// all 32 heads (accumulators stay in registers for the whole range).  The C^T operand comes from the token-major tile through
+// current one is used).  The 4 token tiles x 4 head tiles of scores are split
+// over the wavefronts (2 token tiles of one head tile each), with the latent
+// rows of a k-step read two steps ahead of their MFMAs; the tile maximum of a
+// head is combined through LDS, P is written to LDS in bf16, and wavefront w
+// accumulates dims 64w..64w+63 of out^T for all heads of the group
+// (accumulators stay in registers for the whole range).  The softmax
+// normaliser is kept per lane and summed across lanes and wavefronts once,
+// after the last tile.  The C^T operand comes from the token-major tile through
 // ds_read_b64_tr_b16: in each 16-lane group, lane l receives element l%4 of
 // the 8-byte rows addressed by lanes 4c + l/4 (c = 0..3), so two transposed
 // reads give a lane the 8 tokens of one latent dim.  LDS rows are padded to
@@ -34,7 +40,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kLat = 576;          // kv_lora_rank 512 + rope dim 64
 constexpr int kC = 512;
-constexpr int kHeadsPerGroup = 32;
 constexpr int kTile = 64;          // tokens per tile
 constexpr int kChunksPerRow = kLat * 2 / 16;  // 72 sixteen-byte chunks per token
 constexpr int kRowChunks = kChunksPerRow + 1;  // padded LDS row: 73 chunks = 1168 B
@@ -64,21 +69,36 @@ constexpr int kMlaThreads = 512;  // 8 wavefronts, 2 per SIMD
 constexpr int kMlaWaves = kMlaThreads / 64;
 constexpr int kLoadsPerWave = (kLoadsPerTile + kMlaWaves - 1) / kMlaWaves;
 
-__global__ __launch_bounds__(kMlaThreads, 2) void mla_latent_kernel(MlaArgs a) {
+// HG heads per workgroup (32 or 64).  With HG = 64 each latent tile that a
+// workgroup pulls from L2 into LDS serves twice as many heads, which halves
+// the L2-to-LDS traffic per HBM byte -- the path this kernel waits on.
+//
+// Scores: the 4 token tiles x NHT head tiles of a 64-token tile are spread
+// over the 8 wavefronts, HTW head tiles x TTW token tiles each.  A latent row
+// read from LDS feeds HTW MFMAs; a wave holds q for HTW head tiles.  HTW = 1:
+// q for two head tiles (2 x 18 k-steps) would exceed the 256 registers a
+// wavefront has at 2 per SIMD.
+template <int HG>
+__global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
+  constexpr int HTW = 1;
+  constexpr int NHT = HG / 16;               // 16-head tiles in the group
+  constexpr int TTW = 4 * NHT / (8 * HTW);   // token tiles per wavefront
+  constexpr int WPH = 4 / TTW;               // wavefronts sharing one head tile's 64 tokens
+  static_assert(TTW * HTW * 8 == 4 * NHT, "score tiles must split evenly");
   __shared__ __attribute__((aligned(16))) uint16_t tile_a[kTile * kRow];
   __shared__ __attribute__((aligned(16))) uint16_t tile_b[kTile * kRow];
-  __shared__ __attribute__((aligned(16))) uint16_t p_lds[kHeadsPerGroup * kPRow];
-  __shared__ float pmax[4][kHeadsPerGroup];
-  __shared__ float psum[4][kHeadsPerGroup];
+  __shared__ __attribute__((aligned(16))) uint16_t p_lds[HG * kPRow];
+  __shared__ float pmax[WPH][HG];
+  __shared__ float psum[WPH][HG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);   // 0..7
-  const int tt = w & 3;              // score MFMA: token tile (16 tokens)
-  const int qt = w >> 2;             // score MFMA: head tile (16 heads)
+  const int qt0 = (w % (NHT / HTW)) * HTW;  // score MFMA: head tiles qt0 .. qt0+HTW-1
+  const int wg = w / (NHT / HTW);           // score MFMA: token tiles wg*TTW .. +TTW-1
   const int i16 = lane & 15;
   const int g = lane >> 4;
-  const int NHG = a.H / kHeadsPerGroup;
+  const int NHG = a.H / HG;
 
   // Block -> (task = sequence x range, head group); head groups of one task
   // share bid % 8, i.e. the same XCD.
@@ -103,41 +123,57 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_latent_kernel(MlaArgs a) {
   const int per = (n_tiles + a.NR - 1) / a.NR;
   const int t_lo = range * per;
   const int t_hi = (t_lo + per < n_tiles) ? t_lo + per : n_tiles;
-  const int head0 = hg * kHeadsPerGroup;
+  const int head0 = hg * HG;
   const int32_t* trow = a.table + static_cast<size_t>(b) * a.max_pages;
 
-  // Q^T operand of this wave's head tile, all 18 k-steps: lane (head i16,
+  // Q^T operands of this wave's head tiles, all 18 k-steps: lane (head i16,
   // group g) holds q[head][32s + 8g .. +8].
-  u32x4 qop[kQSteps];
-  {
-    const uint16_t* qh = a.q + (static_cast<size_t>(b) * a.H + head0 + 16 * qt + i16) * kLat;
+  u32x4 qop[HTW][kQSteps];
+#pragma unroll
+  for (int k = 0; k < HTW; ++k) {
+    const uint16_t* qh =
+        a.q + (static_cast<size_t>(b) * a.H + head0 + 16 * (qt0 + k) + i16) * kLat;
 #pragma unroll
     for (int s = 0; s < kQSteps; ++s) {
-      qop[s] = *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g);
+      qop[k][s] = *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g);
     }
   }
 
-  f32x4 acc[4][2];  // out^T tiles: dims 64w + 16dt.., head tile ht
+  f32x4 acc[4][NHT];  // out^T tiles: dims 64w + 16dt.., head tile ht
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
-    acc[dt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht) acc[dt][ht] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float m_run[2] = {-INFINITY, -INFINITY};  // per head tile: head 16ht + i16
-  float l_run[2] = {0.f, 0.f};
+  float m_run[NHT];  // per head tile: head 16ht + i16, common to all waves
+#pragma unroll
+  for (int ht = 0; ht < NHT; ++ht) m_run[ht] = -INFINITY;
+  // m_run of this wave's own head tiles kept apart: qt0 is known only at run
+  // time, and indexing m_run with it would move the array to scratch memory.
+  float m_own[HTW];
+  // Softmax normaliser of the own head tiles, per lane (its tokens only): the
+  // lanes and the wavefronts sharing a head are summed once, after the loop.
+  float l_lane[HTW];
+#pragma unroll
+  for (int k = 0; k < HTW; ++k) {
+    m_own[k] = -INFINITY;
+    l_lane[k] = 0.f;
+  }
 
   // Lane-constant source offsets of this wave's direct-to-LDS loads: load i
   // (i = w, w+8, ...) fills LDS chunks 64i..64i+63 of the padded tile; chunk
   // (row, col) holds bytes 16*col of token row; the padding chunk of a row
   // reads past the buffer end and lands as zeros.
-  int src_off[kLoadsPerWave];
-#pragma unroll
-  for (int k = 0; k < kLoadsPerWave; ++k) {
+  // Source offset of load k.
+  auto src_off_of = [&](int k) {
     const int j = 64 * (w + kMlaWaves * k) + lane;
     const int row = j / kRowChunks;
     const int col = j - row * kRowChunks;
-    src_off[k] = col < kChunksPerRow ? (row * kChunksPerRow + col) * 16 : 0x40000000;
-  }
+    return col < kChunksPerRow ? (row * kChunksPerRow + col) * 16 : 0x40000000;
+  };
+  int src_off[kLoadsPerWave];
+#pragma unroll
+  for (int k = 0; k < kLoadsPerWave; ++k) src_off[k] = src_off_of(k);
 
   // Block-table entries of the range's pages, one per lane, refreshed every 64
   // pages: slot lookups inside the loop are register reads, not memory trips.
@@ -178,77 +214,128 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_latent_kernel(MlaArgs a) {
     lds_barrier();
     if (t + 1 < t_hi) load_tile(t + 1, next);
 
-    // ---- scores: tokens 16tt..16tt+15 x heads 16qt..16qt+15 ----
-    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-    const uint16_t* arow = tile + (16 * tt + i16) * kRow + 8 * g;
-#pragma unroll
-    for (int s = 0; s < kQSteps; ++s) {
-      const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(arow + 32 * s));
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, qop[s]), sc, 0,
-                                                   0, 0);
-    }
-    // lane (head 16qt + i16, group g) holds tokens 16tt + 4g + r, r = 0..3
+    // ---- scores: TTW token tiles x HTW head tiles ----
     const int valid = ctx - t * kTile;
-    float x[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      x[r] = 16 * tt + 4 * g + r < valid ? sc[r] * a.scale_log2e : -INFINITY;
-    }
+    float x[TTW][HTW][4];
     {
-      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      // The latent rows of k-step s + kAhead are read while the MFMAs of
+      // step s run, so no MFMA waits on a read issued just before it.
+      constexpr int kAhead = 2;
+      const uint16_t* arow[TTW];
+      f32x4 sc[TTW][HTW];
+      u32x4 ring[kAhead + 1][TTW];
+#pragma unroll
+      for (int j = 0; j < TTW; ++j) {
+        arow[j] = tile + (16 * (wg * TTW + j) + i16) * kRow + 8 * g;
+#pragma unroll
+        for (int k = 0; k < HTW; ++k) sc[j][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int s = 0; s < kAhead; ++s) {
+#pragma unroll
+        for (int j = 0; j < TTW; ++j) ring[s][j] = *reinterpret_cast<const u32x4*>(arow[j] + 32 * s);
+      }
+#pragma unroll
+      for (int s = 0; s < kQSteps; ++s) {
+        if (s + kAhead < kQSteps) {
+#pragma unroll
+          for (int j = 0; j < TTW; ++j) {
+            ring[(s + kAhead) % (kAhead + 1)][j] =
+                *reinterpret_cast<const u32x4*>(arow[j] + 32 * (s + kAhead));
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < TTW; ++j) {
+#pragma unroll
+          for (int k = 0; k < HTW; ++k) {
+            sc[j][k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, ring[s % (kAhead + 1)][j]),
+                __builtin_bit_cast(bf16x8, qop[k][s]), sc[j][k], 0, 0, 0);
+          }
+        }
+      }
+      // lane (head 16(qt0+k) + i16, group g) holds tokens 16tt + 4g + r, r = 0..3
+#pragma unroll
+      for (int j = 0; j < TTW; ++j) {
+        const int tt = wg * TTW + j;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = 16 * tt + 4 * g + r < valid;
+#pragma unroll
+          for (int k = 0; k < HTW; ++k) x[j][k][r] = ok ? sc[j][k][r] * a.scale_log2e : -INFINITY;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < HTW; ++k) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < TTW; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, x[j][k][r]);
+      }
       mx = wave_max_across_groups(mx);
-      if (g == 0) pmax[tt][16 * qt + i16] = mx;
+      if (g == 0) pmax[wg][16 * (qt0 + k) + i16] = mx;
     }
     lds_barrier();
 
-    float alpha[2];
+    float alpha[NHT];
 #pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
+    for (int ht = 0; ht < NHT; ++ht) {
       const int hh = 16 * ht + i16;
-      const float mp = fmaxf(fmaxf(pmax[0][hh], pmax[1][hh]), fmaxf(pmax[2][hh], pmax[3][hh]));
+      float mp = pmax[0][hh];
+#pragma unroll
+      for (int k = 1; k < WPH; ++k) mp = fmaxf(mp, pmax[k][hh]);
       const float mn = fmaxf(m_run[ht], mp);
       alpha[ht] = fast_exp2(m_run[ht] - mn);
       m_run[ht] = mn;
     }
-    {
-      const int hh = 16 * qt + i16;
-      const float mn = m_run[qt];
-      float p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(x[r] - mn);
-      const uint32_t w0 = pack_bf16x2(p[0], p[1]);
-      const uint32_t w1 = pack_bf16x2(p[2], p[3]);
-      // P row of head hh: tokens 16tt+4g .. +3 in natural order
-      *reinterpret_cast<u32x2*>(p_lds + hh * kPRow + 16 * tt + 4 * g) = u32x2{w0, w1};
-      float ps = __builtin_bit_cast(float, w0 << 16) + __builtin_bit_cast(float, w0 & 0xffff0000u) +
-                 __builtin_bit_cast(float, w1 << 16) + __builtin_bit_cast(float, w1 & 0xffff0000u);
-      ps = wave_sum_across_groups(ps);
-      if (g == 0) psum[tt][hh] = ps;
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int ht = 0; ht < NHT; ++ht) acc[dt][ht] *= alpha[ht];
+    }
+#pragma unroll
+    for (int k = 0; k < HTW; ++k) {
+      const int hh = 16 * (qt0 + k) + i16;
+      float mp = pmax[0][hh];
+#pragma unroll
+      for (int kk = 1; kk < WPH; ++kk) mp = fmaxf(mp, pmax[kk][hh]);
+      const float mn = fmaxf(m_own[k], mp);
+      const float alpha_own = fast_exp2(m_own[k] - mn);
+      m_own[k] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < TTW; ++j) {
+        const int tt = wg * TTW + j;
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = fast_exp2(x[j][k][r] - m_own[k]);
+        const uint32_t w0 = pack_bf16x2(p[0], p[1]);
+        const uint32_t w1 = pack_bf16x2(p[2], p[3]);
+        // P row of head hh: tokens 16tt+4g .. +3 in natural order
+        *reinterpret_cast<u32x2*>(p_lds + hh * kPRow + 16 * tt + 4 * g) = u32x2{w0, w1};
+        ps += __builtin_bit_cast(float, w0 << 16) + __builtin_bit_cast(float, w0 & 0xffff0000u) +
+              __builtin_bit_cast(float, w1 << 16) + __builtin_bit_cast(float, w1 & 0xffff0000u);
+      }
+      l_lane[k] = l_lane[k] * alpha_own + ps;
     }
     lds_barrier();
 
-#pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
-      const int hh = 16 * ht + i16;
-      l_run[ht] = l_run[ht] * alpha[ht] + (psum[0][hh] + psum[1][hh] + psum[2][hh] + psum[3][hh]);
-    }
-
     // ---- out^T[dims 64w.., heads] += C^T . P^T ----
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      acc[dt][0] *= alpha[0];
-      acc[dt][1] *= alpha[1];
-    }
     // Transposed-read addresses: lane k of a 16-lane group supplies token row
     // 8g + (k/4) (+4 for the second read) at dims 4*(k%4) of the dim tile.
     const int trow_tok = 8 * g + (i16 >> 2);
     const int tcol = 4 * (i16 & 3);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8 pb0 = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(p_lds + i16 * kPRow + 32 * ks + 8 * g));
-      const bf16x8 pb1 = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(p_lds + (16 + i16) * kPRow + 32 * ks + 8 * g));
+      bf16x8 pb[NHT];
+#pragma unroll
+      for (int ht = 0; ht < NHT; ++ht) {
+        pb[ht] = __builtin_bit_cast(
+            bf16x8,
+            *reinterpret_cast<const u32x4*>(p_lds + (16 * ht + i16) * kPRow + 32 * ks + 8 * g));
+      }
       const uint16_t* trb = tile + (32 * ks + trow_tok) * kRow + 64 * w + tcol;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
@@ -257,8 +344,10 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_latent_kernel(MlaArgs a) {
         const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
             (lds_bf16x4*)(trb + 4 * kRow + 16 * dt));
         const bf16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb0, acc[dt][0], 0, 0, 0);
-        acc[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb1, acc[dt][1], 0, 0, 0);
+#pragma unroll
+        for (int ht = 0; ht < NHT; ++ht) {
+          acc[dt][ht] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb[ht], acc[dt][ht], 0, 0, 0);
+        }
       }
     }
   };
@@ -275,61 +364,111 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_latent_kernel(MlaArgs a) {
   // ---- partial state of this (sequence, range, head group) ----
   const size_t pbase = (static_cast<size_t>(b) * a.NR + range) * a.H + head0;
 #pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
+  for (int ht = 0; ht < NHT; ++ht) {
     const int hh = 16 * ht + i16;
     float* po = a.part_o + (pbase + hh) * kC + 64 * w + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       *reinterpret_cast<f32x4*>(po + 16 * dt) = acc[dt][ht];
     }
-    if (w == 0 && g == 0) {
+  }
+  // normaliser: lanes of a wave, then the WPH wavefronts sharing each head
+#pragma unroll
+  for (int k = 0; k < HTW; ++k) {
+    const float l = wave_sum_across_groups(l_lane[k]);
+    if (g == 0) psum[wg][16 * (qt0 + k) + i16] = l;
+  }
+  lds_barrier();
+  if (w == 0 && g == 0) {
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht) {
+      const int hh = 16 * ht + i16;
+      float l = psum[0][hh];
+#pragma unroll
+      for (int k = 1; k < WPH; ++k) l += psum[k][hh];
       a.part_ml[(pbase + hh) * 2 + 0] = m_run[ht];
-      a.part_ml[(pbase + hh) * 2 + 1] = l_run[ht];
+      a.part_ml[(pbase + hh) * 2 + 1] = l;
     }
   }
 }
 
-// One wavefront per (sequence, head): merge the NR range partials.
+// One wavefront per (sequence, head): merges the NR range partials.  Lane r
+// holds range r's (m, l); the partial rows of a batch of ranges are all loaded
+// before the first is used (one memory round trip per batch).
 __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     uint16_t* __restrict__ out, float* __restrict__ lse_out, int B, int H, int NR) {
+  constexpr int DPL = kC / 64;  // 8 dims per lane
+  constexpr int kBatch = 8;
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * (kThreads / 64) + uniform(threadIdx.x >> 6);
   if (task >= B * H) return;
   const int b = task / H;
   const int h = task - b * H;
+  const float2* ml2 = reinterpret_cast<const float2*>(part_ml);
   float M = -INFINITY;
-  for (int r = 0; r < NR; ++r) {
-    M = fmaxf(M, part_ml[((static_cast<size_t>(b) * NR + r) * H + h) * 2]);
-  }
-  constexpr int DPL = kC / 64;
-  float accv[DPL];
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) accv[d] = 0.f;
   float L = 0.f;
-  if (M != -INFINITY) {
-    for (int r = 0; r < NR; ++r) {
-      const size_t p = (static_cast<size_t>(b) * NR + r) * H + h;
-      const float m = part_ml[p * 2];
-      if (m == -INFINITY) continue;
-      const float wgt = fast_exp2(m - M);
-      L += part_ml[p * 2 + 1] * wgt;
-      const float* po = part_o + p * kC + lane * DPL;
+  f32x4 acc[DPL / 4];
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) accv[d] += po[d] * wgt;
+  for (int c = 0; c < DPL / 4; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int r0 = 0; r0 < NR; r0 += 64) {
+    const int r = r0 + lane;
+    const float2 ml = r < NR ? ml2[(static_cast<size_t>(b) * NR + r) * H + h]
+                             : make_float2(-INFINITY, 0.f);
+    float Mc = ml.x;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, o));
+    const float Mn = fmaxf(M, Mc);
+    if (Mn == -INFINITY) continue;  // no tokens in any range so far
+    const float rescale = fast_exp2(M - Mn);
+    const float wl = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - Mn);
+    float Lc = ml.y * wl;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) Lc += __shfl_xor(Lc, o);
+    L = L * rescale + Lc;
+    M = Mn;
+#pragma unroll
+    for (int c = 0; c < DPL / 4; ++c) acc[c] *= rescale;
+    const int cnt = NR - r0 < 64 ? NR - r0 : 64;
+    for (int k0 = 0; k0 < cnt; k0 += kBatch) {
+      f32x4 v[kBatch][DPL / 4];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int k = k0 + u < cnt ? k0 + u : cnt - 1;
+        const f32x4* po = reinterpret_cast<const f32x4*>(
+            part_o + ((static_cast<size_t>(b) * NR + r0 + k) * H + h) * kC + lane * DPL);
+#pragma unroll
+        for (int c = 0; c < DPL / 4; ++c) v[u][c] = po[c];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const float wk = k0 + u < cnt ? __shfl(wl, k0 + u) : 0.f;
+        // a range without tokens has weight 0 and an all-zero row
+#pragma unroll
+        for (int c = 0; c < DPL / 4; ++c) acc[c] += v[u][c] * wk;
+      }
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  uint16_t* ob = out + static_cast<size_t>(task) * kC + lane * DPL;
+  uint32_t pk[DPL / 2];
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) ob[d] = f2bf(accv[d] * inv);
+  for (int c = 0; c < DPL / 4; ++c) {
+    pk[2 * c] = pack_bf16x2(acc[c][0] * inv, acc[c][1] * inv);
+    pk[2 * c + 1] = pack_bf16x2(acc[c][2] * inv, acc[c][3] * inv);
+  }
+  *reinterpret_cast<u32x4*>(out + static_cast<size_t>(task) * kC + lane * DPL) =
+      u32x4{pk[0], pk[1], pk[2], pk[3]};
   if (lse_out != nullptr && lane == 0) {
     lse_out[task] = L > 0.f ? (M + __log2f(L)) * 0.6931471805599453f : -INFINITY;
   }
 }
 
+// Heads per workgroup for a head count: 64 when it divides, else 32.
+int heads_per_group(int H) { return H % 64 == 0 ? 64 : 32; }
+
 int default_ranges(int B, int H) {
-  const int wgs_per_range = B * (H / kHeadsPerGroup);
+  const int wgs_per_range = B * (H / heads_per_group(H));
   int nr = (device_cu_count() + wgs_per_range - 1) / wgs_per_range;
   return nr < 1 ? 1 : nr;
 }
@@ -358,7 +497,7 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
   VOOM_REQUIRE(latent_dim == kLat && c_dim == kC,
                "mla_absorbed_decode: latent %d / c_dim %d unsupported (576 / 512)", latent_dim,
                c_dim);
-  VOOM_REQUIRE(batch > 0 && num_heads > 0 && num_heads % kHeadsPerGroup == 0,
+  VOOM_REQUIRE(batch > 0 && num_heads > 0 && num_heads % 32 == 0,
                "mla_absorbed_decode: num_heads %d must be a positive multiple of 32", num_heads);
   VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens >= kTile && page_tokens <= 4096,
                "mla_absorbed_decode: page_tokens %d must be a power of two in [64, 4096]",
@@ -374,7 +513,8 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
                    reinterpret_cast<uintptr_t>(lat_pool) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
                "mla_absorbed_decode: q, pool and workspace must be 16-byte aligned");
-  const long long grid = static_cast<long long>(batch) * num_ranges * (num_heads / kHeadsPerGroup);
+  const int hg = heads_per_group(num_heads);
+  const long long grid = static_cast<long long>(batch) * num_ranges * (num_heads / hg);
   VOOM_REQUIRE(grid < (1LL << 31), "mla_absorbed_decode: grid too large");
 
   const size_t n = static_cast<size_t>(batch) * num_ranges * num_heads;
@@ -393,8 +533,13 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
   a.pt_shift = ilog2(page_tokens);
   a.num_slots = num_slots;
   a.scale_log2e = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(mla_latent_kernel, dim3(static_cast<unsigned>(grid)), dim3(kMlaThreads), 0,
-                     stream, a);
+  if (hg == 64) {
+    hipLaunchKernelGGL(mla_latent_kernel<64>, dim3(static_cast<unsigned>(grid)),
+                       dim3(kMlaThreads), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(mla_latent_kernel<32>, dim3(static_cast<unsigned>(grid)),
+                       dim3(kMlaThreads), 0, stream, a);
+  }
   int rc = VOOM_LAUNCH_CHECK("mla_absorbed_decode: latent kernel launch");
   if (rc) return rc;
   const unsigned red_grid = static_cast<unsigned>((batch * num_heads + 3) / 4);
