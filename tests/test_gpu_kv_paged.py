@@ -282,3 +282,78 @@ def test_prefetched_uploads_match_fresh_ones_through_cache_changes():
         kv.release()
     for a, b in zip(outs[True], outs[False]):
         assert torch.equal(bits(a), bits(b))
+
+
+# ---- disk tier (spill_dir) -------------------------------------------------
+
+@pytest.mark.parametrize("compress", [False, True])
+def test_spill_dir_writes_page_files_like_the_reference(tmp_path, compress):
+    # mirrors tests/test_kv_spill_compress.py:22-60 of the reference
+    print(f"[kv-disk] reference protocol with spill_dir compress={compress}", flush=True)
+    spill_dir = tmp_path / "spill"
+    kv = PagedKVCache(num_layers=2, max_bytes=1, spill_dir=spill_dir, page_positions=4,
+                      resident_pages=0, compress_spill=compress)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    ref_k, ref_v = [], []
+    for layer in range(2):
+        k = rand_bf16((1, 2, 4, 8), gen)
+        v = rand_bf16((1, 2, 4, 8), gen)
+        ref_k.append(k)
+        ref_v.append(v)
+        kv.update(layer, k, v)
+    for layer in range(2):
+        kv.update(layer, rand_bf16((1, 2, 1, 8), gen), rand_bf16((1, 2, 1, 8), gen))
+    assert kv.stats.spills > 0
+    page = kv._pages[0][0]
+    assert not page.resident
+    lk, lv = page.load()
+    torch.cuda.synchronize()
+    assert torch.equal(bits(lk), bits(ref_k[0])) and torch.equal(bits(lv), bits(ref_v[0]))
+    spill_paths = [p.path for pages in kv._pages for p in pages if p.path is not None]
+    assert spill_paths and all(path.exists() for path in spill_paths)
+    assert page.path.name == "kv_l0_p0.vt"
+    kv.release()
+    assert kv.offset == 0 and kv.nbytes() == 0
+    assert not any(path.exists() for path in spill_paths)
+
+
+def test_host_budget_moves_pages_to_disk_and_back(tmp_path):
+    print("[kv-disk] host_max_bytes evicts host copies; attend/load/reload from files", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    B, NQ, NKV, D, PT = 2, 8, 2, 128, 64
+    page_bytes = B * NKV * D * 4 * PT
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, spill_dir=tmp_path,
+                      page_positions=PT, resident_pages=1, compress_spill=True,
+                      host_max_bytes=2 * page_bytes)
+    k = rand_bf16((B, NKV, 640, D), gen)
+    v = torch.randn((B, NKV, 640, D), generator=gen, device="cuda").to(torch.bfloat16)
+    kf = torch.randn((B, NKV, 640, D), generator=gen, device="cuda").to(torch.bfloat16)
+    kv.append(0, kf, v)
+    originals = [tuple(t.clone() for t in p.load()) for p in kv._pages[0]]
+    q = torch.randn((B, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    before = kv.attend(0, q).clone()
+    # three separate spills: the oldest host blocks go over the host budget
+    kv.spill([(0, i) for i in (0, 1, 2)])
+    kv.spill([(0, i) for i in (3, 4)])
+    kv.spill([(0, i) for i in (5, 6)])
+    pages = kv._pages[0]
+    assert all(p.path is not None and p.path.exists() for p in pages[:7])
+    assert kv.arena.used_bytes <= 2 * page_bytes
+    disk_only = [p for p in pages[:7] if p.host is None]
+    assert len(disk_only) >= 3
+    for p in pages[:7]:
+        kl, vl = p.load()
+        assert torch.equal(bits(kl), bits(originals[p.index][0]))
+        assert torch.equal(bits(vl), bits(originals[p.index][1]))
+    spilled_out = kv.attend(0, q)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(spilled_out.float().cpu().numpy(),
+                               before.float().cpu().numpy(), atol=ATOL, rtol=RTOL)
+    files = [p.path for p in pages[:7]]
+    assert kv.reload() == 7
+    assert all(p.resident and p.path is None for p in pages)
+    assert not any(f.exists() for f in files)
+    after = kv.attend(0, q)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(after), bits(before))
+    kv.release()

@@ -21,11 +21,16 @@ Where the reference differs by platform:
   * Pages live in one device pool per layer (slot = one sequence's page) and
     are addressed through a per-layer block table, instead of per-layer lists
     of MLX arrays that are concatenated on every call (kv_paged.py:164-181).
-  * The spill target is pinned host memory (the HBM <-> host boundary exists
-    on MI355X; Apple unified memory has none), and a page is stored as its
-    low-byte and high-byte planes (formats/packed.py:49-50).  With
+  * The first spill tier is pinned host memory (the HBM <-> host boundary
+    exists on MI355X; Apple unified memory has none), and a page is stored as
+    its low-byte and high-byte planes (formats/packed.py:49-50).  With
     ``compress_spill`` the high plane is zstd level 1 compressed on the host,
     as vpack does; the low plane stays raw.
+  * With ``spill_dir`` a spilled page is also written to
+    ``spill_dir/kv_l{L}_p{P}.vt`` (vpack framing, voom_amd/page_file.py) and
+    ``page.path`` names it, as in the reference; ``host_max_bytes`` then caps
+    the host copies, and a page whose host copy was dropped reloads from its
+    file.  ``release()`` deletes the files.
   * Budget accounting, page closing and the eviction order are the
     reference's (kv_paged.py:143-162, 187-194, 216-240).
 """
@@ -41,6 +46,7 @@ import numpy as np
 import torch
 
 from . import ops
+from . import page_file
 from . import zstd as _zstd
 from .host_arena import HostArena, HostBlock
 from .page_pool import DevicePagePool
@@ -81,9 +87,10 @@ class _SpillBlock:
     in a staging buffer.  ``ready`` is recorded after the last D2H copy.
     """
 
-    __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "live", "compressed")
+    __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "live", "compressed", "pages")
 
     def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int):
+        self.pages: list = []
         self.block = block
         self.n_pages = n_pages
         self.parts = list(parts)
@@ -227,7 +234,8 @@ class PagedKVCache:
     def __init__(self, num_layers: int, max_bytes: int, spill_dir: str | Path | None = None,
                  page_positions: int = 256, resident_pages: int = 1,
                  compress_spill: bool = False, *, device=None, initial_slots: int = 0,
-                 arena: HostArena | None = None, prefetch: bool = True):
+                 arena: HostArena | None = None, prefetch: bool = True,
+                 host_max_bytes: int | None = None):
         if num_layers <= 0:
             raise ValueError("num_layers must be positive")
         if page_positions <= 0 or page_positions & (page_positions - 1):
@@ -237,9 +245,12 @@ class PagedKVCache:
         self.page_positions = page_positions
         self.resident_pages = resident_pages
         self.compress_spill = compress_spill
-        # The spill target is the pinned host arena; spill_dir is kept for
-        # interface compatibility and created when given.
+        # Spilled pages live in the pinned host arena; with spill_dir they are
+        # also written to page files, and host_max_bytes bounds the host copies.
         self.spill_dir = Path(spill_dir) if spill_dir is not None else None
+        self.host_max_bytes = host_max_bytes
+        if host_max_bytes is not None and self.spill_dir is None:
+            raise ValueError("host_max_bytes needs a spill_dir to hold the evicted copies")
         if self.spill_dir is not None:
             self.spill_dir.mkdir(parents=True, exist_ok=True)
         self.device = torch.device(device) if device is not None else torch.device("cuda")
@@ -267,6 +278,7 @@ class PagedKVCache:
         self._len = [0] * L
         self._offset = 0
         self._resident_closed = 0  # closed pages held in device slots, all layers
+        self._spill_blocks: list[_SpillBlock] = []  # host blocks, oldest first
         self._pools: list[DevicePagePool | None] = [None] * L
         # one transient staging pool shared by all layers: every transient
         # merge and every read of it is ordered on the main stream
@@ -588,6 +600,9 @@ class PagedKVCache:
             self._set_table_cols(layer, {p.index: None for p in lp})
         if self.compress_spill:
             self._compress_spilled(pages)
+        if self.spill_dir is not None:
+            self._write_files(pages)
+            self._evict_host()
         self.stats.spills += len(pages)
         self.stats.spill_s += time.perf_counter() - t0
         return len(pages)
@@ -604,6 +619,8 @@ class PagedKVCache:
         n = len(pages)
         per_chunk = max(1, self._ring.nbytes // page_bytes)
         sb = _SpillBlock(self.arena.alloc(n * page_bytes), n, parts, per_chunk)
+        sb.pages = list(pages)
+        self._spill_blocks.append(sb)
         for j, p in enumerate(pages):
             p.host = sb
             p.host_j = j
@@ -657,9 +674,67 @@ class PagedKVCache:
             self.stats.spill_bytes_raw += p.nbytes
             self.stats.spill_bytes_compressed += sum(sb.parts) + sum(f.nbytes for f in frames)
 
+    def _tensor_meta(self, layer: int) -> list[dict]:
+        """Name, dtype and page shape ([B, ...slot shape]) of each pool tensor."""
+        pool = self._pool(layer)
+        names = ["k", "v_t"] if self._geom[0] == "kv" else ["latent"]
+        return [{"name": n, "dtype": "BF16", "shape": (self._batch,) + shp}
+                for n, shp in zip(names, pool.slot_shapes)]
+
+    def _write_files(self, pages: list[_Page]) -> None:
+        """Write each spilled page to its page file once its host copy has landed."""
+        waited = set()
+        for p in pages:
+            sb = p.host
+            if id(sb) not in waited:
+                sb.ready.synchronize()
+                waited.add(id(sb))
+            T = len(sb.parts)
+            lo = [sb.part(t, p.host_j).numpy() for t in range(T)]
+            frames = sb.compressed[p.host_j]
+            hi = frames if frames is not None else [sb.part(T + t, p.host_j).numpy()
+                                                     for t in range(T)]
+            path = page_file.page_path(self.spill_dir, p.layer, p.index)
+            page_file.write(path, p.layer, p.index, self._tensor_meta(p.layer), lo, hi,
+                            [frames is not None] * T)
+            p.path = path
+
+    def _evict_host(self) -> None:
+        """Drop host copies, oldest block first, while they exceed host_max_bytes;
+        only blocks whose pages all have page files are dropped."""
+        if self.host_max_bytes is None:
+            return
+        for sb in list(self._spill_blocks):
+            if self.arena.used_bytes <= self.host_max_bytes:
+                break
+            live = [p for p in sb.pages if p.host is sb]
+            if any(p.path is None for p in live):
+                continue
+            for p in live:
+                p.host = None
+            self._release_block(sb)
+
+    def _release_block(self, sb: _SpillBlock) -> None:
+        if sb.ready is not None:
+            sb.ready.synchronize()
+        self.arena.free(sb.block)
+        self._spill_blocks.remove(sb)
+
+    def _file_planes(self, p: _Page) -> list[torch.Tensor]:
+        """Planes of a page that has no host copy, read from its page file into
+        pinned buffers (low planes, then high planes)."""
+        parts = self._plane_parts(self._pool(p.layer))
+        bufs = [torch.empty(n, dtype=torch.uint8, pin_memory=self.arena.pin)
+                for n in parts + parts]
+        T = len(parts)
+        page_file.read(p.path, [b.numpy() for b in bufs[:T]], [b.numpy() for b in bufs[T:]])
+        return bufs
+
     def _host_planes(self, p: _Page) -> list[torch.Tensor]:
         """Pinned host tensors of a spilled page's planes: low planes of every
         pool tensor, then high planes (decompressed when compressed)."""
+        if p.host is None:
+            return self._file_planes(p)
         sb = p.host
         T = len(sb.parts)
         planes = [sb.part(w, p.host_j) for w in range(2 * T)]
@@ -682,7 +757,7 @@ class PagedKVCache:
         n = len(pages)
         p0 = pages[0]
         sb = p0.host
-        if (p0.host_j % sb.chunk == 0 and n == sb.record_pages(p0.host_j // sb.chunk)
+        if (sb is not None and p0.host_j % sb.chunk == 0 and n == sb.record_pages(p0.host_j // sb.chunk)
                 and all(p.host is sb and p.host_j == p0.host_j + j
                         and sb.compressed[p.host_j] is None for j, p in enumerate(pages))):
             staging.copy_(sb.record(p0.host_j // sb.chunk), non_blocking=True)
@@ -708,7 +783,7 @@ class PagedKVCache:
 
     @staticmethod
     def _chunk_sig(pages: list[_Page]) -> tuple:
-        return tuple((id(p.host), p.host_j) for p in pages)
+        return tuple((id(p.host), p.host_j, p.path) for p in pages)
 
     def _acquire(self, writer: torch.cuda.Stream, nbytes: int):
         """Next staging buffer; an upload started ahead into it is given up
@@ -754,7 +829,7 @@ class PagedKVCache:
         per_chunk = max(1, self._ring.nbytes // (2 * sum(parts)))
         cp = spilled[:per_chunk]
         copy = self._stream()
-        for sb in {id(p.host): p.host for p in cp}.values():
+        for sb in {id(p.host): p.host for p in cp if p.host is not None}.values():
             copy.wait_event(sb.ready)
         idx, buf = self._acquire(copy, 2 * len(cp) * sum(parts))
         with torch.cuda.stream(copy):
@@ -794,7 +869,7 @@ class PagedKVCache:
             per_chunk = max(1, self._ring.nbytes // (2 * sum(parts)))
             if transient:
                 target.ensure_capacity(nbuf * per_chunk * B)
-            for sb in {id(p.host): p.host for p in pages}.values():
+            for sb in {id(p.host): p.host for p in pages if p.host is not None}.values():
                 copy.wait_event(sb.ready)
             for c0 in range(0, len(pages), per_chunk):
                 cp = pages[c0:c0 + per_chunk]
@@ -868,13 +943,21 @@ class PagedKVCache:
         return len(pages)
 
     def _drop_host(self, p: _Page) -> None:
+        """Forget the spilled copies of a page that is resident again."""
         sb = p.host
         p.host = None
         p._compressed = False
+        if p.path is not None:
+            try:
+                p.path.unlink()
+            except FileNotFoundError:
+                pass
+            p.path = None
+        if sb is None:
+            return
         sb.live -= 1
-        if sb.live == 0:
-            sb.ready.synchronize()
-            self.arena.free(sb.block)
+        if sb.live == 0 and sb in self._spill_blocks:
+            self._release_block(sb)
 
     def _slot_contents(self, pool: DevicePagePool, idx: torch.Tensor):
         if self._geom[0] == "kv":
