@@ -127,6 +127,36 @@ int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
                              int num_ranges, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Position-free paged attention (keys stored before RoPE).
+ *
+ * Replaces position_free_paged_attention and its Metal kernel
+ * (runtime/pic_attention.py:22-232): pages hold unrotated K and ordinary V,
+ * [num_pages, num_kv_heads, block_size, head_dim] each; block_table
+ * [ceil(num_keys / block_size)] int32 maps the logical keys (shared by all
+ * batch rows; repeating a page id is legal and is how pages are shared);
+ * key k is rotated at key_positions[k] with the fp32 NeoX tables
+ * cos/sin [max_position, head_dim/2], rounded to bf16, and attended by query
+ * tq iff key_positions[k] <= query_positions[tq].
+ *   q    [batch, num_q_heads, num_queries, head_dim] bf16, already rotated
+ *   out  same shape, bf16; rows with no visible key are zeros
+ * head_dim in {64, 128}; (num_q_heads / num_kv_heads) * num_queries <= 16.
+ * num_splits splits each (batch, kv head)'s keys over wavefronts (0 = library
+ * default); the workspace must hold voom_position_free_workspace_bytes(...)
+ * for the same values.  Page ids outside [0, num_pages) read page 0 and
+ * positions are clamped to [0, max_position); callers validate them.
+ * ------------------------------------------------------------------------- */
+size_t voom_position_free_workspace_bytes(int batch, int num_kv_heads, int head_dim,
+                                          int num_keys, int num_splits);
+int voom_position_free_attention(const void* q, const void* k_pages, const void* v_pages,
+                                 const int32_t* block_table, const int32_t* key_positions,
+                                 const int32_t* query_positions, const float* cos_table,
+                                 const float* sin_table, void* out, void* workspace,
+                                 size_t ws_bytes, int batch, int num_q_heads, int num_queries,
+                                 int num_kv_heads, int head_dim, int block_size, int num_pages,
+                                 int num_keys, int max_position, float scale, int num_splits,
+                                 hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Page writes and reads.
  *
  * voom_append_kv writes L new tokens per sequence into the pools at logical

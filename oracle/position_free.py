@@ -1,0 +1,67 @@
+"""CPU restatement of position-free paged attention -- TEST INFRASTRUCTURE ONLY.
+
+Follows runtime/pic_attention.py:
+  rope_tables      :150-167  angles = position / theta^(i / half), fp32
+  rotate           :68-90    NeoX rotate-half of the stored key at its
+                             logical position, fp32, then rounded to bf16
+  attention        :44-128   q * scale in fp32, visible iff key position <=
+                             query position, softmax, zeros when nothing is
+                             visible; page row ((blk * NKV + kvh) * BLOCK + off)
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .bf16 import round_bf16
+
+
+def rope_tables(max_position: int, head_dim: int, theta: float):
+    half = head_dim // 2
+    den = np.float32(theta) ** (np.arange(half, dtype=np.float32) / np.float32(half))
+    ang = np.arange(max_position, dtype=np.float32)[:, None] / den[None, :].astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def rotate(k: np.ndarray, positions: np.ndarray, cos: np.ndarray, sin: np.ndarray, *,
+           bf16: bool = True) -> np.ndarray:
+    """Rotate rows k [..., N, D] at positions [N] (rotate-half)."""
+    half = k.shape[-1] // 2
+    c = cos[positions]
+    s = sin[positions]
+    a = k[..., :half].astype(np.float32)
+    b = k[..., half:].astype(np.float32)
+    out = np.concatenate([a * c - b * s, b * c + a * s], axis=-1).astype(np.float32)
+    return round_bf16(out) if bf16 else out
+
+
+def attention(q: np.ndarray, k_pages: np.ndarray, v_pages: np.ndarray, block_table: np.ndarray,
+              key_positions: np.ndarray, query_positions: np.ndarray, cos: np.ndarray,
+              sin: np.ndarray, scale: float, *, bf16: bool = True) -> np.ndarray:
+    """Output [B, NQ, TQ, D] in fp32 (before the final bf16 store)."""
+    B, NQ, TQ, D = q.shape
+    _, NKV, BLOCK, _ = k_pages.shape
+    G = NQ // NKV
+    TK = key_positions.size
+    keys = np.arange(TK)
+    pages = block_table[keys // BLOCK] if TK else np.zeros(0, np.int64)
+    offs = keys % BLOCK
+    out = np.zeros((B, NQ, TQ, D), dtype=np.float32)
+    for kvh in range(NKV):
+        k_rows = k_pages[pages, kvh, offs].astype(np.float32)     # [TK, D]
+        v_rows = v_pages[pages, kvh, offs].astype(np.float32)
+        k_rot = rotate(k_rows, key_positions, cos, sin, bf16=bf16)
+        for b in range(B):
+            for j in range(G):
+                h = kvh * G + j
+                qv = q[b, h].astype(np.float32) * np.float32(scale)  # [TQ, D]
+                s = qv @ k_rot.T                                      # [TQ, TK]
+                vis = key_positions[None, :] <= query_positions[:, None]
+                s = np.where(vis, s, -np.inf)
+                m = s.max(axis=1, initial=-np.inf)
+                ok = np.isfinite(m)
+                p = np.where(vis, np.exp(s - np.where(ok, m, 0)[:, None]), 0.0)
+                l = p.sum(axis=1)
+                o = p @ v_rows
+                out[b, h] = np.where(ok[:, None], o / np.where(l > 0, l, 1)[:, None], 0.0)
+    return out

@@ -1,0 +1,93 @@
+"""GPU parity of voom_position_free_attention against oracle/position_free.py
+(runtime/pic_attention.py restated), 2e-2 abs / 1e-2 rel in bf16 -- the
+reference's own test tolerance for this kernel (tests/test_pic_attention.py:48)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import position_free as opf
+from voom_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def run(B, NQ, NKV, TQ, D, BLOCK, TK, P, *, seed, kpos=None, qpos=None, table=None,
+        num_splits=0, max_pos=None):
+    print(f"[pf] B={B} NQ={NQ} NKV={NKV} TQ={TQ} D={D} BLOCK={BLOCK} TK={TK} P={P} "
+          f"splits={num_splits}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((B, NQ, TQ, D), generator=g).to(torch.bfloat16)
+    kp = torch.randn((P, NKV, BLOCK, D), generator=g).to(torch.bfloat16)
+    vp = torch.randn((P, NKV, BLOCK, D), generator=g).to(torch.bfloat16)
+    nblk = (TK + BLOCK - 1) // BLOCK
+    if table is None:
+        table = torch.randint(0, P, (nblk,), generator=g, dtype=torch.int32)
+    if kpos is None:
+        kpos = torch.arange(TK, dtype=torch.int32)
+    if qpos is None:
+        qpos = torch.arange(TK - TQ, TK, dtype=torch.int32).clamp(min=0)
+    max_pos = max_pos or max(int(kpos.max()) + 1 if TK else 1, int(qpos.max()) + 1)
+    cos, sin = ops.rope_cache(max_pos, D, 10000.0, device="cuda")
+    out = ops.position_free_paged_attention(
+        q.cuda(), kp.cuda(), vp.cuda(), table.cuda(), kpos.cuda(), qpos.cuda(), cos, sin,
+        scale=D ** -0.5, num_splits=num_splits)
+    torch.cuda.synchronize()
+    ref = opf.attention(q.float().numpy(), kp.float().numpy(), vp.float().numpy(),
+                        table.numpy().astype(np.int64), kpos.numpy().astype(np.int64),
+                        qpos.numpy().astype(np.int64), cos.cpu().numpy(), sin.cpu().numpy(),
+                        D ** -0.5)
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    return out
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("BLOCK", [1, 4, 64])
+def test_block_sizes_and_head_dims(D, BLOCK):
+    run(1, 8, 2, 1, D, BLOCK, 300, max(8, 600 // BLOCK), seed=1)
+
+
+@pytest.mark.parametrize("NQ,NKV,TQ", [(9, 3, 4), (4, 4, 2), (16, 1, 1), (32, 8, 4)])
+def test_head_groups_and_queries(NQ, NKV, TQ):
+    run(2, NQ, NKV, TQ, 64, 16, 517, 80, seed=2)
+
+
+def test_repeated_pages_and_unordered_positions():
+    g = torch.Generator().manual_seed(3)
+    TK, BLOCK = 200, 1
+    table = torch.randint(0, 7, (TK,), generator=g, dtype=torch.int32)  # heavy sharing
+    kpos = torch.randperm(400, generator=g)[:TK].to(torch.int32)
+    qpos = torch.tensor([150, 399], dtype=torch.int32)  # first query sees only part
+    run(1, 8, 2, 2, 128, BLOCK, TK, 7, seed=3, kpos=kpos, qpos=qpos, table=table)
+
+
+@pytest.mark.parametrize("splits", [1, 3, 40])
+def test_split_counts(splits):
+    run(1, 4, 1, 1, 128, 64, 3000, 60, seed=4, num_splits=splits)
+
+
+def test_nothing_visible_and_empty_key_set():
+    out = run(1, 4, 2, 2, 64, 4, 40, 12, seed=5,
+              qpos=torch.tensor([0, 1], dtype=torch.int32),
+              kpos=torch.arange(10, 50, dtype=torch.int32))
+    assert torch.all(out == 0)
+    out = run(1, 4, 2, 1, 64, 4, 0, 3, seed=6, qpos=torch.tensor([5], dtype=torch.int32))
+    assert torch.all(out == 0)
+
+
+def test_validation_matches_the_reference_errors():
+    q = torch.zeros((1, 4, 1, 64), dtype=torch.bfloat16, device="cuda")
+    kp = torch.zeros((3, 2, 4, 64), dtype=torch.bfloat16, device="cuda")
+    cos, sin = ops.rope_cache(16, 64, 1e4, device="cuda")
+    i32 = lambda *v: torch.tensor(v, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="block table"):
+        ops.position_free_paged_attention(q, kp, kp, i32(0), i32(*range(8)), i32(7), cos, sin,
+                                          scale=1.0)
+    with pytest.raises(ValueError, match="RoPE cache"):
+        ops.position_free_paged_attention(q, kp, kp, i32(0), i32(0), i32(0),
+                                          cos[:, :16].contiguous(), sin[:, :16].contiguous(),
+                                          scale=1.0)
+    with pytest.raises(ValueError, match="geometry"):
+        ops.position_free_paged_attention(q, kp, kp, i32(0), i32(0), i32(0, 1), cos, sin,
+                                          scale=1.0)

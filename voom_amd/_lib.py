@@ -37,6 +37,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "voom_mla_absorbed_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int,
                                          c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P]),
+    "voom_position_free_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "voom_position_free_attention": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_size_t,
+                                             c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                             c_int, c_int, c_float, c_int, _P]),
     "voom_append_kv": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int,
                                c_int, c_int, _P]),
     "voom_gather_kv": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -386,3 +386,63 @@ def gather_rows(pool: torch.Tensor, block_table: torch.Tensor, seq_len: int, *,
     _lib.call("voom_gather_rows", _ptr(pool), _ptr(block_table), _ptr(out), B, seq_len, W, PT,
               block_table.shape[1], slots, _stream(stream))
     return out
+
+
+def rope_cache(max_position: int, head_dim: int, theta: float, *,
+               denominators: torch.Tensor | None = None, device=None):
+    """fp32 NeoX RoPE tables (cos, sin) [max_position, head_dim / 2]:
+    angle = position / theta^(i / half) (runtime/pic_attention.py:150-167)."""
+    if max_position <= 0 or head_dim <= 0 or head_dim % 2:
+        raise ValueError("RoPE cache dimensions must be positive and even")
+    half = head_dim // 2
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    if denominators is None:
+        denominators = theta ** (torch.arange(half, dtype=torch.float32, device=dev) / half)
+    else:
+        _require(tuple(denominators.shape) == (half,), "RoPE denominators do not match head_dim")
+        denominators = denominators.to(device=dev, dtype=torch.float32)
+    angles = torch.arange(max_position, dtype=torch.float32, device=dev)[:, None] / denominators
+    return torch.cos(angles).contiguous(), torch.sin(angles).contiguous()
+
+
+def position_free_workspace_bytes(batch: int, num_kv_heads: int, head_dim: int, num_keys: int,
+                                  num_splits: int = 0) -> int:
+    return int(_lib.lib().voom_position_free_workspace_bytes(batch, num_kv_heads, head_dim,
+                                                            num_keys, num_splits))
+
+
+def position_free_paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                                  block_table: torch.Tensor, key_positions: torch.Tensor,
+                                  query_positions: torch.Tensor, cos: torch.Tensor,
+                                  sin: torch.Tensor, *, scale: float, num_splits: int = 0,
+                                  stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Attend rotated q [B, Nq, Tq, D] to unrotated K / V pages [P, Nkv, BLOCK, D]
+    through block_table [ceil(Tk / BLOCK)], rotating each key at its logical
+    position (runtime/pic_attention.py:184-232, same arguments and checks).
+    Repeating a physical block id is legal and is the sharing primitive."""
+    _require_device(q, k_pages, v_pages, block_table, key_positions, query_positions, cos, sin)
+    if q.dim() != 4 or k_pages.dim() != 4 or tuple(v_pages.shape) != tuple(k_pages.shape):
+        raise ValueError("invalid Q/K/V page ranks or shapes")
+    B, NQ, TQ, D = q.shape
+    P, NKV, BLOCK, Dp = k_pages.shape
+    TK = key_positions.numel()
+    if Dp != D or D % 32 or NQ % NKV or query_positions.numel() != TQ:
+        raise ValueError("unsupported head or position geometry")
+    if block_table.dim() != 1 or block_table.numel() != (TK + BLOCK - 1) // BLOCK:
+        raise ValueError("block table does not cover logical key positions")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] * 2 != D:
+        raise ValueError("RoPE cache does not match head dimension")
+    if not (q.dtype == k_pages.dtype == v_pages.dtype == torch.bfloat16):
+        raise ValueError("Q/K/V page dtypes must match (bfloat16)")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError("RoPE cache must be FP32")
+    _require(block_table.dtype == key_positions.dtype == query_positions.dtype == torch.int32,
+             "block table and positions must be int32")
+    need = position_free_workspace_bytes(B, NKV, D, TK, num_splits)
+    ws = workspace(q.device, need, tag=3)
+    out = torch.empty_like(q)
+    _lib.call("voom_position_free_attention", _ptr(q), _ptr(k_pages), _ptr(v_pages),
+              _ptr(block_table), _ptr(key_positions), _ptr(query_positions), _ptr(cos),
+              _ptr(sin), _ptr(out), _ptr(ws), need, B, NQ, TQ, NKV, D, BLOCK, P, TK,
+              cos.shape[0], float(scale), int(num_splits), _stream(stream))
+    return out
