@@ -91,3 +91,48 @@ def test_validation_matches_the_reference_errors():
     with pytest.raises(ValueError, match="geometry"):
         ops.position_free_paged_attention(q, kp, kp, i32(0), i32(0), i32(0, 1), cos, sin,
                                           scale=1.0)
+
+
+def test_pool_cache_sharing_matches_the_oracle():
+    """PositionFreeKVCache over a shared pool: a second request reuses the first
+    one's prefix pages by reference; both attend through the kernel and match
+    the oracle over their own logical tables (runtime/kv_cache.py:555-701)."""
+    from voom_amd.position_free import PositionFreeKVCache, PositionFreePagePool
+    print("[pf] pool/cache sharing", flush=True)
+    L, NKV, NQ, D = 2, 2, 8, 64
+    pool = PositionFreePagePool(L, NKV, D, min_capacity=16, device="cuda")
+    g = torch.Generator().manual_seed(11)
+
+    def chunk(n):
+        return [(torch.randn((1, NKV, n, D), generator=g).to(torch.bfloat16).cuda(),
+                 torch.randn((1, NKV, n, D), generator=g).to(torch.bfloat16).cuda())
+                for _ in range(L)]
+
+    a = PositionFreeKVCache(pool)
+    for n in (40, 25):
+        for layer, (k, v) in enumerate(chunk(n)):
+            a.update_unrotated(layer, k, v)
+    b = PositionFreeKVCache.share_prefix(a, 50)
+    for layer, (k, v) in enumerate(chunk(30)):
+        b.update_unrotated(layer, k, v)
+    assert pool.capacity > 16                      # grew geometrically, ids kept
+    for cache in (a, b):
+        for layer in range(L):
+            TQ = 2
+            q = torch.randn((1, NQ, TQ, D), generator=g).to(torch.bfloat16)
+            qpos = torch.tensor([cache.offset - 5, cache.offset - 1], dtype=torch.int32)
+            out = cache.paged_attention(layer, q.cuda(), qpos, theta=10000.0, scale=D ** -0.5)
+            torch.cuda.synchronize()
+            kp, vp = pool.pages(layer)
+            cos, sin = pool.rope(cache.offset, 10000.0)
+            ref = opf.attention(q.float().numpy(), kp.float().cpu().numpy(),
+                                vp.float().cpu().numpy(),
+                                np.asarray(cache.page_ids, dtype=np.int64),
+                                np.arange(cache.offset), qpos.numpy().astype(np.int64),
+                                cos.cpu().numpy(), sin.cpu().numpy(), D ** -0.5)
+            np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    a.release()
+    Kb, _ = b.gather_unrotated(1)                  # shared pages survive a's release
+    assert Kb.shape == (1, NKV, 80, D)
+    b.release()
+    assert pool.live_pages == 0
