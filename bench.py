@@ -546,6 +546,88 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
     return res
 
 
+def bench_position_free(steps: int, warmup: int, cpu_sample: bool) -> dict:
+    """Position-free decode (SURVEY next row 3): Llama-3-8B shape, one request,
+    32768 keys in one-token pages drawn at random from a 40000-page pool,
+    keys stored before RoPE and rotated in the kernel at positions 0..32767,
+    one query at position 32767.  Four rotating page pools (4 x 164 MB) keep the
+    working set out of the Infinity Cache.
+
+    Algorithmic bytes per key: K + V rows of all 8 KV heads (4096 B), its table
+    entry and position (8 B) and its cos/sin rows (2 x 64 fp32 = 512 B)."""
+    import numpy as np
+    import torch
+
+    from voom_amd import ops
+
+    NQ, NKV, D, TK, P = 32, 8, 128, 32768, 40000
+    log("position-free: 4 rotating pools of 40000 one-token pages, 32768 keys, 32q/8kv, D=128")
+    sets = []
+    for i in range(4):
+        g = torch.Generator().manual_seed(30 + i)
+        kp = torch.randn((P, NKV, 1, D), generator=g).to(torch.bfloat16).cuda()
+        vp = torch.randn((P, NKV, 1, D), generator=g).to(torch.bfloat16).cuda()
+        table = torch.randperm(P, generator=g)[:TK].to(torch.int32).cuda()
+        q = torch.randn((1, NQ, 1, D), generator=g).to(torch.bfloat16).cuda()
+        sets.append((q, kp, vp, table))
+    kpos = torch.arange(TK, dtype=torch.int32, device="cuda")
+    qpos = torch.tensor([TK - 1], dtype=torch.int32, device="cuda")
+    cos, sin = ops.rope_cache(TK, D, 500000.0, device="cuda")
+    scale = D ** -0.5
+
+    def step(i):
+        q, kp, vp, table = sets[i % 4]
+        return ops.position_free_paged_attention(q, kp, vp, table, kpos, qpos, cos, sin,
+                                                 scale=scale)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / steps / 1e3
+    nbytes = TK * (2 * NKV * D * 2 + 8 + D * 4) + 2 * NQ * D * 2
+    res = {
+        "workload": "position-free decode: B=1, 32q/8kv, D=128, 32768 keys in one-token pages "
+                    "(random ids from 40000), in-kernel RoPE theta 5e5, 4 rotating pools",
+        "op_us": t * 1e6,
+        "hbm_gbs": nbytes / t / 1e9,
+        "hbm_frac": nbytes / t / 1e9 / HBM_PEAK_GBS,
+        "bytes_per_call": nbytes,
+        "traffic": profiled_traffic("position_free_decode"),
+        "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, calibrated; "
+                          "profiles/position_free_decode.md (attention kernel)",
+    }
+    log(f"position-free: {t * 1e6:.1f} us per call, {res['hbm_gbs']:.0f} GB/s "
+        f"({100 * res['hbm_frac']:.1f}% HBM)")
+    if cpu_sample:
+        from oracle import position_free as opf
+
+        q, kp, vp, table = sets[0]
+        args_np = (q.float().cpu().numpy(), kp.float().cpu().numpy(), vp.float().cpu().numpy(),
+                   table.cpu().numpy().astype(np.int64), kpos.cpu().numpy().astype(np.int64),
+                   qpos.cpu().numpy().astype(np.int64), cos.cpu().numpy(), sin.cpu().numpy())
+        t0 = time.perf_counter()
+        ref = opf.attention(*args_np, scale)
+        dt = time.perf_counter() - t0
+        out = step(0)
+        torch.cuda.synchronize()
+        res["cpu_baseline"] = {"value": TK / dt, "unit": "keys/s (all 8 KV heads)",
+                               "cores": cpu_threads(), "kind": "port",
+                               "sample": "one full call (32768 keys), numpy, "
+                                         "oracle/position_free.py"}
+        res["gpu_keys_per_s"] = TK / t
+        res["parity_max_abs_err_vs_oracle"] = float(
+            np.abs(out.float().cpu().numpy() - ref).max())
+    del sets
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_e2e(cpu_sample: bool) -> dict:
     """Config 1: SmolLM2-135M-shaped decoder, random N(0, 0.02) bf16 weights
     (seed 0), a 512-token prompt of uniform ids (seed 1), greedy decode of 128
@@ -631,9 +713,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="gqa,spill,long,mla,e2e",
+    ap.add_argument("--only", default="gqa,spill,long,mla,pf,e2e",
                     help="comma list of legs: gqa (config 2, headline), spill (config 3), "
-                         "long (config 4), mla (config 5), e2e (config 1)")
+                         "long (config 4), mla (config 5), pf (position-free), e2e (config 1)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a known-size 1 GiB streaming kernel (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -690,6 +772,9 @@ def main() -> int:
         extra["long_context"] = bench_long_context(64, cpu_sample=not args.no_cpu)
     if "mla" in legs:
         extra["mla"] = bench_mla(args.steps, args.warmup, cpu_sample=not args.no_cpu)
+    if "pf" in legs:
+        extra["position_free"] = bench_position_free(args.steps, args.warmup,
+                                                     cpu_sample=not args.no_cpu)
     if "e2e" in legs:
         extra["e2e"] = bench_e2e(cpu_sample=not args.no_cpu)
     if extra:
