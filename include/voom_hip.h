@@ -126,6 +126,44 @@ int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
                              int page_tokens, int max_pages, int num_slots, float scale,
                              int num_ranges, hipStream_t stream);
 
+/* The same contraction over a selection of each sequence's positions: the
+ * DSA gather of the top-k latent rows feeding absorbed MLA
+ * (runtime/glm.py:280-289).  sel [batch, sel_stride] int32 holds ascending
+ * logical positions (voom_dsa_topk's output), sel_lens [batch] how many are
+ * used; the rows are read through block_table straight from the pool (no
+ * gathered copy).  The pool must be smaller than 4 GiB.  The workspace is
+ * voom_mla_workspace_bytes(batch, num_heads, num_ranges). */
+int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool, const int32_t* block_table,
+                           const int32_t* sel, const int32_t* sel_lens, void* out_c,
+                           float* lse_out, void* workspace, size_t ws_bytes, int batch,
+                           int num_heads, int latent_dim, int c_dim, int page_tokens,
+                           int max_pages, int num_slots, int sel_stride, float scale,
+                           int num_ranges, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * DSA (DeepSeek Sparse Attention) selection for a decode step.
+ *
+ * voom_dsa_index_scores replaces the lightning-indexer scores of
+ * DSAState.update_and_select (runtime/glm_dsa.py:140-150):
+ *   scores[b][s] = sum_j w_head[b][j] * max(scale * (q_idx[b][j] . k_idx[b][s]), 0)
+ * in fp32 for s < lens[b].  q_idx [batch, num_heads, head_dim] bf16 (after the
+ * indexer RoPE), w_head [batch, num_heads] fp32 (weights_proj output already
+ * multiplied by num_heads^-0.5), k_idx [batch, cap, head_dim] bf16 (the
+ * cached index keys), scores [batch, cap] fp32 (entries at or past lens[b]
+ * are not written).  head_dim 128; num_heads 16, 32, 48 or 64.
+ *
+ * voom_dsa_topk replaces the selection (glm_dsa.py:151-160): the k highest
+ * scores of keys s < lens[b] (causal for a decode step at position
+ * lens[b] - 1), written to sel [batch, k] as ascending indices, with
+ * sel_lens[b] = min(lens[b], k).  Among keys tied at the k-th score the
+ * lowest indices are kept.
+ * ------------------------------------------------------------------------- */
+int voom_dsa_index_scores(const void* q_idx, const float* w_head, const void* k_idx,
+                          const int32_t* lens, float* scores, int batch, int num_heads,
+                          int head_dim, int cap, float scale, hipStream_t stream);
+int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* sel, int32_t* sel_lens,
+                  int batch, int cap, int k, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Position-free paged attention (keys stored before RoPE).
  *

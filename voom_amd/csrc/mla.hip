@@ -58,10 +58,12 @@ struct MlaArgs {
   const uint16_t* __restrict__ q;        // [B, H, 576]
   const uint16_t* __restrict__ lat;      // [slots, PT, 576]
   const int32_t* __restrict__ table;     // [B, max_pages]
-  const int32_t* __restrict__ ctx_lens;  // [B]
+  const int32_t* __restrict__ ctx_lens;  // [B] (sparse: selected counts)
   float* __restrict__ part_o;            // [B, NR, H, 512]
   float* __restrict__ part_ml;           // [B, NR, H, 2]
-  int B, H, NR, max_pages, pt_shift, num_slots;
+  const int32_t* __restrict__ sel;       // sparse: [B, sel_stride] positions, ascending
+  int B, H, NR, max_pages, pt_shift, num_slots, sel_stride;
+  uint32_t pool_bytes;                   // sparse: bytes of the latent pool (< 4 GiB)
   float scale_log2e;
 };
 
@@ -78,7 +80,16 @@ constexpr int kLoadsPerWave = (kLoadsPerTile + kMlaWaves - 1) / kMlaWaves;
 // read from LDS feeds HTW MFMAs; a wave holds q for HTW head tiles.  HTW = 1:
 // q for two head tiles (2 x 18 k-steps) would exceed the 256 registers a
 // wavefront has at 2 per SIMD.
-template <int HG>
+//
+// SPARSE: the context of sequence b is the list of positions sel[b][0..n)
+// (the DSA top-k, runtime/glm.py:280-289) instead of positions 0..ctx-1.
+// Row j of tile t is position sel[b][64t + j]; each lane resolves one of the
+// tile's positions through the block table to a byte offset in the pool, and
+// the direct-to-LDS loads take per-lane offsets into one descriptor over the
+// whole pool, so the selected rows are gathered on the way into LDS with no
+// intermediate copy.  Rows past n, and the padding chunks, use an offset past
+// the descriptor's end and land as zeros.
+template <int HG, bool SPARSE>
 __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
   constexpr int HTW = 1;
   constexpr int NHT = HG / 16;               // 16-head tiles in the group
@@ -117,7 +128,7 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
   const int b = task / a.NR;
   const int range = task - b * a.NR;
   int ctx = a.ctx_lens[b];
-  const int cap = a.max_pages << a.pt_shift;
+  const int cap = SPARSE ? a.sel_stride : a.max_pages << a.pt_shift;
   ctx = uniform(ctx < 0 ? 0 : (ctx > cap ? cap : ctx));
   const int n_tiles = (ctx + kTile - 1) / kTile;
   const int per = (n_tiles + a.NR - 1) / a.NR;
@@ -183,6 +194,41 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
   // Issues the loads of tile t into LDS buffer dst; tokens at or past the
   // context end read as zeros (the descriptor covers only valid rows).
   auto load_tile = [&](int t, uint16_t* dst) {
+    if constexpr (SPARSE) {
+      // lane j resolves position sel[b][64t + j] to its row's byte offset
+      const int tok = t * kTile + lane;
+      uint32_t row_off = 0xFFFFFFF0u;
+      if (tok < ctx) {
+        const int pos = a.sel[static_cast<size_t>(b) * a.sel_stride + tok];
+        const int page = pos >> a.pt_shift;
+        int slot = 0;
+        if (pos >= 0 && page < a.max_pages) slot = trow[page];
+        if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
+        const long long row = (static_cast<long long>(slot) << a.pt_shift) +
+                              (pos >= 0 ? (pos & ((1 << a.pt_shift) - 1)) : 0);
+        row_off = static_cast<uint32_t>(row * (kLat * 2));
+      }
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(a.lat), static_cast<short>(0), static_cast<int>(a.pool_bytes),
+          0x00020000);
+#pragma unroll
+      for (int k = 0; k < kLoadsPerWave; ++k) {
+        const int i = w + kMlaWaves * k;
+        const int j = 64 * i + lane;
+        const int row = j / kRowChunks;
+        const int col = j - row * kRowChunks;
+        // every lane takes part in the cross-lane read
+        const uint32_t base = static_cast<uint32_t>(__shfl(static_cast<int>(row_off), row & 63));
+        const uint32_t off =
+            (row < kTile && col < kChunksPerRow && base != 0xFFFFFFF0u) ? base + col * 16
+                                                                         : 0xFFFFFFF0u;
+        if (i < kLoadsPerTile) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + i * 64 * 8), 16,
+                                                   static_cast<int>(off), 0, 0, 0);
+        }
+      }
+      return;
+    }
     const int page = t >> tile_shift;
     const int sub = t - (page << tile_shift);
     if (page >= tab_base + 64) {
@@ -473,6 +519,31 @@ int default_ranges(int B, int H) {
   return nr < 1 ? 1 : nr;
 }
 
+// Latent kernel (dense or sparse) and the range reduce.
+int launch_mla(const MlaArgs& a, int hg, bool sparse, long long grid, uint16_t* out,
+               float* lse_out, hipStream_t stream) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (hg == 64) {
+    if (sparse) {
+      hipLaunchKernelGGL((mla_latent_kernel<64, true>), g, dim3(kMlaThreads), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((mla_latent_kernel<64, false>), g, dim3(kMlaThreads), 0, stream, a);
+    }
+  } else {
+    if (sparse) {
+      hipLaunchKernelGGL((mla_latent_kernel<32, true>), g, dim3(kMlaThreads), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((mla_latent_kernel<32, false>), g, dim3(kMlaThreads), 0, stream, a);
+    }
+  }
+  int rc = VOOM_LAUNCH_CHECK("mla: latent kernel launch");
+  if (rc) return rc;
+  const unsigned red_grid = static_cast<unsigned>((a.B * a.H + 3) / 4);
+  hipLaunchKernelGGL(mla_reduce_kernel, dim3(red_grid), dim3(kThreads), 0, stream, a.part_o,
+                     a.part_ml, out, lse_out, a.B, a.H, a.NR);
+  return VOOM_LAUNCH_CHECK("mla: reduce kernel launch");
+}
+
 }  // namespace
 }  // namespace voom
 
@@ -533,18 +604,64 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
   a.pt_shift = ilog2(page_tokens);
   a.num_slots = num_slots;
   a.scale_log2e = scale * 1.4426950408889634f;
-  if (hg == 64) {
-    hipLaunchKernelGGL(mla_latent_kernel<64>, dim3(static_cast<unsigned>(grid)),
-                       dim3(kMlaThreads), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL(mla_latent_kernel<32>, dim3(static_cast<unsigned>(grid)),
-                       dim3(kMlaThreads), 0, stream, a);
-  }
-  int rc = VOOM_LAUNCH_CHECK("mla_absorbed_decode: latent kernel launch");
-  if (rc) return rc;
-  const unsigned red_grid = static_cast<unsigned>((batch * num_heads + 3) / 4);
-  hipLaunchKernelGGL(mla_reduce_kernel, dim3(red_grid), dim3(kThreads), 0, stream, a.part_o,
-                     a.part_ml, static_cast<uint16_t*>(out_c), lse_out, batch, num_heads,
-                     num_ranges);
-  return VOOM_LAUNCH_CHECK("mla_absorbed_decode: reduce kernel launch");
+  a.sel = nullptr;
+  a.sel_stride = 0;
+  a.pool_bytes = 0;
+  return launch_mla(a, hg, false, grid, static_cast<uint16_t*>(out_c), lse_out, stream);
+}
+
+extern "C" int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool,
+                                      const int32_t* block_table, const int32_t* sel,
+                                      const int32_t* sel_lens, void* out_c, float* lse_out,
+                                      void* workspace, size_t ws_bytes, int batch, int num_heads,
+                                      int latent_dim, int c_dim, int page_tokens, int max_pages,
+                                      int num_slots, int sel_stride, float scale, int num_ranges,
+                                      hipStream_t stream) {
+  const char* who = "mla_sparse_decode";
+  VOOM_REQUIRE(q_lat && lat_pool && block_table && sel && sel_lens && out_c && workspace,
+               "%s: null pointer argument", who);
+  VOOM_REQUIRE(latent_dim == kLat && c_dim == kC, "%s: latent %d / c_dim %d unsupported (576 / 512)",
+               who, latent_dim, c_dim);
+  VOOM_REQUIRE(batch > 0 && num_heads > 0 && num_heads % 32 == 0,
+               "%s: num_heads %d must be a positive multiple of 32", who, num_heads);
+  VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens >= kTile && page_tokens <= 4096,
+               "%s: page_tokens %d must be a power of two in [64, 4096]", who, page_tokens);
+  VOOM_REQUIRE(max_pages > 0 && num_slots > 0 && sel_stride > 0, "%s: empty table, pool or selection",
+               who);
+  const unsigned long long pool =
+      static_cast<unsigned long long>(num_slots) * page_tokens * kLat * 2;
+  VOOM_REQUIRE(pool < 0xFFFF0000ull,
+               "%s: latent pool of %llu bytes exceeds the 4 GiB a gathered load can address", who,
+               pool);
+  if (num_ranges <= 0) num_ranges = default_ranges(batch, num_heads);
+  const size_t need = voom_mla_workspace_bytes(batch, num_heads, num_ranges);
+  VOOM_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(q_lat) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(lat_pool) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "%s: q, pool and workspace must be 16-byte aligned", who);
+  const int hg = heads_per_group(num_heads);
+  const long long grid = static_cast<long long>(batch) * num_ranges * (num_heads / hg);
+  VOOM_REQUIRE(grid < (1LL << 31), "%s: grid too large", who);
+
+  const size_t n = static_cast<size_t>(batch) * num_ranges * num_heads;
+  MlaArgs a;
+  a.q = static_cast<const uint16_t*>(q_lat);
+  a.lat = static_cast<const uint16_t*>(lat_pool);
+  a.table = block_table;
+  a.ctx_lens = sel_lens;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                       ((n * kC * sizeof(float) + 255) & ~size_t(255)));
+  a.sel = sel;
+  a.B = batch;
+  a.H = num_heads;
+  a.NR = num_ranges;
+  a.max_pages = max_pages;
+  a.pt_shift = ilog2(page_tokens);
+  a.num_slots = num_slots;
+  a.sel_stride = sel_stride;
+  a.pool_bytes = static_cast<uint32_t>(pool);
+  a.scale_log2e = scale * 1.4426950408889634f;
+  return launch_mla(a, hg, true, grid, static_cast<uint16_t*>(out_c), lse_out, stream);
 }

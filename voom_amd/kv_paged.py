@@ -1039,7 +1039,7 @@ class PagedKVCache:
 
     def attend_mla(self, layer: int, q_nope: torch.Tensor, q_rope: torch.Tensor,
                    w_uk: torch.Tensor, w_uv_t: torch.Tensor, scale: float,
-                   return_weighted_c: bool = False):
+                   return_weighted_c: bool = False, selection=None):
         """Absorbed-MLA decode over the layer's latent pages (runtime/glm.py:78-202).
 
         q_nope [B, H, dn], q_rope [B, H, 64] bf16 (one query token); W_UK
@@ -1048,9 +1048,19 @@ class PagedKVCache:
         is contracted with the paged latent in the HIP kernel (resident pages
         first, spilled pages chunk by chunk as they land, LSE-merged), and
         weighted_c . W_UV gives the per-head output [B, H, dv] before o_proj.
+
+        ``selection``: the DSA top-k of this step (runtime/glm.py:280-289) --
+        ascending positions [B, k] int32 (or [B, 1, k] as DSAState returns
+        them), optionally with their counts as ``(sel, sel_lens)``.  The
+        contraction then runs over those rows only, read straight from the
+        pages; spilled pages that the selection touches are reloaded first.
         """
         self._require_kind(layer, "latent")
         q_lat = ops.mla_absorb_query(q_nope, q_rope, w_uk)
+        if selection is not None:
+            wc = self._attend_selected(layer, q_lat, selection, scale)
+            out = ops.mla_project_out(wc, w_uv_t)
+            return (out, wc) if return_weighted_c else out
 
         def run(pool, table, ctx, lse):
             return ops.mla_latent_decode(q_lat, pool.lat, table, ctx, scale=scale,
@@ -1059,6 +1069,35 @@ class PagedKVCache:
         wc = self._attend_pages(layer, run)
         out = ops.mla_project_out(wc, w_uv_t)
         return (out, wc) if return_weighted_c else out
+
+    def _attend_selected(self, layer: int, q_lat: torch.Tensor, selection, scale: float):
+        if isinstance(selection, tuple):
+            sel, sel_lens = selection
+        else:
+            sel, sel_lens = selection, None
+        if sel.dim() == 3:
+            sel = sel[:, 0]
+        sel = sel.to(device=self.device, dtype=torch.int32).contiguous()
+        B, k = sel.shape
+        if sel_lens is None:
+            sel_lens = torch.full((B,), min(k, self._len[layer]), dtype=torch.int32,
+                                  device=self.device)
+        else:
+            sel_lens = sel_lens.to(device=self.device, dtype=torch.int32).contiguous()
+        spilled = {p.index: p for p in self._pages[layer] if not p.resident}
+        if spilled:
+            # the pages this selection reads must be resident (one host sync,
+            # only when the layer has spilled pages)
+            used = sel.cpu().numpy()
+            counts = sel_lens.cpu().numpy()
+            need = set()
+            for b in range(B):
+                need.update((used[b, :counts[b]] // self.page_positions).tolist())
+            pages = [spilled[i] for i in sorted(need) if i in spilled]
+            if pages:
+                self.reload(pages)
+        return ops.mla_sparse_decode(q_lat, self._pool(layer).lat, self._tables[layer], sel,
+                                     sel_lens, scale=scale)
 
     def _attend_pages(self, layer: int, run) -> torch.Tensor:
         """Drive ``run(pool, block_table, ctx_lens, return_lse)`` over a layer:

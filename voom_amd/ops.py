@@ -316,6 +316,87 @@ def mla_latent_decode(q_lat: torch.Tensor, lat_pool: torch.Tensor, block_table: 
     return (out, lse) if return_lse else out
 
 
+def mla_sparse_decode(q_lat: torch.Tensor, lat_pool: torch.Tensor, block_table: torch.Tensor,
+                      sel: torch.Tensor, sel_lens: torch.Tensor, *, scale: float,
+                      out: torch.Tensor | None = None, return_lse: bool = False,
+                      num_ranges: int = 0, ws: torch.Tensor | None = None,
+                      stream: torch.cuda.Stream | None = None):
+    """Latent contraction over the DSA-selected positions of each sequence.
+
+    sel [B, k] int32 ascending logical positions, sel_lens [B] int32 (how many
+    of each row are used); the rows are read through block_table from the
+    pool, the gather of runtime/glm.py:280-289 fused into the contraction.
+    Returns weighted_c [B, H, 512] bf16 (and the fp32 LSE with return_lse).
+    """
+    dev = _require_device(q_lat, lat_pool, block_table, sel, sel_lens, out)
+    _require(q_lat.dim() == 3 and lat_pool.dim() == 3, "q_lat [B,H,576], lat_pool [slots,PT,576]")
+    B, H, LD = q_lat.shape
+    slots, PT, LD2 = lat_pool.shape
+    _require(LD == LD2 == 576, "latent width must be 576 (512 + 64)")
+    _require(q_lat.dtype == lat_pool.dtype == torch.bfloat16, "q_lat and lat_pool must be bf16")
+    _require(block_table.dtype == sel.dtype == sel_lens.dtype == torch.int32,
+             "block_table, sel and sel_lens must be int32")
+    _require(block_table.dim() == 2 and block_table.shape[0] == B and sel.dim() == 2
+             and sel.shape[0] == B and tuple(sel_lens.shape) == (B,),
+             "block_table [B, max_pages], sel [B, k], sel_lens [B]")
+    need = mla_workspace_bytes(B, H, num_ranges)
+    if ws is None:
+        ws = workspace(dev, need, tag=2)
+    _require(ws.numel() * ws.element_size() >= need, "workspace too small")
+    if out is None:
+        out = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, H), dtype=torch.float32, device=dev) if return_lse else None
+    _lib.call("voom_mla_sparse_decode", _ptr(q_lat), _ptr(lat_pool), _ptr(block_table),
+              _ptr(sel), _ptr(sel_lens), _ptr(out), _ptr(lse), _ptr(ws), need, B, H, LD, 512, PT,
+              block_table.shape[1], slots, sel.shape[1], float(scale), int(num_ranges),
+              _stream(stream))
+    return (out, lse) if return_lse else out
+
+
+def dsa_index_scores(q_idx: torch.Tensor, w_head: torch.Tensor, k_idx: torch.Tensor,
+                     lens: torch.Tensor, *, scale: float, out: torch.Tensor | None = None,
+                     stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Lightning-indexer scores of a decode step (runtime/glm_dsa.py:140-150).
+
+    q_idx [B, NH, 128] bf16 (after the indexer RoPE), w_head [B, NH] fp32
+    (weights_proj output times NH^-0.5), k_idx [B, cap, 128] bf16, lens [B]
+    int32.  Returns scores [B, cap] fp32; entries at or past lens[b] are left
+    as they were.
+    """
+    dev = _require_device(q_idx, w_head, k_idx, lens, out)
+    _require(q_idx.dim() == 3 and k_idx.dim() == 3 and w_head.dim() == 2,
+             "q_idx [B,NH,D], w_head [B,NH], k_idx [B,cap,D]")
+    B, NH, D = q_idx.shape
+    _require(k_idx.shape[0] == B and k_idx.shape[2] == D and tuple(w_head.shape) == (B, NH)
+             and tuple(lens.shape) == (B,), "inconsistent DSA shapes")
+    _require(q_idx.dtype == k_idx.dtype == torch.bfloat16 and w_head.dtype == torch.float32
+             and lens.dtype == torch.int32, "q_idx/k_idx bf16, w_head fp32, lens int32")
+    cap = k_idx.shape[1]
+    if out is None:
+        out = torch.empty((B, cap), dtype=torch.float32, device=dev)
+    _require(tuple(out.shape) == (B, cap) and out.dtype == torch.float32, "scores [B, cap] fp32")
+    _lib.call("voom_dsa_index_scores", _ptr(q_idx), _ptr(w_head), _ptr(k_idx), _ptr(lens),
+              _ptr(out), B, NH, D, cap, float(scale), _stream(stream))
+    return out
+
+
+def dsa_topk(scores: torch.Tensor, lens: torch.Tensor, k: int, *,
+             stream: torch.cuda.Stream | None = None):
+    """Top-k of each row's first lens[b] scores as ascending int32 indices
+    (runtime/glm_dsa.py:151-160).  Returns (sel [B, k], sel_lens [B]);
+    sel_lens[b] = min(lens[b], k), entries past it are unspecified."""
+    dev = _require_device(scores, lens)
+    _require(scores.dim() == 2 and scores.dtype == torch.float32, "scores [B, cap] fp32")
+    _require(lens.dtype == torch.int32 and tuple(lens.shape) == (scores.shape[0],), "lens [B] int32")
+    _require(int(k) > 0, "k must be positive")
+    B, cap = scores.shape
+    sel = torch.empty((B, int(k)), dtype=torch.int32, device=dev)
+    sel_lens = torch.empty((B,), dtype=torch.int32, device=dev)
+    _lib.call("voom_dsa_topk", _ptr(scores), _ptr(lens), _ptr(sel), _ptr(sel_lens), B, cap,
+              int(k), _stream(stream))
+    return sel, sel_lens
+
+
 def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
     """kv_b_proj weight [H*(dn+dv), C] -> (W_UK [H, dn, C], W_UV^T [H, C, dv]), contiguous.
 
