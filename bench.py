@@ -628,6 +628,104 @@ def bench_position_free(steps: int, warmup: int, cpu_sample: bool) -> dict:
     return res
 
 
+def bench_dsa(steps: int, warmup: int, cpu_sample: bool) -> dict:
+    """DSA decode step (SURVEY next row 4): B=1, 131,072 cached tokens, index
+    keys [131072, 128] bf16, 32 index heads, top-2048, then the absorbed-MLA
+    contraction (128 heads, latent 576 in 64-token pages) over the selected
+    rows only.  Eight rotating index-key sets (8 x 33.5 MB) keep the scoring
+    kernel's reads out of the Infinity Cache.  Timed per kernel with HIP
+    events; the scoring kernel's algorithmic bytes are the index keys (256 B
+    per token) plus q, w and the scores it writes (4 B per token)."""
+    import numpy as np
+    import torch
+
+    from voom_amd import ops, synthetic
+
+    S, NH, K, H = 131072, 32, 2048, 128
+    log("dsa: 8 rotating index-key sets of 131072 x 128 bf16, top-2048, 128 MLA heads")
+    g = torch.Generator(device="cuda").manual_seed(40)
+    keys = [torch.randn((1, S, 128), generator=g, device="cuda").to(torch.bfloat16)
+            for _ in range(8)]
+    q_idx = torch.randn((1, NH, 128), generator=g, device="cuda").to(torch.bfloat16)
+    w_head = (torch.randn((1, NH), generator=g, device="cuda") * NH ** -0.5).float()
+    lens = torch.tensor([S], dtype=torch.int32, device="cuda")
+    scores = torch.empty((1, S), dtype=torch.float32, device="cuda")
+    inp = synthetic.mla_decode_inputs(batch=1, heads=H, ctx=S, seed=41)
+    w_uk, _ = ops.split_kv_b(inp.kv_b, H, inp.dn, inp.dv)
+    q_abs = torch.bmm(inp.q_nope.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
+    q_lat = torch.cat([q_abs, inp.q_rope], -1).contiguous()
+    out_c = torch.empty((1, H, 512), dtype=torch.bfloat16, device="cuda")
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    t_sc = t_tk = t_mla = 0.0
+    sel = sel_lens = None
+    for i in range(warmup + steps):
+        ev[0].record()
+        ops.dsa_index_scores(q_idx, w_head, keys[i % 8], lens, scale=128 ** -0.5, out=scores)
+        ev[1].record()
+        sel, sel_lens = ops.dsa_topk(scores, lens, K)
+        ev[2].record()
+        ops.mla_sparse_decode(q_lat, inp.lat_pool, inp.block_table, sel, sel_lens,
+                              scale=inp.scale, out=out_c)
+        ev[3].record()
+        if i >= warmup:
+            torch.cuda.synchronize()
+            t_sc += ev[0].elapsed_time(ev[1]) / 1e3
+            t_tk += ev[1].elapsed_time(ev[2]) / 1e3
+            t_mla += ev[2].elapsed_time(ev[3]) / 1e3
+    t_sc, t_tk, t_mla = t_sc / steps, t_tk / steps, t_mla / steps
+    sc_bytes = S * 128 * 2 + NH * 128 * 2 + NH * 4 + S * 4
+    sel_bytes = K * 576 * 2 + H * 576 * 2 + H * 512 * 2 + K * 4
+    # the dense contraction the selection replaces, same cache
+    d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens, scale=inp.scale,
+                          out=out_c)
+    d0.record()
+    for _ in range(steps):
+        ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                              scale=inp.scale, out=out_c)
+    d1.record()
+    torch.cuda.synchronize()
+    t_dense = d0.elapsed_time(d1) / steps / 1e3
+    res = {
+        "workload": "DSA decode: B=1, 131072 cached tokens, index 32 heads x 128 bf16, top-2048, "
+                    "absorbed MLA 128 heads over the selected latent rows (64-token pages)",
+        "index_scores_us": t_sc * 1e6,
+        "index_scores_gbs": sc_bytes / t_sc / 1e9,
+        "index_scores_hbm_frac": sc_bytes / t_sc / 1e9 / HBM_PEAK_GBS,
+        "topk_us": t_tk * 1e6,
+        "sparse_mla_us": t_mla * 1e6,
+        "step_us": (t_sc + t_tk + t_mla) * 1e6,
+        "dense_mla_same_cache_us": t_dense * 1e6,
+        "index_scores_bytes": sc_bytes,
+        "sparse_mla_bytes": sel_bytes,
+    }
+    log(f"dsa: scores {t_sc * 1e6:.1f} us ({res['index_scores_gbs']:.0f} GB/s), top-k "
+        f"{t_tk * 1e6:.1f} us, sparse MLA {t_mla * 1e6:.1f} us; dense MLA over all "
+        f"{S} tokens {t_dense * 1e6:.1f} us")
+    if cpu_sample:
+        from oracle import dsa as odsa
+
+        kk = keys[(warmup + steps - 1) % 8][0].float().cpu().numpy()
+        qq = q_idx[0].float().cpu().numpy()
+        ww = w_head[0].cpu().numpy()
+        t0 = time.perf_counter()
+        ref = odsa.select(qq, ww, kk, S, K, 128 ** -0.5)
+        dt = time.perf_counter() - t0
+        ref_sc = odsa.index_scores(qq, ww, kk, 128 ** -0.5)
+        kth = np.sort(ref_sc)[::-1][K - 1]
+        got = set(sel[0].cpu().numpy().tolist())
+        off = [i for i in got ^ set(ref.tolist())
+               if abs(ref_sc[i] - kth) > 1e-5 * abs(kth) + 1e-5]
+        res["cpu_baseline"] = {"value": S / dt, "unit": "keys/s (scores + top-k)",
+                               "cores": cpu_threads(), "kind": "port",
+                               "sample": "one selection over 131072 keys, numpy, oracle/dsa.py"}
+        res["selection_matches_oracle"] = not off
+    del keys
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_e2e(cpu_sample: bool) -> dict:
     """Config 1: SmolLM2-135M-shaped decoder, random N(0, 0.02) bf16 weights
     (seed 0), a 512-token prompt of uniform ids (seed 1), greedy decode of 128
@@ -713,9 +811,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="gqa,spill,long,mla,pf,e2e",
+    ap.add_argument("--only", default="gqa,spill,long,mla,pf,dsa,e2e",
                     help="comma list of legs: gqa (config 2, headline), spill (config 3), "
-                         "long (config 4), mla (config 5), pf (position-free), e2e (config 1)")
+                         "long (config 4), mla (config 5), pf (position-free), dsa (DSA decode), "
+                         "e2e (config 1)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a known-size 1 GiB streaming kernel (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -775,6 +874,8 @@ def main() -> int:
     if "pf" in legs:
         extra["position_free"] = bench_position_free(args.steps, args.warmup,
                                                      cpu_sample=not args.no_cpu)
+    if "dsa" in legs:
+        extra["dsa"] = bench_dsa(args.steps, args.warmup, cpu_sample=not args.no_cpu)
     if "e2e" in legs:
         extra["e2e"] = bench_e2e(cpu_sample=not args.no_cpu)
     if extra:

@@ -131,8 +131,10 @@ int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
  * (runtime/glm.py:280-289).  sel [batch, sel_stride] int32 holds ascending
  * logical positions (voom_dsa_topk's output), sel_lens [batch] how many are
  * used; the rows are read through block_table straight from the pool (no
- * gathered copy).  The pool must be smaller than 4 GiB.  The workspace is
- * voom_mla_workspace_bytes(batch, num_heads, num_ranges). */
+ * gathered copy).  The pool must be smaller than 4 GiB.  num_ranges 0 picks
+ * a split sized to the selection; the workspace must hold
+ * voom_mla_sparse_workspace_bytes(batch, num_heads, sel_stride, num_ranges). */
+size_t voom_mla_sparse_workspace_bytes(int batch, int num_heads, int sel_stride, int num_ranges);
 int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool, const int32_t* block_table,
                            const int32_t* sel, const int32_t* sel_lens, void* out_c,
                            float* lse_out, void* workspace, size_t ws_bytes, int batch,
@@ -156,13 +158,16 @@ int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool, const int32_
  * scores of keys s < lens[b] (causal for a decode step at position
  * lens[b] - 1), written to sel [batch, k] as ascending indices, with
  * sel_lens[b] = min(lens[b], k).  Among keys tied at the k-th score the
- * lowest indices are kept.
+ * lowest indices are kept.  The workspace (candidate slots) must hold
+ * voom_dsa_topk_workspace_bytes(batch, cap) bytes.
  * ------------------------------------------------------------------------- */
 int voom_dsa_index_scores(const void* q_idx, const float* w_head, const void* k_idx,
                           const int32_t* lens, float* scores, int batch, int num_heads,
                           int head_dim, int cap, float scale, hipStream_t stream);
+size_t voom_dsa_topk_workspace_bytes(int batch, int cap);
 int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* sel, int32_t* sel_lens,
-                  int batch, int cap, int k, hipStream_t stream);
+                  void* workspace, size_t ws_bytes, int batch, int cap, int k,
+                  hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Position-free paged attention (keys stored before RoPE).

@@ -109,8 +109,9 @@ def _q_lat(inp):
     return torch.cat([q_abs, inp.q_rope], -1).contiguous()
 
 
-@pytest.mark.parametrize("nr", [0, 1, 5])
+@pytest.mark.parametrize("nr", [10, 16, 40])
 def test_sparse_over_all_positions_equals_dense(nr):
+    """Same range split (so the same rounding), same rows: bit for bit."""
     print(f"[dsa] sparse == dense nr={nr}", flush=True)
     inp = synthetic.mla_decode_inputs(batch=2, heads=64, ctx_lens=[1000, 2500], slack_pages=2)
     q = _q_lat(inp)
@@ -160,6 +161,11 @@ def test_sparse_validation():
     with pytest.raises(ValueError):
         ops.dsa_topk(torch.zeros((1, 8), device="cuda"), torch.ones(1, dtype=torch.int32,
                                                                      device="cuda"), 0)
+    # a range may hold at most four 64-row tiles: 600 positions need 3 ranges
+    sel = torch.zeros((1, 600), dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="ranges"):
+        ops.mla_sparse_decode(q, inp.lat_pool, inp.block_table, sel, inp.ctx_lens, scale=1.0,
+                              num_ranges=2)
 
 
 def test_dsa_state_selects_like_the_oracle():

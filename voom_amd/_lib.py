@@ -37,12 +37,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "voom_mla_absorbed_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int,
                                          c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P]),
+    "voom_mla_sparse_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "voom_mla_sparse_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int,
                                        c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
                                        _P]),
     "voom_dsa_index_scores": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_float,
                                       _P]),
-    "voom_dsa_topk": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),
+    "voom_dsa_topk_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "voom_dsa_topk": (c_int, [_P, _P, _P, _P, _P, c_size_t, c_int, c_int, c_int, _P]),
     "voom_position_free_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "voom_position_free_attention": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_size_t,
                                              c_int, c_int, c_int, c_int, c_int, c_int, c_int,

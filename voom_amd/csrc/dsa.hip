@@ -18,12 +18,15 @@
 // weights and the head sum stay in registers plus two cross-group adds.
 //
 // Top-k: one workgroup of 1024 threads per row.  Scores map to order-
-// preserving 32-bit keys; three radix passes (11, 11 and 10 bits) with LDS
-// histograms find the k-th largest key T and how many keys equal to T to
-// keep.  Two ordered passes then write the selection: each wavefront owns a
-// contiguous index range, counts its keys above T and equal to T, and after
-// an exclusive scan over wavefronts writes its indices in order, so the
-// output is sorted without a sort.
+// preserving 32-bit keys.  A strided sample places a first threshold; one
+// pass counts the keys above it and a second moves them, in index order, into
+// LDS (at most 16,384), so the row is read from memory about twice.  Three
+// radix passes (11, 11 and 10 bits) over the LDS candidates then find the
+// k-th largest key T and how many keys equal to T to keep, and an ordered
+// write -- each wavefront owns a contiguous range, counts its keys above and
+// equal to T, and after an exclusive scan over wavefronts writes its indices
+// -- leaves the output sorted without a sort.  When the sample misjudges the
+// row, the same exact selection runs over the row in memory.
 #include "common.h"
 
 namespace voom {
@@ -93,6 +96,8 @@ __global__ __launch_bounds__(kScoreThreads) void dsa_scores_kernel(DsaScoreArgs 
       for (int s = 0; s < kDsaSteps; ++s) kop[it][tt][s] = *reinterpret_cast<const u32x4*>(kr + 32 * s);
     }
   }
+  // every load above issues before the first MFMA (one memory round trip)
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int it = 0; it < kItersPerWave; ++it) {
 #pragma unroll
@@ -150,59 +155,92 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* tmp, int& total)
   return before + inc - x;
 }
 
-__global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(const float* __restrict__ scores,
-                                                                const int32_t* __restrict__ lens,
-                                                                int32_t* __restrict__ sel,
-                                                                int32_t* __restrict__ sel_lens,
-                                                                int cap, int K) {
-  __shared__ int hist[2048];
-  __shared__ int scan_tmp[kTopkWaves];
-  __shared__ int found[2];
-  __shared__ int wave_gt[kTopkWaves];
-  __shared__ int wave_eq[kTopkWaves];
+constexpr int kCandCap = 16384;  // candidate keys held in LDS
+constexpr int kSample = 4096;    // keys sampled to place the threshold
+constexpr int kChunkKeys = 4096; // keys per compaction workgroup
+constexpr int kCompactThreads = 256;
+
+// Radix select over `count` keys read by key(i): the rank-th largest key T
+// (rank >= 1) and how many keys equal to T belong to the top `rank` (kk).
+// The digits start below the leading bits that every key shares (from a
+// min/max reduction): scores of one row share their sign and most of their
+// exponent, and a first digit over those bits would send every key to a
+// handful of histogram bins, serialising the LDS atomics.  Passes of 11 bits
+// then walk down to bit 0; a thread adds runs of equal bins as one atomic.
+template <typename KeyFn>
+__device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* scan_tmp,
+                             int* found, uint32_t& T, int& kk_out) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
-  const int b = blockIdx.x;
-  int n = lens[b];
-  n = n < 0 ? 0 : (n > cap ? cap : n);
-  const float* sb = scores + static_cast<size_t>(b) * cap;
-  int32_t* ob = sel + static_cast<size_t>(b) * K;
-  if (n <= K) {  // every key is selected
-    for (int i = tid; i < n; i += kTopkThreads) ob[i] = i;
-    if (tid == 0) sel_lens[b] = n;
-    return;
+  uint32_t lo_k = 0xFFFFFFFFu;
+  uint32_t hi_k = 0u;
+  for (int i = tid; i < count; i += kTopkThreads) {
+    const uint32_t u = key(i);
+    lo_k = u < lo_k ? u : lo_k;
+    hi_k = u > hi_k ? u : hi_k;
   }
-
-  // ---- radix select of the K-th largest key ----
-  uint32_t prefix = 0;
-  uint32_t pmask = 0;
-  int kk = K;  // keys still to take at or below the current prefix
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo_k), o));
+    const uint32_t b = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi_k), o));
+    lo_k = a < lo_k ? a : lo_k;
+    hi_k = b > hi_k ? b : hi_k;
+  }
+  if (lane == 0) {
+    scan_tmp[wv] = static_cast<int>(lo_k);
+    hist[wv] = static_cast<int>(hi_k);
+  }
+  __syncthreads();
+  lo_k = 0xFFFFFFFFu;
+  hi_k = 0u;
+  for (int k = 0; k < kTopkWaves; ++k) {
+    const uint32_t a = static_cast<uint32_t>(scan_tmp[k]);
+    const uint32_t b = static_cast<uint32_t>(hist[k]);
+    lo_k = a < lo_k ? a : lo_k;
+    hi_k = b > hi_k ? b : hi_k;
+  }
+  __syncthreads();
+  // bits above `top` are common to every key
+  int top = 31 - __clz(static_cast<int>(lo_k ^ hi_k));  // -1 when all keys are equal
+  uint32_t prefix = top < 31 ? (hi_k & ~((2u << (top < 0 ? 0 : top)) - 1u)) : 0u;
+  if (top < 0) prefix = hi_k;
+  uint32_t pmask = top < 31 ? ~((2u << (top < 0 ? 0 : top)) - 1u) : 0u;
+  if (top < 0) pmask = 0xFFFFFFFFu;
+  int kk = rank;
 #pragma unroll 1
-  for (int p = 0; p < 3; ++p) {
-    const int shift = p == 0 ? 21 : (p == 1 ? 10 : 0);
-    const int bins = p == 2 ? 1024 : 2048;
-    for (int i = tid; i < bins; i += kTopkThreads) hist[i] = 0;
+  while (top >= 0) {
+    const int width = top + 1 < 11 ? top + 1 : 11;
+    const int shift = top + 1 - width;
+    const int bins = 1 << width;
+    for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
     __syncthreads();
-    for (int i = tid; i < n; i += kTopkThreads) {
-      const uint32_t u = order_key(sb[i]);
-      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & (bins - 1)], 1);
+    int run_bin = -1;
+    int run_n = 0;
+    for (int i = tid; i < count; i += kTopkThreads) {
+      const uint32_t u = key(i);
+      if ((u & pmask) == prefix) {
+        const int bin = static_cast<int>((u >> shift) & static_cast<uint32_t>(bins - 1));
+        if (bin != run_bin) {
+          if (run_n) atomicAdd(&hist[run_bin], run_n);
+          run_bin = bin;
+          run_n = 0;
+        }
+        ++run_n;
+      }
     }
+    if (run_n) atomicAdd(&hist[run_bin], run_n);
     __syncthreads();
-    // bins in descending order: thread t holds bins - 1 - (E t + e), e < E
-    const int E = bins / kTopkThreads;
-    int c[2] = {0, 0};
-    int mine = 0;
-    for (int e = 0; e < E; ++e) {
-      c[e] = hist[bins - 1 - (E * tid + e)];
-      mine += c[e];
-    }
+    // bins in descending order, two per thread over the 2048-entry table
+    int c[2];
+    c[0] = hist[2047 - 2 * tid];
+    c[1] = hist[2046 - 2 * tid];
     int total;
-    int run = block_exclusive_scan(mine, scan_tmp, total);
-    for (int e = 0; e < E; ++e) {
+    int run = block_exclusive_scan(c[0] + c[1], scan_tmp, total);
+    for (int e = 0; e < 2; ++e) {
       if (run < kk && run + c[e] >= kk) {
-        found[0] = bins - 1 - (E * tid + e);  // the digit
-        found[1] = run;                       // keys above it
+        found[0] = 2047 - (2 * tid + e);  // the digit
+        found[1] = run;                   // keys above it
       }
       run += c[e];
     }
@@ -211,19 +249,30 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(const float* __r
     kk -= found[1];
     prefix |= static_cast<uint32_t>(d) << shift;
     pmask |= static_cast<uint32_t>(bins - 1) << shift;
+    top = shift - 1;
     __syncthreads();
   }
-  const uint32_t T = prefix;  // keys > T are all kept, kk of the keys == T
+  T = prefix;
+  kk_out = kk;
+}
 
-  // ---- ordered write: wave wv owns [lo, hi), 64 indices per step ----
-  const int per = ((n + kTopkWaves - 1) / kTopkWaves + kWave - 1) / kWave * kWave;
+// Ordered selection write: keys i < count in index order; every key > T and
+// the first kk keys == T go to out[] in that order, as idx(i).  Wavefront w
+// owns a contiguous range of i; counts, an exclusive scan over wavefronts,
+// then ballots place each index.
+template <typename KeyFn, typename IdxFn>
+__device__ void ordered_write(KeyFn key, IdxFn idx, int count, uint32_t T, int kk, int* wave_gt,
+                              int* wave_eq, int32_t* out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const int per = ((count + kTopkWaves - 1) / kTopkWaves + kWave - 1) / kWave * kWave;
   const int lo = wv * per;
-  const int hi = lo + per < n ? lo + per : n;
+  const int hi = lo + per < count ? lo + per : count;
   int gt = 0;
   int eq = 0;
   for (int i0 = lo; i0 < hi; i0 += kWave) {
     const int i = i0 + lane;
-    const uint32_t u = i < hi ? order_key(sb[i]) : 0u;
+    const uint32_t u = i < hi ? key(i) : 0u;
     gt += __popcll(__ballot(i < hi && u > T));
     eq += __popcll(__ballot(i < hi && u == T));
   }
@@ -238,20 +287,267 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(const float* __r
     gt_before += wave_gt[k];
     eq_before += wave_eq[k];
   }
-  int out = gt_before + (eq_before < kk ? eq_before : kk);  // selections before this wave
+  int pos = gt_before + (eq_before < kk ? eq_before : kk);  // selections before this wave
   int eq_seen = eq_before;
   for (int i0 = lo; i0 < hi; i0 += kWave) {
     const int i = i0 + lane;
-    const uint32_t u = i < hi ? order_key(sb[i]) : 0u;
+    const uint32_t u = i < hi ? key(i) : 0u;
     const bool is_gt = i < hi && u > T;
     const bool is_eq = i < hi && u == T;
     const unsigned long long eq_mask = __ballot(is_eq);
     const int eq_rank = eq_seen + __popcll(eq_mask & ((1ull << lane) - 1ull));
     const bool take = is_gt || (is_eq && eq_rank < kk);
     const unsigned long long take_mask = __ballot(take);
-    if (take) ob[out + __popcll(take_mask & ((1ull << lane) - 1ull))] = i;
-    out += __popcll(take_mask);
+    if (take) out[pos + __popcll(take_mask & ((1ull << lane) - 1ull))] = idx(i);
+    pos += __popcll(take_mask);
     eq_seen += __popcll(eq_mask);
+  }
+  __syncthreads();
+}
+
+// Workspace of the top-k (per row): the threshold T0, per-chunk candidate
+// counts, and per-chunk candidate slots of (key, index) pairs.
+struct TopkWs {
+  uint32_t* t0;     // [B]
+  int* counts;      // [B, chunks]
+  uint2* cand;      // [B, chunks, kChunkKeys]
+  int chunks;
+};
+
+__host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys - 1) / kChunkKeys; }
+
+// 1. Threshold: rows of at most kCandCap keys take every key as a candidate
+// (T0 = 0).  Longer rows: one radix-style histogram pass over a strided sample
+// of kSample keys, below the bits the sample's keys all share, places T0 at
+// the lower edge of the bin where the count from the top reaches 1.5 x the
+// sample's share of k, plus 32 -- a few more candidates than k, with margin.
+__global__ __launch_bounds__(kTopkThreads) void dsa_topk_threshold_kernel(
+    const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
+    int K) {
+  __shared__ int hist[2048];
+  __shared__ int scan_tmp[kTopkWaves];
+  __shared__ int found[2];
+  __shared__ uint32_t mm[2][kTopkWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
+  const int b = blockIdx.x;
+  int n = lens[b];
+  n = n < 0 ? 0 : (n > cap ? cap : n);
+  if (n <= kCandCap) {
+    if (tid == 0) ws.t0[b] = 0u;
+    return;
+  }
+  const float* sb = scores + static_cast<size_t>(b) * cap;
+  constexpr int kPer = kSample / kTopkThreads;
+  uint32_t u[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int j = tid + k * kTopkThreads;
+    u[k] = order_key(sb[static_cast<int>(static_cast<long long>(j) * n / kSample)]);
+  }
+  uint32_t lo_k = u[0], hi_k = u[0];
+#pragma unroll
+  for (int k = 1; k < kPer; ++k) {
+    lo_k = u[k] < lo_k ? u[k] : lo_k;
+    hi_k = u[k] > hi_k ? u[k] : hi_k;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo_k), o));
+    const uint32_t c = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi_k), o));
+    lo_k = a < lo_k ? a : lo_k;
+    hi_k = c > hi_k ? c : hi_k;
+  }
+  if (lane == 0) {
+    mm[0][wv] = lo_k;
+    mm[1][wv] = hi_k;
+  }
+  for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
+  __syncthreads();
+  lo_k = mm[0][0];
+  hi_k = mm[1][0];
+  for (int k = 1; k < kTopkWaves; ++k) {
+    lo_k = mm[0][k] < lo_k ? mm[0][k] : lo_k;
+    hi_k = mm[1][k] > hi_k ? mm[1][k] : hi_k;
+  }
+  const int top = 31 - __clz(static_cast<int>(lo_k ^ hi_k));
+  if (top < 0) {  // the sample is one value: take everything at or above it
+    if (tid == 0) ws.t0[b] = lo_k;
+    return;
+  }
+  const int width = top + 1 < 11 ? top + 1 : 11;
+  const int shift = top + 1 - width;
+  const uint32_t common = top < 31 ? (hi_k & ~((2u << top) - 1u)) : 0u;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    atomicAdd(&hist[(u[k] >> shift) & static_cast<uint32_t>((1 << width) - 1)], 1);
+  }
+  __syncthreads();
+  long long r = (static_cast<long long>(K) * kSample + n - 1) / n;
+  r = r + r / 2 + 32;
+  const int want = static_cast<int>(r > kSample ? kSample : r);
+  int c[2];
+  c[0] = hist[2047 - 2 * tid];
+  c[1] = hist[2046 - 2 * tid];
+  int total;
+  int run = block_exclusive_scan(c[0] + c[1], scan_tmp, total);
+  for (int e = 0; e < 2; ++e) {
+    if (run < want && run + c[e] >= want) found[0] = 2047 - (2 * tid + e);
+    run += c[e];
+  }
+  __syncthreads();
+  if (tid == 0) ws.t0[b] = common | (static_cast<uint32_t>(found[0]) << shift);
+}
+
+// 2. Compaction: one workgroup per chunk of kChunkKeys keys of a row; every
+// key >= T0 goes, with its index and in index order, to the chunk's slots.
+// Each lane holds 16 keys in registers (the row is read once).
+template <bool VEC>
+__global__ __launch_bounds__(kCompactThreads) void dsa_topk_compact_kernel(
+    const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
+    int K) {
+  constexpr int kPerLane = kChunkKeys / kCompactThreads;  // 16, four groups of 4
+  __shared__ int wave_cnt[kCompactThreads / kWave];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
+  const int b = blockIdx.y;
+  const int chunk = blockIdx.x;
+  int n = lens[b];
+  n = n < 0 ? 0 : (n > cap ? cap : n);
+  if (n <= K) return;  // the select kernel takes every key; nothing to compact
+  const int c0 = chunk * kChunkKeys;
+  if (c0 >= n) return;
+  const float* sb = scores + static_cast<size_t>(b) * cap;
+  const uint32_t T0 = ws.t0[b];
+  // wave wv owns keys [c0 + wv*1024, +1024): 4 groups of 256, four keys per lane
+  const int base = c0 + wv * (kChunkKeys / (kCompactThreads / kWave));
+  float v[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = base + k * 256 + 4 * lane;
+    if constexpr (VEC) {
+      if (i < n) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(sb + i);
+        v[k][0] = t[0]; v[k][1] = t[1]; v[k][2] = t[2]; v[k][3] = t[3];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[k][e] = i + e < n ? sb[i + e] : 0.f;
+    }
+  }
+  bool in[4][4];
+  int cnt[4];
+  int mine = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    cnt[k] = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = base + k * 256 + 4 * lane + e;
+      in[k][e] = i < n && order_key(v[k][e]) >= T0;
+      cnt[k] += in[k][e] ? 1 : 0;
+    }
+    mine += cnt[k];
+  }
+  int wave_total = mine;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) wave_total += __shfl_xor(wave_total, o);
+  if (lane == 0) wave_cnt[wv] = wave_total;
+  __syncthreads();
+  int pos = 0;
+  int all = 0;
+  for (int k = 0; k < kCompactThreads / kWave; ++k) {
+    pos += k < wv ? wave_cnt[k] : 0;
+    all += wave_cnt[k];
+  }
+  uint2* slots = ws.cand + (static_cast<size_t>(b) * ws.chunks + chunk) * kChunkKeys;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int inc = wave_inclusive_scan(cnt[k], lane);
+    int at = pos + inc - cnt[k];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (in[k][e]) {
+        slots[at] = make_uint2(order_key(v[k][e]), static_cast<uint32_t>(base + k * 256 + 4 * lane + e));
+        ++at;
+      }
+    }
+    pos += __shfl(inc, kWave - 1);
+  }
+  if (tid == 0) ws.counts[static_cast<size_t>(b) * ws.chunks + chunk] = all;
+}
+
+// 3. Select: one workgroup per row.  The chunks' candidates, in chunk order
+// (index order), go to LDS when there are between k and kCandCap of them;
+// the exact selection and the ordered write run there.  Otherwise -- a
+// threshold that the sample misplaced -- the exact selection runs over the
+// row in memory.
+__global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
+    const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws,
+    int32_t* __restrict__ sel, int32_t* __restrict__ sel_lens, int cap, int K) {
+  __shared__ uint32_t cand_key[kCandCap];
+  __shared__ int32_t cand_idx[kCandCap];
+  __shared__ int hist[2048];
+  __shared__ int scan_tmp[kTopkWaves];
+  __shared__ int found[2];
+  __shared__ int wave_gt[kTopkWaves];
+  __shared__ int wave_eq[kTopkWaves];
+  __shared__ int chunk_off[2049];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  int n = lens[b];
+  n = n < 0 ? 0 : (n > cap ? cap : n);
+  const float* sb = scores + static_cast<size_t>(b) * cap;
+  int32_t* ob = sel + static_cast<size_t>(b) * K;
+  if (n <= K) {  // every key is selected
+    for (int i = tid; i < n; i += kTopkThreads) ob[i] = i;
+    if (tid == 0) sel_lens[b] = n;
+    return;
+  }
+  // candidate offsets of the row's chunks (up to 2048 chunks in LDS)
+  const int nch = (n + kChunkKeys - 1) / kChunkKeys;
+  const int* cnt = ws.counts + static_cast<size_t>(b) * ws.chunks;
+  int C = 0;
+  bool fits = nch <= 2048;
+  if (fits) {
+    int c2[2];
+    c2[0] = 2 * tid < nch ? cnt[2 * tid] : 0;
+    c2[1] = 2 * tid + 1 < nch ? cnt[2 * tid + 1] : 0;
+    int total;
+    const int run = block_exclusive_scan(c2[0] + c2[1], scan_tmp, total);
+    if (2 * tid < nch) chunk_off[2 * tid] = run;
+    if (2 * tid + 1 < nch) chunk_off[2 * tid + 1] = run + c2[0];
+    if (tid == 0) chunk_off[nch] = total;
+    C = total;
+    fits = C >= K && C <= kCandCap;
+    __syncthreads();
+  }
+  uint32_t T;
+  int kk;
+  if (fits) {
+    // flat candidate j -> its chunk by binary search over the offsets
+    for (int j = tid; j < C; j += kTopkThreads) {
+      int lo = 0, hi = nch;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (chunk_off[mid] <= j) lo = mid; else hi = mid;
+      }
+      const uint2 e = ws.cand[(static_cast<size_t>(b) * ws.chunks + lo) * kChunkKeys +
+                              (j - chunk_off[lo])];
+      cand_key[j] = e.x;
+      cand_idx[j] = static_cast<int32_t>(e.y);
+    }
+    __syncthreads();
+    auto lds_key = [&](int i) { return cand_key[i]; };
+    auto lds_idx = [&](int i) { return cand_idx[i]; };
+    radix_select(lds_key, C, K, hist, scan_tmp, found, T, kk);
+    ordered_write(lds_key, lds_idx, C, T, kk, wave_gt, wave_eq, ob);
+  } else {
+    auto mem_key = [&](int i) { return order_key(sb[i]); };
+    radix_select(mem_key, n, K, hist, scan_tmp, found, T, kk);
+    ordered_write(mem_key, [](int i) { return i; }, n, T, kk, wave_gt, wave_eq, ob);
   }
   if (tid == 0) sel_lens[b] = K;
 }
@@ -295,12 +591,48 @@ extern "C" int voom_dsa_index_scores(const void* q_idx, const float* w_head, con
   return VOOM_LAUNCH_CHECK("dsa_index_scores: kernel launch");
 }
 
+extern "C" size_t voom_dsa_topk_workspace_bytes(int batch, int cap) {
+  if (batch <= 0 || cap <= 0) return 0;
+  const size_t chunks = static_cast<size_t>(topk_chunks(cap));
+  return ((static_cast<size_t>(batch) * 4 + 255) & ~size_t(255)) +
+         ((static_cast<size_t>(batch) * chunks * 4 + 255) & ~size_t(255)) +
+         static_cast<size_t>(batch) * chunks * kChunkKeys * sizeof(uint2);
+}
+
 extern "C" int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* sel,
-                             int32_t* sel_lens, int batch, int cap, int k, hipStream_t stream) {
+                             int32_t* sel_lens, void* workspace, size_t ws_bytes, int batch,
+                             int cap, int k, hipStream_t stream) {
   const char* who = "dsa_topk";
-  VOOM_REQUIRE(scores && lens && sel && sel_lens, "%s: null pointer argument", who);
-  VOOM_REQUIRE(batch > 0 && cap > 0 && k > 0, "%s: bad batch, capacity or k", who);
-  hipLaunchKernelGGL(dsa_topk_kernel, dim3(static_cast<unsigned>(batch)), dim3(kTopkThreads), 0,
-                     stream, scores, lens, sel, sel_lens, cap, k);
-  return VOOM_LAUNCH_CHECK("dsa_topk: kernel launch");
+  VOOM_REQUIRE(scores && lens && sel && sel_lens && workspace, "%s: null pointer argument", who);
+  VOOM_REQUIRE(batch > 0 && batch < 65536 && cap > 0 && k > 0, "%s: bad batch, capacity or k",
+               who);
+  const size_t need = voom_dsa_topk_workspace_bytes(batch, cap);
+  VOOM_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+               "%s: workspace must be 16-byte aligned", who);
+  TopkWs ws;
+  ws.chunks = topk_chunks(cap);
+  char* p = static_cast<char*>(workspace);
+  const size_t t0_bytes = (static_cast<size_t>(batch) * 4 + 255) & ~size_t(255);
+  ws.t0 = reinterpret_cast<uint32_t*>(p);
+  ws.counts = reinterpret_cast<int*>(p + t0_bytes);
+  ws.cand = reinterpret_cast<uint2*>(
+      p + t0_bytes + ((static_cast<size_t>(batch) * ws.chunks * 4 + 255) & ~size_t(255)));
+  hipLaunchKernelGGL(dsa_topk_threshold_kernel, dim3(static_cast<unsigned>(batch)),
+                     dim3(kTopkThreads), 0, stream, scores, lens, ws, cap, k);
+  int rc = VOOM_LAUNCH_CHECK("dsa_topk: threshold kernel launch");
+  if (rc) return rc;
+  const dim3 cgrid(static_cast<unsigned>(ws.chunks), static_cast<unsigned>(batch));
+  if (cap % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0) {
+    hipLaunchKernelGGL(dsa_topk_compact_kernel<true>, cgrid, dim3(kCompactThreads), 0, stream,
+                       scores, lens, ws, cap, k);
+  } else {
+    hipLaunchKernelGGL(dsa_topk_compact_kernel<false>, cgrid, dim3(kCompactThreads), 0, stream,
+                       scores, lens, ws, cap, k);
+  }
+  rc = VOOM_LAUNCH_CHECK("dsa_topk: compaction kernel launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL(dsa_topk_select_kernel, dim3(static_cast<unsigned>(batch)),
+                     dim3(kTopkThreads), 0, stream, scores, lens, ws, sel, sel_lens, cap, k);
+  return VOOM_LAUNCH_CHECK("dsa_topk: select kernel launch");
 }

@@ -68,6 +68,7 @@ struct MlaArgs {
 };
 
 constexpr int kMlaThreads = 512;  // 8 wavefronts, 2 per SIMD
+constexpr int kPre = 4;           // sparse: tiles per range at most
 constexpr int kMlaWaves = kMlaThreads / 64;
 constexpr int kLoadsPerWave = (kLoadsPerTile + kMlaWaves - 1) / kMlaWaves;
 
@@ -193,21 +194,46 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
   int tab = 0;
   // Issues the loads of tile t into LDS buffer dst; tokens at or past the
   // context end read as zeros (the descriptor covers only valid rows).
+  // SPARSE: byte offset of the pool row behind position `pos` (sentinel past
+  // the descriptor for no row).
+  auto row_offset = [&](int pos, int slot) -> uint32_t {
+    if (pos < 0) return 0xFFFFFFF0u;
+    if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
+    const long long row = (static_cast<long long>(slot) << a.pt_shift) +
+                          (pos & ((1 << a.pt_shift) - 1));
+    return static_cast<uint32_t>(row * (kLat * 2));
+  };
+  // SPARSE: the range's tiles (at most kPre, the host sizes the ranges so)
+  // have their rows resolved up front into LDS -- all positions, then all
+  // table entries: two round trips for the range instead of two per tile.
+  // Wave 0 resolves, every wave reads.
+  __shared__ uint32_t pre_off[SPARSE ? kPre : 1][kTile];
+  if constexpr (SPARSE) {
+    if (w == 0) {
+      int pos[kPre];
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) {
+        const int tok = (t_lo + k) * kTile + lane;
+        pos[k] = (t_lo + k < t_hi && tok < ctx)
+                     ? a.sel[static_cast<size_t>(b) * a.sel_stride + tok]
+                     : -1;
+      }
+      int slot[kPre];
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) {
+        const int page = pos[k] >> a.pt_shift;
+        slot[k] = (pos[k] >= 0 && page < a.max_pages) ? trow[page] : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) pre_off[k][lane] = row_offset(pos[k], slot[k]);
+    }
+    lds_barrier();
+  }
+
   auto load_tile = [&](int t, uint16_t* dst) {
     if constexpr (SPARSE) {
-      // lane j resolves position sel[b][64t + j] to its row's byte offset
-      const int tok = t * kTile + lane;
-      uint32_t row_off = 0xFFFFFFF0u;
-      if (tok < ctx) {
-        const int pos = a.sel[static_cast<size_t>(b) * a.sel_stride + tok];
-        const int page = pos >> a.pt_shift;
-        int slot = 0;
-        if (pos >= 0 && page < a.max_pages) slot = trow[page];
-        if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
-        const long long row = (static_cast<long long>(slot) << a.pt_shift) +
-                              (pos >= 0 ? (pos & ((1 << a.pt_shift) - 1)) : 0);
-        row_off = static_cast<uint32_t>(row * (kLat * 2));
-      }
+      // row r of tile t: the offset resolved in the prologue (a sparse range
+      // has at most kPre tiles)
       const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<uint16_t*>(a.lat), static_cast<short>(0), static_cast<int>(a.pool_bytes),
           0x00020000);
@@ -217,8 +243,7 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
         const int j = 64 * i + lane;
         const int row = j / kRowChunks;
         const int col = j - row * kRowChunks;
-        // every lane takes part in the cross-lane read
-        const uint32_t base = static_cast<uint32_t>(__shfl(static_cast<int>(row_off), row & 63));
+        const uint32_t base = pre_off[(t - t_lo) & (kPre - 1)][row & 63];
         const uint32_t off =
             (row < kTile && col < kChunksPerRow && base != 0xFFFFFFF0u) ? base + col * 16
                                                                          : 0xFFFFFFF0u;
@@ -544,10 +569,35 @@ int launch_mla(const MlaArgs& a, int hg, bool sparse, long long grid, uint16_t* 
   return VOOM_LAUNCH_CHECK("mla: reduce kernel launch");
 }
 
+// Ranges for a selection of at most sel_stride positions: one per two 64-row
+// tiles (a selection is short, and every range costs a partial row per head
+// that the reduce reads back) unless the dense default is lower, and never so
+// few that a range holds more than kPre tiles.
+int sparse_min_ranges(int sel_stride) {
+  const int tiles = (sel_stride + kTile - 1) / kTile;
+  return (tiles + kPre - 1) / kPre;
+}
+
+int sparse_ranges(int B, int H, int sel_stride) {
+  const int by_tiles = (sel_stride + 2 * kTile - 1) / (2 * kTile);
+  int nr = default_ranges(B, H);
+  nr = nr < by_tiles ? nr : by_tiles;
+  const int lo = sparse_min_ranges(sel_stride);
+  return nr < lo ? lo : (nr < 1 ? 1 : nr);
+}
+
 }  // namespace
 }  // namespace voom
 
 using namespace voom;
+
+extern "C" size_t voom_mla_sparse_workspace_bytes(int batch, int num_heads, int sel_stride,
+                                                  int num_ranges) {
+  if (batch <= 0 || num_heads <= 0 || sel_stride <= 0) return 0;
+  if (num_ranges <= 0) num_ranges = sparse_ranges(batch, num_heads, sel_stride);
+  const size_t n = static_cast<size_t>(batch) * num_ranges * num_heads;
+  return ((n * kC * sizeof(float) + 255) & ~size_t(255)) + n * 2 * sizeof(float);
+}
 
 extern "C" size_t voom_mla_workspace_bytes(int batch, int num_heads, int num_ranges) {
   if (batch <= 0 || num_heads <= 0) return 0;
@@ -633,7 +683,10 @@ extern "C" int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool,
   VOOM_REQUIRE(pool < 0xFFFF0000ull,
                "%s: latent pool of %llu bytes exceeds the 4 GiB a gathered load can address", who,
                pool);
-  if (num_ranges <= 0) num_ranges = default_ranges(batch, num_heads);
+  if (num_ranges <= 0) num_ranges = sparse_ranges(batch, num_heads, sel_stride);
+  VOOM_REQUIRE(num_ranges >= sparse_min_ranges(sel_stride),
+               "%s: %d ranges leave more than %d tiles per range (at least %d needed)", who,
+               num_ranges, kPre, sparse_min_ranges(sel_stride));
   const size_t need = voom_mla_workspace_bytes(batch, num_heads, num_ranges);
   VOOM_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
   VOOM_REQUIRE(reinterpret_cast<uintptr_t>(q_lat) % 16 == 0 &&

@@ -339,7 +339,7 @@ def mla_sparse_decode(q_lat: torch.Tensor, lat_pool: torch.Tensor, block_table: 
     _require(block_table.dim() == 2 and block_table.shape[0] == B and sel.dim() == 2
              and sel.shape[0] == B and tuple(sel_lens.shape) == (B,),
              "block_table [B, max_pages], sel [B, k], sel_lens [B]")
-    need = mla_workspace_bytes(B, H, num_ranges)
+    need = int(_lib.lib().voom_mla_sparse_workspace_bytes(B, H, sel.shape[1], int(num_ranges)))
     if ws is None:
         ws = workspace(dev, need, tag=2)
     _require(ws.numel() * ws.element_size() >= need, "workspace too small")
@@ -392,8 +392,10 @@ def dsa_topk(scores: torch.Tensor, lens: torch.Tensor, k: int, *,
     B, cap = scores.shape
     sel = torch.empty((B, int(k)), dtype=torch.int32, device=dev)
     sel_lens = torch.empty((B,), dtype=torch.int32, device=dev)
-    _lib.call("voom_dsa_topk", _ptr(scores), _ptr(lens), _ptr(sel), _ptr(sel_lens), B, cap,
-              int(k), _stream(stream))
+    need = int(_lib.lib().voom_dsa_topk_workspace_bytes(B, cap))
+    ws = workspace(dev, need, tag=4)
+    _lib.call("voom_dsa_topk", _ptr(scores), _ptr(lens), _ptr(sel), _ptr(sel_lens), _ptr(ws),
+              need, B, cap, int(k), _stream(stream))
     return sel, sel_lens
 
 
