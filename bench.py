@@ -742,26 +742,37 @@ def bench_e2e(cpu_sample: bool) -> dict:
     dec = PagedDecoder(cfg, weights)
     prompt = torch.randint(0, cfg.vocab_size, (1, 512), generator=torch.Generator().manual_seed(1))
     dec.generate(prompt[:, :64], 4, dec.new_cache())  # warm the GEMM heuristics
+    dec.generate_graph(prompt[:, :64], 4, dec.new_cache())
     torch.cuda.synchronize()
+    # eager loop (one host-driven forward per token)
+    kv_e = dec.new_cache(page_positions=64)
+    toks_e, _, times_e = dec.generate(prompt, 128, kv_e)
+    # the same loop with every decode step replayed from one captured HIP graph
     kv = dec.new_cache(page_positions=64)
-    toks, prefill_s, times = dec.generate(prompt, 128, kv)
+    toks, prefill_s, times = dec.generate_graph(prompt, 128, kv)
     decode_s = sum(times)
     tok_s = len(times) / decode_s
     weight_bytes = cfg.param_count * 2
     res = {
         "workload": "config 1: SmolLM2-135M-shaped decoder (30 layers, 9q/3kv, D=64), random "
                     "N(0,0.02) bf16 weights seed 0, 512-token prompt seed 1, greedy 128 tokens, "
-                    "PagedKVCache 64-token pages, no spill",
+                    "PagedKVCache 64-token pages, no spill; decode steps replayed from a "
+                    "captured HIP graph",
         "decode_tokens_per_s": tok_s,
         "ms_per_token": 1e3 * decode_s / len(times),
+        "eager_decode_tokens_per_s": len(times_e) / sum(times_e),
+        "eager_ms_per_token": 1e3 * sum(times_e) / len(times_e),
+        "graph_tokens_equal_eager": toks == toks_e,
         "prefill_ms": prefill_s * 1e3,
         "prefill_tokens_per_s": 512 / prefill_s,
         "weight_gbs_per_token": weight_bytes * tok_s / 1e9,
+        "weight_hbm_frac": weight_bytes * tok_s / 1e9 / HBM_PEAK_GBS,
         "kv_pages": sum(len(p) for p in kv._pages),
         "first_tokens": toks[:8],
     }
-    log(f"config 1: prefill {prefill_s * 1e3:.1f} ms, decode {res['ms_per_token']:.2f} ms/token "
-        f"({tok_s:.1f} tok/s)")
+    log(f"config 1: prefill {prefill_s * 1e3:.1f} ms, decode {res['ms_per_token']:.3f} ms/token "
+        f"({tok_s:.1f} tok/s) with the graph, eager {res['eager_ms_per_token']:.2f} ms/token; "
+        f"tokens equal: {toks == toks_e}")
     if cpu_sample:
         from transformers import LlamaConfig, LlamaForCausalLM
 
@@ -800,7 +811,7 @@ def bench_e2e(cpu_sample: bool) -> dict:
         res["greedy_prefix_agreement_vs_cpu_fp32"] = agree
         log(f"config 1: cpu baseline {n_cpu / dt:.1f} tok/s; greedy tokens agree for the first "
             f"{agree} of {len(ref_toks)}")
-    del dec, weights, kv
+    del dec, weights, kv, kv_e
     torch.cuda.empty_cache()
     return res
 

@@ -200,6 +200,33 @@ int voom_position_free_attention(const void* q, const void* k_pages, const void*
                                  hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Decoder-block ops of the end-to-end decode harness (all bf16, memory-bound).
+ *
+ * voom_add_rms_norm: with delta, x = bf16(x + delta) in place (the residual
+ * add); then out = bf16(weight * bf16(x * rsqrt(mean(x^2) + eps))), fp32
+ * statistics -- mx.fast.rms_norm at runtime/layer_runner.py:263,309, with
+ * Hugging Face Llama's cast order.  x, delta, out [rows, hidden], weight
+ * [hidden]; hidden a multiple of 8 up to 8192; delta may be NULL.
+ *
+ * voom_rope_split: qkv [batch * seq, (nq + 2 nkv) * head_dim] (the fused
+ * projection) -> q [batch, nq, seq, head_dim], k and v [batch, nkv, seq,
+ * head_dim], q and k rotated (rotate-half RoPE, fp32 products, bf16 out) with
+ * the fp32 tables cos/sin [seq, head_dim] -- mx.fast.rope at
+ * runtime/layer_runner.py:99-103 plus the head split and transpose.
+ *
+ * voom_silu_mul: gate_up [rows, 2 * intermediate] (gate first) ->
+ * out [rows, intermediate] = bf16(bf16(silu(gate)) * up) -- _silu_mul,
+ * runtime/layer_runner.py:43-46,188.
+ * ------------------------------------------------------------------------- */
+int voom_add_rms_norm(void* x, const void* delta, const void* weight, void* out, int rows,
+                      int hidden, float eps, hipStream_t stream);
+int voom_rope_split(const void* qkv, const float* cos_table, const float* sin_table, void* q,
+                    void* k, void* v, int batch, int seq, int num_q_heads, int num_kv_heads,
+                    int head_dim, hipStream_t stream);
+int voom_silu_mul(const void* gate_up, void* out, int rows, int intermediate,
+                  hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Page writes and reads.
  *
  * voom_append_kv writes L new tokens per sequence into the pools at logical

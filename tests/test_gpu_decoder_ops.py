@@ -1,0 +1,74 @@
+"""GPU numerics of the decoder-block HIP kernels against plain PyTorch fp32
+references of the same ops (Hugging Face Llama's formulas and cast order):
+RoPE + split bit-exact (each product and sum rounded as torch rounds them);
+RMSNorm and SwiGLU within one bf16 ulp (the fp32 reduction order and exp
+implementation may differ)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from voom_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp_close(a: torch.Tensor, b: torch.Tensor, ulps: int = 1) -> None:
+    ai = a.view(torch.int16).int()
+    bi = b.view(torch.int16).int()
+    # bf16 bit patterns of the same sign differ by the ulp count
+    same_sign = (ai < 0) == (bi < 0)
+    diff = (ai - bi).abs()
+    bad = ~(same_sign & (diff <= ulps)) & (a.float() != b.float())
+    assert not bool(bad.any()), f"{int(bad.sum())} values beyond {ulps} ulp"
+
+
+@pytest.mark.parametrize("rows,H,with_delta", [(1, 576, True), (37, 576, False), (5, 4096, True)])
+def test_add_rms_norm(rows, H, with_delta):
+    print(f"[decoder-ops] rms rows={rows} H={H}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows + H)
+    x = torch.randn((rows, H), generator=g, device="cuda").to(torch.bfloat16)
+    d = torch.randn((rows, H), generator=g, device="cuda").to(torch.bfloat16) if with_delta else None
+    w = (1 + 0.1 * torch.randn((H,), generator=g, device="cuda")).to(torch.bfloat16)
+    x_ref = x + d if with_delta else x.clone()
+    xf = x_ref.float()
+    ref = w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
+    got = ops.add_rms_norm(x, w, 1e-5, delta=d)
+    torch.cuda.synchronize()
+    assert torch.equal(x.view(torch.int16), x_ref.view(torch.int16))   # residual exact
+    ulp_close(got, ref)
+
+
+@pytest.mark.parametrize("B,L,nq,nkv,hd", [(1, 1, 9, 3, 64), (2, 33, 9, 3, 64), (1, 5, 32, 8, 128)])
+def test_rope_split_is_the_torch_rotation(B, L, nq, nkv, hd):
+    print(f"[decoder-ops] rope B={B} L={L}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(B * L + hd)
+    qkv = torch.randn((B, L, (nq + 2 * nkv) * hd), generator=g, device="cuda").to(torch.bfloat16)
+    pos = torch.arange(100, 100 + L, device="cuda")
+    inv = 1.0 / (10000.0 ** (torch.arange(hd // 2, device="cuda", dtype=torch.float32) / (hd // 2)))
+    ang = pos.float()[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).contiguous()
+    sin = torch.cat([ang.sin(), ang.sin()], -1).contiguous()
+    q, k, v = ops.rope_split(qkv, cos, sin, nq, nkv, hd)
+    torch.cuda.synchronize()
+
+    def rope(x):  # x [B, H, L, hd]
+        xf = x.float()
+        rot = torch.cat([-xf[..., hd // 2:], xf[..., :hd // 2]], -1)
+        return (xf * cos + rot * sin).to(x.dtype)
+
+    qr, kr, vr = qkv.split([nq * hd, nkv * hd, nkv * hd], -1)
+    assert torch.equal(q, rope(qr.reshape(B, L, nq, hd).transpose(1, 2)))
+    assert torch.equal(k, rope(kr.reshape(B, L, nkv, hd).transpose(1, 2)))
+    assert torch.equal(v, vr.reshape(B, L, nkv, hd).transpose(1, 2))
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 1536), (40, 1536), (3, 14336)])
+def test_silu_mul(rows, inter):
+    print(f"[decoder-ops] silu rows={rows}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows + inter)
+    gu = (torch.randn((rows, 2 * inter), generator=g, device="cuda") * 3).to(torch.bfloat16)
+    gate, up = gu.chunk(2, dim=-1)
+    ref = F.silu(gate) * up
+    got = ops.silu_mul(gu)
+    torch.cuda.synchronize()
+    ulp_close(got, ref)

@@ -1,0 +1,216 @@
+// Fused per-token ops of the config-1 decoder harness (a Llama-style block
+// around the paged attention), so that one decode step is a short chain of
+// launches: the residual add + RMSNorm, RoPE of q and k together with the
+// split of the fused qkv projection into the attention layouts, and SwiGLU.
+// They restate the block math of runtime/layer_runner.py (rms_norm :263,309,
+// rope :99-103, _silu_mul :43-46 and :188) with Hugging Face LlamaForCausalLM's
+// cast order -- the reference its parity tests use:
+//   rms_norm:  y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))   stats in fp32
+//   rope:      rotate-half, fp32 products from fp32 cos/sin tables, bf16 out
+//   swiglu:    bf16(bf16(g / (1 + exp(-g))) * u)
+// All memory-bound; each kernel reads and writes its rows once.
+#include "common.h"
+
+namespace voom {
+namespace {
+
+constexpr int kRowThreads = 256;
+
+// One workgroup per row of `hidden` bf16 values (hidden % 8 == 0, <= 8192).
+// With delta, the row first becomes bf16(x + delta) and is written back.
+__global__ __launch_bounds__(kRowThreads) void add_rms_norm_kernel(
+    uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
+    const uint16_t* __restrict__ weight, uint16_t* __restrict__ out, int hidden, float eps) {
+  __shared__ float partial[kRowThreads / kWave];
+  const size_t row = blockIdx.x;
+  uint16_t* xr = x + row * hidden;
+  const uint16_t* dr = delta ? delta + row * hidden : nullptr;
+  uint16_t* orow = out + row * hidden;
+  constexpr int kMaxPer = 8192 / (kRowThreads * 8);  // 16-byte chunks per thread
+  float v[kMaxPer][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMaxPer; ++c) {
+    const int col = (c * kRowThreads + threadIdx.x) * 8;
+    if (col < hidden) {
+      u32x4 a = *reinterpret_cast<const u32x4*>(xr + col);
+      if (dr) {
+        const u32x4 d = *reinterpret_cast<const u32x4*>(dr + col);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float lo = bf2f(static_cast<uint16_t>(a[w] & 0xffffu)) +
+                           bf2f(static_cast<uint16_t>(d[w] & 0xffffu));
+          const float hi = bf2f(static_cast<uint16_t>(a[w] >> 16)) +
+                           bf2f(static_cast<uint16_t>(d[w] >> 16));
+          a[w] = pack_bf16x2(lo, hi);
+        }
+        *reinterpret_cast<u32x4*>(xr + col) = a;
+      }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        v[c][2 * w] = bf2f(static_cast<uint16_t>(a[w] & 0xffffu));
+        v[c][2 * w + 1] = bf2f(static_cast<uint16_t>(a[w] >> 16));
+        ss += v[c][2 * w] * v[c][2 * w] + v[c][2 * w + 1] * v[c][2 * w + 1];
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < kRowThreads / kWave; ++k) tot += partial[k];
+  const float inv = 1.f / sqrtf(tot / static_cast<float>(hidden) + eps);
+#pragma unroll
+  for (int c = 0; c < kMaxPer; ++c) {
+    const int col = (c * kRowThreads + threadIdx.x) * 8;
+    if (col < hidden) {
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(weight + col);
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float n0 = bf2f(f2bf(v[c][2 * w] * inv));
+        const float n1 = bf2f(f2bf(v[c][2 * w + 1] * inv));
+        o[w] = pack_bf16x2(bf2f(static_cast<uint16_t>(wv[w] & 0xffffu)) * n0,
+                           bf2f(static_cast<uint16_t>(wv[w] >> 16)) * n1);
+      }
+      *reinterpret_cast<u32x4*>(orow + col) = o;
+    }
+  }
+}
+
+// qkv [B * L, (nq + 2 nkv) * hd] -> q [B, nq, L, hd], k and v [B, nkv, L, hd];
+// q and k rotated (rotate-half) with the fp32 tables cos/sin [L, hd]
+// (cos[i] = cos[i + hd/2]).  One thread per (row, head, dim pair).
+__global__ __launch_bounds__(kRowThreads) void rope_split_kernel(
+    const uint16_t* __restrict__ qkv, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+    uint16_t* __restrict__ v, int B, int L, int nq, int nkv, int hd) {
+  const int half = hd / 2;
+  const int heads = nq + 2 * nkv;
+  const long long idx = static_cast<long long>(blockIdx.x) * kRowThreads + threadIdx.x;
+  const long long total = static_cast<long long>(B) * L * heads * half;
+  if (idx >= total) return;
+  const int i = static_cast<int>(idx % half);
+  const long long rh = idx / half;
+  const int h = static_cast<int>(rh % heads);
+  const int row = static_cast<int>(rh / heads);
+  const int b = row / L;
+  const int l = row - b * L;
+  const uint16_t* src = qkv + (static_cast<size_t>(row) * heads + h) * hd;
+  const float x1 = bf2f(src[i]);
+  const float x2 = bf2f(src[i + half]);
+  uint16_t* dst;
+  if (h < nq) {
+    dst = q + ((static_cast<size_t>(b) * nq + h) * L + l) * hd;
+  } else if (h < nq + nkv) {
+    dst = k + ((static_cast<size_t>(b) * nkv + (h - nq)) * L + l) * hd;
+  } else {
+    dst = v + ((static_cast<size_t>(b) * nkv + (h - nq - nkv)) * L + l) * hd;
+    dst[i] = src[i];
+    dst[i + half] = src[i + half];
+    return;
+  }
+  {
+    // x * cos + rotate_half(x) * sin with each product and the sum rounded as
+    // separate fp32 ops (no fused multiply-add), as torch evaluates it
+#pragma clang fp contract(off)
+    const float c0 = cos_t[static_cast<size_t>(l) * hd + i];
+    const float s0 = sin_t[static_cast<size_t>(l) * hd + i];
+    const float c1 = cos_t[static_cast<size_t>(l) * hd + i + half];
+    const float s1 = sin_t[static_cast<size_t>(l) * hd + i + half];
+    const float a0 = x1 * c0;
+    const float b0 = -x2 * s0;
+    const float a1 = x2 * c1;
+    const float b1 = x1 * s1;
+    dst[i] = f2bf(a0 + b0);
+    dst[i + half] = f2bf(a1 + b1);
+  }
+}
+
+// gate_up [rows, 2 I] (gate first) -> out [rows, I]; 8 values per thread.
+__global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(
+    const uint16_t* __restrict__ gate_up, uint16_t* __restrict__ out, int rows, int inter) {
+  const long long idx = static_cast<long long>(blockIdx.x) * kRowThreads + threadIdx.x;
+  const int per_row = inter / 8;
+  if (idx >= static_cast<long long>(rows) * per_row) return;
+  const int row = static_cast<int>(idx / per_row);
+  const int c = static_cast<int>(idx - static_cast<long long>(row) * per_row) * 8;
+  const uint16_t* gr = gate_up + static_cast<size_t>(row) * 2 * inter;
+  const u32x4 g = *reinterpret_cast<const u32x4*>(gr + c);
+  const u32x4 u = *reinterpret_cast<const u32x4*>(gr + inter + c);
+  u32x4 o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float r[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float gv = bf2f(static_cast<uint16_t>(e ? g[w] >> 16 : g[w] & 0xffffu));
+      const float uv = bf2f(static_cast<uint16_t>(e ? u[w] >> 16 : u[w] & 0xffffu));
+      const float s = bf2f(f2bf(gv / (1.f + expf(-gv))));
+      r[e] = s * uv;
+    }
+    o[w] = pack_bf16x2(r[0], r[1]);
+  }
+  *reinterpret_cast<u32x4*>(out + static_cast<size_t>(row) * inter + c) = o;
+}
+
+}  // namespace
+}  // namespace voom
+
+using namespace voom;
+
+extern "C" int voom_add_rms_norm(void* x, const void* delta, const void* weight, void* out,
+                                 int rows, int hidden, float eps, hipStream_t stream) {
+  const char* who = "add_rms_norm";
+  VOOM_REQUIRE(x && weight && out, "%s: null pointer argument", who);
+  VOOM_REQUIRE(rows > 0 && hidden > 0 && hidden % 8 == 0 && hidden <= 8192,
+               "%s: hidden %d must be a multiple of 8 up to 8192", who, hidden);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(delta) % 16 == 0,
+               "%s: tensors must be 16-byte aligned", who);
+  hipLaunchKernelGGL(add_rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowThreads),
+                     0, stream, static_cast<uint16_t*>(x), static_cast<const uint16_t*>(delta),
+                     static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out), hidden,
+                     eps);
+  return VOOM_LAUNCH_CHECK("add_rms_norm: kernel launch");
+}
+
+extern "C" int voom_rope_split(const void* qkv, const float* cos_table, const float* sin_table,
+                               void* q, void* k, void* v, int batch, int seq, int num_q_heads,
+                               int num_kv_heads, int head_dim, hipStream_t stream) {
+  const char* who = "rope_split";
+  VOOM_REQUIRE(qkv && cos_table && sin_table && q && k && v, "%s: null pointer argument", who);
+  VOOM_REQUIRE(batch > 0 && seq > 0 && num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
+                   head_dim % 2 == 0,
+               "%s: bad geometry", who);
+  const long long total =
+      static_cast<long long>(batch) * seq * (num_q_heads + 2 * num_kv_heads) * (head_dim / 2);
+  VOOM_REQUIRE(total < (1LL << 40), "%s: too large", who);
+  hipLaunchKernelGGL(rope_split_kernel,
+                     dim3(static_cast<unsigned>((total + kRowThreads - 1) / kRowThreads)),
+                     dim3(kRowThreads), 0, stream, static_cast<const uint16_t*>(qkv), cos_table,
+                     sin_table, static_cast<uint16_t*>(q), static_cast<uint16_t*>(k),
+                     static_cast<uint16_t*>(v), batch, seq, num_q_heads, num_kv_heads, head_dim);
+  return VOOM_LAUNCH_CHECK("rope_split: kernel launch");
+}
+
+extern "C" int voom_silu_mul(const void* gate_up, void* out, int rows, int intermediate,
+                             hipStream_t stream) {
+  const char* who = "silu_mul";
+  VOOM_REQUIRE(gate_up && out, "%s: null pointer argument", who);
+  VOOM_REQUIRE(rows > 0 && intermediate > 0 && intermediate % 8 == 0,
+               "%s: intermediate %d must be a positive multiple of 8", who, intermediate);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(gate_up) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0,
+               "%s: tensors must be 16-byte aligned", who);
+  const long long total = static_cast<long long>(rows) * (intermediate / 8);
+  hipLaunchKernelGGL(silu_mul_kernel,
+                     dim3(static_cast<unsigned>((total + kRowThreads - 1) / kRowThreads)),
+                     dim3(kRowThreads), 0, stream, static_cast<const uint16_t*>(gate_up),
+                     static_cast<uint16_t*>(out), rows, intermediate);
+  return VOOM_LAUNCH_CHECK("silu_mul: kernel launch");
+}

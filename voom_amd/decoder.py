@@ -3,19 +3,23 @@ shape by default) whose attention runs entirely through PagedKVCache.
 
 It restates, for one dense architecture, the three reference pieces that
 drive the cache:
-  * ``_attention``  (runtime/layer_runner.py:48-182): q/k/v projections,
-    NeoX RoPE at the cache offset, ``kv.append`` and then attention over the
-    cache -- ``kv.attend`` for one query token, causal ``kv.attend_prefill``
-    for a prompt (the reference's explicit causal mask at :166-177);
-  * ``run_block``  (runtime/layer_runner.py:320-344): RMSNorm, attention,
-    residual, RMSNorm, SwiGLU, residual;
+  * ``_block``, the attention part (runtime/layer_runner.py:48-182): q/k/v
+    projections, NeoX RoPE at the cache offset, ``kv.append`` and then
+    attention over the cache -- ``kv.attend`` for one query token, causal
+    ``kv.attend_prefill`` for a prompt (the reference's explicit causal mask
+    at :166-177);
+  * ``_block``, the rest of the layer (runtime/layer_runner.py:320-344):
+    RMSNorm, attention, residual, RMSNorm, SwiGLU, residual;
   * the greedy decode loop of StreamingEngine.generate
     (runtime/engine.py:8459-8503): embed the pending token, sweep the
     layers at ``kv.offset``, final norm + tied lm_head, argmax.
 
-GEMMs, norms and RoPE are plain PyTorch-ROCm ops (hipBLASLt GEMMs); every
-attention call is the paged HIP kernel.  Weights use the Hugging Face Llama
-parameter names so that an in-code ``LlamaForCausalLM`` can load them.
+GEMMs are PyTorch-ROCm (hipBLASLt); the residual add + RMSNorm, RoPE with
+the q/k/v split, and SwiGLU are fused HIP kernels (voom_add_rms_norm,
+voom_rope_split, voom_silu_mul), and every attention call is the paged HIP
+kernel.  ``generate_graph`` replays each decode step from one captured HIP
+graph.  Weights use the Hugging Face Llama parameter names so that an
+in-code ``LlamaForCausalLM`` can load them.
 """
 
 from __future__ import annotations
@@ -26,6 +30,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import ops
 from .kv_paged import PagedKVCache
 
 
@@ -112,54 +117,45 @@ class PagedDecoder:
 
     # ---- pieces -------------------------------------------------------------
 
-    def _rms_norm(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        """fp32 statistics, result cast back before the weight (HF LlamaRMSNorm)."""
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg.rms_norm_eps)
-        return weight * xf.to(x.dtype)
+    def _norm(self, x: torch.Tensor, weight: torch.Tensor,
+              delta: torch.Tensor | None = None) -> torch.Tensor:
+        """x += delta (in place, when given), then RMSNorm: fp32 statistics,
+        result cast to bf16 before the weight (HF LlamaRMSNorm)."""
+        return ops.add_rms_norm(x, weight, self.cfg.rms_norm_eps, delta=delta)
 
     @staticmethod
     def _linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
         shape = x.shape
         return F.linear(x.reshape(-1, shape[-1]), weight).reshape(*shape[:-1], weight.shape[0])
 
-    def _rope(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        """NeoX (rotate-half) RoPE on x [B, H, L, D] at integer positions [L]."""
+    def _rope_tables(self, positions: torch.Tensor):
+        """fp32 cos/sin [L, head_dim] at integer positions [L] (NeoX layout)."""
         ang = positions.to(torch.float32)[:, None] * self.inv_freq[None, :]
-        cos = torch.cat([ang.cos(), ang.cos()], -1)
-        sin = torch.cat([ang.sin(), ang.sin()], -1)
-        xf = x.float()
-        half = x.shape[-1] // 2
-        rot = torch.cat([-xf[..., half:], xf[..., :half]], -1)
-        return (xf * cos + rot * sin).to(x.dtype)
+        return (torch.cat([ang.cos(), ang.cos()], -1).contiguous(),
+                torch.cat([ang.sin(), ang.sin()], -1).contiguous())
 
-    def _attention(self, h: torch.Tensor, layer: int, kv: PagedKVCache,
-                   offset: int) -> torch.Tensor:
+    def _block(self, x: torch.Tensor, delta: torch.Tensor | None, layer: int,
+               kv: PagedKVCache, cos: torch.Tensor, sin: torch.Tensor,
+               graph: bool = False) -> torch.Tensor:
+        """One layer on the residual stream x [B, L, H] (updated in place with
+        the previous layer's MLP output ``delta``); returns this layer's MLP
+        output, the next layer's delta."""
         cfg = self.cfg
-        B, L, _ = h.shape
-        nq, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-        qkv = self._linear(h, self.layers[layer]["qkv"])
-        q, k, v = qkv.split([nq * hd, nkv * hd, nkv * hd], dim=-1)
-        q = q.reshape(B, L, nq, hd).transpose(1, 2)
-        k = k.reshape(B, L, nkv, hd).transpose(1, 2)
-        v = v.reshape(B, L, nkv, hd).transpose(1, 2).contiguous()
-        pos = torch.arange(offset, offset + L, device=h.device)
-        q = self._rope(q, pos).contiguous()
-        k = self._rope(k, pos).contiguous()
-        kv.append(layer, k, v)
-        if L == 1:
-            attn = kv.attend(layer, q, scale=hd ** -0.5)
-        else:
-            attn = kv.attend_prefill(layer, q, scale=hd ** -0.5)
-        attn = attn.transpose(1, 2).reshape(B, L, nq * hd)
-        return self._linear(attn, self.layers[layer]["o"])
-
-    def run_block(self, x: torch.Tensor, layer: int, kv: PagedKVCache, offset: int):
         lw = self.layers[layer]
-        x = x + self._attention(self._rms_norm(x, lw["ln1"]), layer, kv, offset)
-        h = self._rms_norm(x, lw["ln2"])
-        gate, up = self._linear(h, lw["gate_up"]).chunk(2, dim=-1)
-        return x + self._linear(F.silu(gate) * up, lw["down"])
+        B, L, _ = x.shape
+        nq, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        h = self._norm(x, lw["ln1"], delta)
+        q, k, v = ops.rope_split(self._linear(h, lw["qkv"]), cos, sin, nq, nkv, hd)
+        if graph:
+            kv.append_at(layer, k, v)
+            attn = kv.attend_at(layer, q, hd ** -0.5)
+        else:
+            kv.append(layer, k, v)
+            attn = (kv.attend(layer, q, scale=hd ** -0.5) if L == 1
+                    else kv.attend_prefill(layer, q, scale=hd ** -0.5))
+        o = self._linear(attn.transpose(1, 2).reshape(B, L, nq * hd), lw["o"])
+        h = self._norm(x, lw["ln2"], o)
+        return self._linear(ops.silu_mul(self._linear(h, lw["gate_up"])), lw["down"])
 
     # ---- model --------------------------------------------------------------
 
@@ -173,13 +169,84 @@ class PagedDecoder:
                 last_only: bool = False) -> torch.Tensor:
         """Logits [B, L, vocab] (fp32) for tokens [B, L] appended at kv.offset."""
         offset = kv.offset
+        L = tokens.shape[1]
+        cos, sin = self._rope_tables(torch.arange(offset, offset + L, device=self.device))
         x = self.embed[tokens]
+        delta = None
         for layer in range(self.cfg.num_hidden_layers):
-            x = self.run_block(x, layer, kv, offset)
+            delta = self._block(x, delta, layer, kv, cos, sin)
+        x = self._norm(x, self.final_norm, delta)
         if last_only:
             x = x[:, -1:]
-        x = self._rms_norm(x, self.final_norm)
         return self._linear(x, self.embed).float()
+
+    # ---- one decode step in a HIP graph ------------------------------------------
+
+    def _graph_step(self, tok: torch.Tensor, nxt: torch.Tensor, kv: PagedKVCache) -> None:
+        """One token per sequence from device state only: tok [B, 1] in, the
+        greedy next token written to nxt [B] and back into tok, K/V written at
+        the cache's device position counter, counters advanced.  Every op is a
+        device op with fixed shapes and addresses, so the step can be captured
+        and replayed; it computes what ``forward`` computes for one token."""
+        B = tok.shape[0]
+        cos, sin = self._rope_tables(kv._pos_dev[:1])
+        x = self.embed[tok]
+        delta = None
+        for layer in range(self.cfg.num_hidden_layers):
+            delta = self._block(x, delta, layer, kv, cos, sin, graph=True)
+        x = self._norm(x, self.final_norm, delta)
+        logits = self._linear(x, self.embed).float()
+        nxt.copy_(logits[:, -1].argmax(-1))
+        tok.copy_(nxt.view(B, 1))
+        kv.step_counters()
+
+    @torch.no_grad()
+    def capture_decode(self, kv: PagedKVCache, max_len: int):
+        """Reserve the cache up to ``max_len`` tokens and capture one decode
+        step; returns (graph, tok [B, 1], nxt [B]).  Before each replay put the
+        step's input token in ``tok`` (a replay leaves its output there);
+        after it call ``kv.advance(1)``."""
+        kv.reserve(max_len)
+        B = kv._batch
+        tok = torch.zeros((B, 1), dtype=torch.long, device=self.device)
+        nxt = torch.zeros((B,), dtype=torch.long, device=self.device)
+        # one eager run on a side stream sets up the libraries' handles and the
+        # workspaces; its K/V write lands at the next position and is
+        # overwritten by the first replay, and its counter step is undone
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._graph_step(tok, nxt, kv)
+        torch.cuda.current_stream().wait_stream(side)
+        kv._pos_dev.sub_(1)
+        kv._ctx_dev.sub_(1)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._graph_step(tok, nxt, kv)
+        torch.cuda.synchronize()
+        return graph, tok, nxt
+
+    @torch.no_grad()
+    def generate_graph(self, prompt: torch.Tensor, max_tokens: int, kv: PagedKVCache):
+        """``generate`` with every decode step replayed from one captured HIP
+        graph.  Same returns; each per-token time still ends at the token's
+        argmax on the host."""
+        t0 = time.perf_counter()
+        logits = self.forward(prompt.to(self.device), kv, last_only=True)
+        first = int(logits[0, -1].argmax())
+        prefill_s = time.perf_counter() - t0
+        graph, tok, nxt = self.capture_decode(kv, kv.offset + max_tokens)
+        out = [first]
+        times = []
+        tok.fill_(first)
+        while len(out) < max_tokens:
+            t1 = time.perf_counter()
+            graph.replay()
+            kv.advance(1)
+            out.append(int(nxt[0]))
+            times.append(time.perf_counter() - t1)
+        return out, prefill_s, times
 
     @torch.no_grad()
     def generate(self, prompt: torch.Tensor, max_tokens: int, kv: PagedKVCache):

@@ -460,7 +460,8 @@ class PagedKVCache:
         start = self._len[layer]
         end = start + L
         PT = self.page_positions
-        new_pages = range(-(-start // PT), -(-end // PT))
+        new_pages = [p for p in range(-(-start // PT), -(-end // PT))
+                     if p not in self._open_slots[layer]]  # reserve() may have opened them
         if len(new_pages):
             slots = pool.allocate(B * len(new_pages))
             cols = {}
@@ -480,6 +481,78 @@ class PagedKVCache:
         if layer == self.num_layers - 1:
             self._offset += L
             self._enforce_budget()
+
+    # ---- decode steps that a HIP graph can capture ------------------------------
+
+    def reserve(self, total_len: int) -> None:
+        """Open pool slots and block-table entries now for every page up to
+        ``total_len`` tokens in every layer, and create the device position
+        counters of ``append_at`` / ``attend_at``.
+
+        After it, appends up to ``total_len`` allocate nothing and the pools
+        and tables keep their device addresses -- what a captured decode step
+        needs.  Nothing may spill meanwhile: raises if the reserved pages do
+        not fit ``max_bytes``.
+        """
+        if self._geom is None:
+            raise ValueError("reserve() needs the page geometry: append once first")
+        PT = self.page_positions
+        B = self._batch
+        total_pages = -(-int(total_len) // PT)
+        if total_pages * self.page_nbytes * self.num_layers > self.max_bytes:
+            raise ValueError(f"{total_len} tokens exceed max_bytes={self.max_bytes}; "
+                             "reserve() cannot spill")
+        for layer in range(self.num_layers):
+            first = -(-self._len[layer] // PT)
+            pages = [p for p in range(first, total_pages) if p not in self._open_slots[layer]]
+            if not pages:
+                continue
+            slots = self._pool(layer).allocate(B * len(pages))
+            cols = {}
+            for j, page in enumerate(pages):
+                cols[page] = slots[j * B:(j + 1) * B]
+                self._open_slots[layer][page] = cols[page]
+            self._set_table_cols(layer, cols)
+        self._reserved = int(total_len)
+        self._pos_dev = torch.full((B,), self._offset, dtype=torch.int32, device=self.device)
+        self._ctx_dev = self._pos_dev + 1
+
+    def append_at(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Write one token's k, v [B, NKV, 1, D] at the device position counter
+        (no host bookkeeping; ``advance`` does it after the step)."""
+        pool = self._pool(layer)
+        ops.append_kv(k.contiguous(), v.contiguous(), pool.k, pool.v, self._tables[layer],
+                      self._pos_dev)
+
+    def attend_at(self, layer: int, q: torch.Tensor, scale: float) -> torch.Tensor:
+        """Decode attention of q [B, NQ, 1, D] over the device context counter
+        (all pages resident, as ``reserve`` guarantees)."""
+        pool = self._pool(layer)
+        return ops.paged_gqa_decode(q, pool.k, pool.v, self._tables[layer], self._ctx_dev,
+                                    scale=scale)
+
+    def step_counters(self) -> None:
+        """Advance the device position counters by one token (the end of a
+        captured step)."""
+        self._pos_dev.add_(1)
+        self._ctx_dev.add_(1)
+
+    def advance(self, L: int = 1) -> None:
+        """Host bookkeeping of ``L`` tokens written by ``append_at`` in every
+        layer: lengths, closed pages, the offset."""
+        PT = self.page_positions
+        end = self._offset + L
+        if end > getattr(self, "_reserved", 0):
+            raise ValueError(f"advance past the reserved {getattr(self, '_reserved', 0)} tokens")
+        for layer in range(self.num_layers):
+            self._len[layer] = end
+            pages = self._pages[layer]
+            while (len(pages) + 1) * PT <= end:
+                idx = len(pages)
+                pages.append(_Page(self, layer, idx, self._open_slots[layer].pop(idx),
+                                   self.page_nbytes))
+                self._resident_closed += 1
+        self._offset = end
 
     def update(self, layer: int, k: torch.Tensor, v: torch.Tensor):
         """Append, then return the layer's full K/V [B, NKV, S, D] (kv_paged.py:143-181).

@@ -399,6 +399,51 @@ def dsa_topk(scores: torch.Tensor, lens: torch.Tensor, k: int, *,
     return sel, sel_lens
 
 
+def add_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                 delta: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                 stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Residual add (x += delta, in place, when delta is given) and RMSNorm of
+    x [..., hidden] bf16 with HF Llama's cast order; returns the normed rows."""
+    dev = _require_device(x, weight, delta, out)
+    _require(x.dtype == weight.dtype == torch.bfloat16, "bf16 rows and weight")
+    H = x.shape[-1]
+    _require(tuple(weight.shape) == (H,), "weight [hidden]")
+    _require(delta is None or (delta.shape == x.shape and delta.dtype == x.dtype), "delta like x")
+    if out is None:
+        out = torch.empty_like(x)
+    _lib.call("voom_add_rms_norm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out),
+              x.numel() // H, H, float(eps), _stream(stream))
+    return out
+
+
+def rope_split(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, num_q_heads: int,
+               num_kv_heads: int, head_dim: int, stream: torch.cuda.Stream | None = None):
+    """qkv [B, L, (nq + 2 nkv) * hd] -> (q [B, nq, L, hd], k [B, nkv, L, hd],
+    v [B, nkv, L, hd]), q and k rotated with cos/sin [L, hd] fp32."""
+    dev = _require_device(qkv, cos, sin)
+    B, L, W = qkv.shape
+    _require(W == (num_q_heads + 2 * num_kv_heads) * head_dim, "qkv width")
+    _require(qkv.dtype == torch.bfloat16 and cos.dtype == sin.dtype == torch.float32
+             and tuple(cos.shape) == (L, head_dim) == tuple(sin.shape), "bf16 qkv, fp32 [L, hd] tables")
+    q = torch.empty((B, num_q_heads, L, head_dim), dtype=qkv.dtype, device=dev)
+    k = torch.empty((B, num_kv_heads, L, head_dim), dtype=qkv.dtype, device=dev)
+    v = torch.empty_like(k)
+    _lib.call("voom_rope_split", _ptr(qkv), _ptr(cos), _ptr(sin), _ptr(q), _ptr(k), _ptr(v),
+              B, L, num_q_heads, num_kv_heads, head_dim, _stream(stream))
+    return q, k, v
+
+
+def silu_mul(gate_up: torch.Tensor, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """gate_up [..., 2 I] (gate first) -> bf16(silu(gate)) * up [..., I]."""
+    dev = _require_device(gate_up)
+    _require(gate_up.dtype == torch.bfloat16 and gate_up.shape[-1] % 2 == 0, "bf16 [..., 2I]")
+    inter = gate_up.shape[-1] // 2
+    out = torch.empty((*gate_up.shape[:-1], inter), dtype=gate_up.dtype, device=dev)
+    _lib.call("voom_silu_mul", _ptr(gate_up), _ptr(out), gate_up.numel() // (2 * inter), inter,
+              _stream(stream))
+    return out
+
+
 def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
     """kv_b_proj weight [H*(dn+dv), C] -> (W_UK [H, dn, C], W_UV^T [H, C, dv]), contiguous.
 
