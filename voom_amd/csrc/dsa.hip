@@ -17,16 +17,19 @@
 // (key i16, group g) then holds heads 4g + r of its key, so relu, the head
 // weights and the head sum stay in registers plus two cross-group adds.
 //
-// Top-k: one workgroup of 1024 threads per row.  Scores map to order-
-// preserving 32-bit keys.  A strided sample places a first threshold; one
-// pass counts the keys above it and a second moves them, in index order, into
-// LDS (at most 16,384), so the row is read from memory about twice.  Three
-// radix passes (11, 11 and 10 bits) over the LDS candidates then find the
-// k-th largest key T and how many keys equal to T to keep, and an ordered
-// write -- each wavefront owns a contiguous range, counts its keys above and
-// equal to T, and after an exclusive scan over wavefronts writes its indices
-// -- leaves the output sorted without a sort.  When the sample misjudges the
-// row, the same exact selection runs over the row in memory.
+// Top-k, three launches per call: (1) one workgroup per row places a
+// threshold T0 at a fixed rank of a strided sample of the row; (2) chunk
+// workgroups (4,096 keys each) move the keys >= T0, with their indices and in
+// index order, to per-chunk slots -- the row is read once, by many CUs;
+// (3) one workgroup per row gathers the candidates into LDS (at most 16,384)
+// and runs the exact selection there: radix passes of up to 11 bits below the
+// leading bits every candidate shares find the k-th largest key T and how
+// many keys equal to T to keep, and an ordered write -- each wavefront owns a
+// contiguous range, counts its keys above and equal to T, and after an
+// exclusive scan over wavefronts writes its indices -- leaves the output
+// sorted without a sort.  Scores map to order-preserving 32-bit keys.  When
+// the sample misjudges the row (fewer than k or more than 16,384
+// candidates), the same exact selection runs over the row in memory.
 #include "common.h"
 
 namespace voom {
@@ -125,6 +128,7 @@ __global__ __launch_bounds__(kScoreThreads) void dsa_scores_kernel(DsaScoreArgs 
 // ---------------------------------------------------------------- top-k ----
 
 constexpr int kTopkThreads = 1024;
+constexpr int kBinsPerThread = 2048 / kTopkThreads;
 constexpr int kTopkWaves = kTopkThreads / kWave;
 
 // Order-preserving map of fp32 onto uint32: a > b  <=>  key(a) > key(b), and
@@ -159,6 +163,31 @@ constexpr int kCandCap = 16384;  // candidate keys held in LDS
 constexpr int kSample = 4096;    // keys sampled to place the threshold
 constexpr int kChunkKeys = 4096; // keys per compaction workgroup
 constexpr int kCompactThreads = 256;
+
+// Over the 2048-entry histogram in descending bin order: the bin where the
+// running count from the top reaches `want` (found[0]) and the count of the
+// bins above it (found[1]).  Thread t holds bins 2047 - (E t + e), e < E.
+__device__ __forceinline__ void find_bin(const int* hist, int want, int* scan_tmp, int* found) {
+  const int tid = threadIdx.x;
+  int c[kBinsPerThread];
+  int mine = 0;
+#pragma unroll
+  for (int e = 0; e < kBinsPerThread; ++e) {
+    c[e] = hist[2047 - (kBinsPerThread * tid + e)];
+    mine += c[e];
+  }
+  int total;
+  int run = block_exclusive_scan(mine, scan_tmp, total);
+#pragma unroll
+  for (int e = 0; e < kBinsPerThread; ++e) {
+    if (run < want && run + c[e] >= want) {
+      found[0] = 2047 - (kBinsPerThread * tid + e);
+      found[1] = run;
+    }
+    run += c[e];
+  }
+  __syncthreads();
+}
 
 // Radix select over `count` keys read by key(i): the rank-th largest key T
 // (rank >= 1) and how many keys equal to T belong to the top `rank` (kk).
@@ -231,20 +260,7 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
     }
     if (run_n) atomicAdd(&hist[run_bin], run_n);
     __syncthreads();
-    // bins in descending order, two per thread over the 2048-entry table
-    int c[2];
-    c[0] = hist[2047 - 2 * tid];
-    c[1] = hist[2046 - 2 * tid];
-    int total;
-    int run = block_exclusive_scan(c[0] + c[1], scan_tmp, total);
-    for (int e = 0; e < 2; ++e) {
-      if (run < kk && run + c[e] >= kk) {
-        found[0] = 2047 - (2 * tid + e);  // the digit
-        found[1] = run;                   // keys above it
-      }
-      run += c[e];
-    }
-    __syncthreads();
+    find_bin(hist, kk, scan_tmp, found);
     const int d = found[0];
     kk -= found[1];
     prefix |= static_cast<uint32_t>(d) << shift;
@@ -317,20 +333,18 @@ struct TopkWs {
 __host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys - 1) / kChunkKeys; }
 
 // 1. Threshold: rows of at most kCandCap keys take every key as a candidate
-// (T0 = 0).  Longer rows: one radix-style histogram pass over a strided sample
-// of kSample keys, below the bits the sample's keys all share, places T0 at
-// the lower edge of the bin where the count from the top reaches 1.5 x the
-// sample's share of k, plus 32 -- a few more candidates than k, with margin.
+// (T0 = 0).  Longer rows: T0 is the key of rank 1.5 x (the sample's share of
+// k) + 32 in a strided sample of kSample keys, found exactly by the radix
+// select in LDS -- about 1.5 k candidates, with margin, and no more than the
+// sample's ties at T0 allow.
 __global__ __launch_bounds__(kTopkThreads) void dsa_topk_threshold_kernel(
     const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
     int K) {
+  __shared__ uint32_t sample[kSample];
   __shared__ int hist[2048];
   __shared__ int scan_tmp[kTopkWaves];
   __shared__ int found[2];
-  __shared__ uint32_t mm[2][kTopkWaves];
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wv = tid / kWave;
   const int b = blockIdx.x;
   int n = lens[b];
   n = n < 0 ? 0 : (n > cap ? cap : n);
@@ -340,64 +354,23 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_threshold_kernel(
   }
   const float* sb = scores + static_cast<size_t>(b) * cap;
   constexpr int kPer = kSample / kTopkThreads;
-  uint32_t u[kPer];
+  float v[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int j = tid + k * kTopkThreads;
-    u[k] = order_key(sb[static_cast<int>(static_cast<long long>(j) * n / kSample)]);
-  }
-  uint32_t lo_k = u[0], hi_k = u[0];
-#pragma unroll
-  for (int k = 1; k < kPer; ++k) {
-    lo_k = u[k] < lo_k ? u[k] : lo_k;
-    hi_k = u[k] > hi_k ? u[k] : hi_k;
+    v[k] = sb[static_cast<int>(static_cast<long long>(j) * n / kSample)];
   }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo_k), o));
-    const uint32_t c = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi_k), o));
-    lo_k = a < lo_k ? a : lo_k;
-    hi_k = c > hi_k ? c : hi_k;
-  }
-  if (lane == 0) {
-    mm[0][wv] = lo_k;
-    mm[1][wv] = hi_k;
-  }
-  for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
-  __syncthreads();
-  lo_k = mm[0][0];
-  hi_k = mm[1][0];
-  for (int k = 1; k < kTopkWaves; ++k) {
-    lo_k = mm[0][k] < lo_k ? mm[0][k] : lo_k;
-    hi_k = mm[1][k] > hi_k ? mm[1][k] : hi_k;
-  }
-  const int top = 31 - __clz(static_cast<int>(lo_k ^ hi_k));
-  if (top < 0) {  // the sample is one value: take everything at or above it
-    if (tid == 0) ws.t0[b] = lo_k;
-    return;
-  }
-  const int width = top + 1 < 11 ? top + 1 : 11;
-  const int shift = top + 1 - width;
-  const uint32_t common = top < 31 ? (hi_k & ~((2u << top) - 1u)) : 0u;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    atomicAdd(&hist[(u[k] >> shift) & static_cast<uint32_t>((1 << width) - 1)], 1);
-  }
+  for (int k = 0; k < kPer; ++k) sample[tid + k * kTopkThreads] = order_key(v[k]);
   __syncthreads();
   long long r = (static_cast<long long>(K) * kSample + n - 1) / n;
   r = r + r / 2 + 32;
   const int want = static_cast<int>(r > kSample ? kSample : r);
-  int c[2];
-  c[0] = hist[2047 - 2 * tid];
-  c[1] = hist[2046 - 2 * tid];
-  int total;
-  int run = block_exclusive_scan(c[0] + c[1], scan_tmp, total);
-  for (int e = 0; e < 2; ++e) {
-    if (run < want && run + c[e] >= want) found[0] = 2047 - (2 * tid + e);
-    run += c[e];
-  }
-  __syncthreads();
-  if (tid == 0) ws.t0[b] = common | (static_cast<uint32_t>(found[0]) << shift);
+  uint32_t T0;
+  int unused;
+  radix_select([&](int i) { return sample[i]; }, kSample, want, hist, scan_tmp, found, T0,
+               unused);
+  if (tid == 0) ws.t0[b] = T0;
 }
 
 // 2. Compaction: one workgroup per chunk of kChunkKeys keys of a row; every
@@ -512,13 +485,22 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
   int C = 0;
   bool fits = nch <= 2048;
   if (fits) {
-    int c2[2];
-    c2[0] = 2 * tid < nch ? cnt[2 * tid] : 0;
-    c2[1] = 2 * tid + 1 < nch ? cnt[2 * tid + 1] : 0;
+    int c2[kBinsPerThread];
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < kBinsPerThread; ++e) {
+      const int ch = kBinsPerThread * tid + e;
+      c2[e] = ch < nch ? cnt[ch] : 0;
+      mine += c2[e];
+    }
     int total;
-    const int run = block_exclusive_scan(c2[0] + c2[1], scan_tmp, total);
-    if (2 * tid < nch) chunk_off[2 * tid] = run;
-    if (2 * tid + 1 < nch) chunk_off[2 * tid + 1] = run + c2[0];
+    int run = block_exclusive_scan(mine, scan_tmp, total);
+#pragma unroll
+    for (int e = 0; e < kBinsPerThread; ++e) {
+      const int ch = kBinsPerThread * tid + e;
+      if (ch < nch) chunk_off[ch] = run;
+      run += c2[e];
+    }
     if (tid == 0) chunk_off[nch] = total;
     C = total;
     fits = C >= K && C <= kCandCap;
