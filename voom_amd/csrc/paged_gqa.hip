@@ -45,6 +45,9 @@ constexpr int kBlockTokens = 32;
 #ifndef VOOM_GQA_WAVES_PER_EU_128
 #define VOOM_GQA_WAVES_PER_EU_128 1
 #endif
+#ifndef VOOM_GQA_K_CACHE_POLICY
+#define VOOM_GQA_K_CACHE_POLICY 0
+#endif
 #ifndef VOOM_GQA_CACHE_POLICY
 #define VOOM_GQA_CACHE_POLICY 0
 #endif
@@ -149,7 +152,7 @@ __device__ __forceinline__ void load_block(BlockRegs<D>& r, const SegmentArgs& a
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) {
       r.k[t][s] = __builtin_amdgcn_raw_buffer_load_b128(kr, lo.k + (4 * t * D + 32 * s) * 2,
-                                                        k_sub, VOOM_GQA_CACHE_POLICY);
+                                                        k_sub, VOOM_GQA_K_CACHE_POLICY);
     }
   }
   const int v_sub = sub * kBlockTokens * 2;
