@@ -15,11 +15,13 @@
  *
  * Device page layouts (one tensor per layer)
  *   K pool  [num_slots, num_kv_heads, page_tokens, head_dim]   token-major
- *   V pool  [num_slots, num_kv_heads, head_dim, page_tokens]   dim-major (V^T)
+ *   V pool  [num_slots, num_kv_heads, page_tokens/VB, head_dim, VB]
+ *           V^T in blocks of VB = min(page_tokens, 32) tokens
  *   latent  [num_slots, page_tokens, latent_dim]               token-major
  *   block_table [batch, max_pages] int32 slot ids, ctx_lens [batch] int32.
- *   V is stored transposed inside each page so that the P.V contraction reads
- *   16 contiguous bytes per lane straight into the MFMA operand.
+ *   V is stored as transposed 32-token blocks so that the P.V contraction
+ *   reads 16 contiguous bytes per lane straight into the MFMA operand and each
+ *   block of K and of V is one contiguous run (64 * head_dim bytes).
  */
 #ifndef VOOM_HIP_H
 #define VOOM_HIP_H

@@ -5,6 +5,7 @@ import torch
 
 from oracle import byteplane as ob
 from voom_amd import ops
+from voom_amd.page_pool import v_pages_to_tokens, v_slot_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -70,7 +71,7 @@ def test_append_then_gather_round_trips():
     perm = np.random.default_rng(3).permutation(slots)[: B * pages].reshape(B, pages)
     table = torch.from_numpy(perm.astype(np.int32)).cuda()
     kp = torch.zeros((slots, NKV, PT, D), dtype=torch.bfloat16, device="cuda")
-    vp = torch.zeros((slots, NKV, D, PT), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros((slots,) + v_slot_shape(NKV, D, PT), dtype=torch.bfloat16, device="cuda")
     k = torch.randn((B, NKV, S, D), device="cuda").to(torch.bfloat16)
     v = torch.randn((B, NKV, S, D), device="cuda").to(torch.bfloat16)
     # append in three uneven steps, as prefill chunk + decode tokens would
@@ -81,5 +82,7 @@ def test_append_then_gather_round_trips():
     kg, vg = ops.gather_kv(kp, vp, table, S)
     torch.cuda.synchronize()
     assert torch.equal(kg, k) and torch.equal(vg, v)
-    # V really is stored transposed inside the page
-    assert torch.equal(vp[int(perm[1, 0]), 1, :, 5], v[1, 1, 5])
+    # V really is stored as V^T blocks of 32 tokens: token 37 of page 0 is
+    # column 5 of block 1
+    assert torch.equal(vp[int(perm[1, 0]), 1, 1, :, 5], v[1, 1, 37])
+    assert torch.equal(v_pages_to_tokens(vp[int(perm[1, 0])].unsqueeze(0)), v[1:2, :, :PT])

@@ -10,6 +10,7 @@ import torch
 
 from oracle import paged_attention as opa
 from voom_amd import ops, synthetic
+from voom_amd.page_pool import v_pages_to_tokens, v_tokens_to_pages
 
 pytestmark = pytest.mark.gpu
 
@@ -94,7 +95,7 @@ def test_single_token_context_returns_value_row_exactly():
     for b in range(2):
         slot = int(inp.table_host[b, 0])
         for h in range(8):
-            assert torch.equal(out[b, h], inp.v_pool[slot, h // 4, :, 0])
+            assert torch.equal(out[b, h], v_pages_to_tokens(inp.v_pool[slot:slot + 1])[0, h // 4, 0])
 
 
 def test_nan_garbage_past_context_is_ignored():
@@ -106,7 +107,9 @@ def test_nan_garbage_past_context_is_ignored():
         last = int(inp.table_host[b, (ctx - 1) // 64])
         off = int(ctx % 64)
         inp.k_pool[last, :, off:, :] = float("nan")
-        inp.v_pool[last, :, :, off:] = float("nan")
+        vt = v_pages_to_tokens(inp.v_pool[last:last + 1]).clone()
+        vt[:, :, off:] = float("nan")
+        inp.v_pool[last:last + 1] = v_tokens_to_pages(vt)
     out = ops.paged_gqa_decode(inp.q, inp.k_pool, inp.v_pool, inp.block_table, inp.ctx_lens)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
@@ -191,7 +194,7 @@ def test_config2_full_size_matches_oracle_on_four_sequences():
         slots = inp.table_host[b, : -(-int(inp.ctx_host[b]) // 64)]
         idx = torch.from_numpy(slots.astype(np.int64)).cuda()
         k = inp.k_pool[idx].float().cpu().numpy()
-        v = inp.v_pool[idx].transpose(2, 3).float().cpu().numpy()
+        v = v_pages_to_tokens(inp.v_pool[idx]).float().cpu().numpy()
         table = np.arange(len(slots))[None]
         q = inp.q[b:b + 1].float().cpu().numpy()
         ref = opa.paged_decode(q, k, v, table, inp.ctx_host[b:b + 1], inp.scale)

@@ -27,7 +27,7 @@ def test_round_trip_and_header(tmp_path, compressed):
     (klo, khi), (vlo, vhi) = planes(k), planes(v)
     his = [vz.compress(khi, 1), vz.compress(vhi, 1)] if compressed else [khi, vhi]
     meta = [{"name": "k", "dtype": "BF16", "shape": [1, 2, 4, 8]},
-            {"name": "v_t", "dtype": "BF16", "shape": [1, 2, 8, 4]}]
+            {"name": "v", "dtype": "BF16", "shape": [1, 2, 1, 8, 4]}]
     path = page_file.page_path(tmp_path, 3, 7)
     assert path.name == "kv_l3_p7.vt"
     n = page_file.write(path, 3, 7, meta, [klo, vlo], his, [compressed] * 2)
@@ -36,7 +36,8 @@ def test_round_trip_and_header(tmp_path, compressed):
     (hlen,) = struct.unpack("<Q", raw[:8])
     head = json.loads(raw[8:8 + hlen])
     assert head["format"] == "voom-kv-page" and head["layer"] == 3 and head["page"] == 7
-    assert [t["shape"] for t in head["tensors"]] == [[1, 2, 4, 8], [1, 2, 8, 4]]
+    assert head["version"] == page_file.VERSION
+    assert [t["shape"] for t in head["tensors"]] == [[1, 2, 4, 8], [1, 2, 1, 8, 4]]
     assert (head["tensors"][0]["hi_z"] is not None) == compressed
     # payload order per tensor: high plane, then low plane
     body = raw[8 + hlen:]

@@ -6,7 +6,9 @@
 // step, which concatenates every page of the layer (runtime/kv_paged.py:164-181)
 // and then calls MLX SDPA with the GQA broadcast (runtime/layer_runner.py:
 // 179-180); the page indexing follows the reference's Metal paged kernel
-// (runtime/pic_attention.py:60-65) with V stored transposed inside a page.
+// (runtime/pic_attention.py:60-65) with V stored as transposed 32-token blocks
+// inside a page: V pool [slots, NKV, PT/32, D, 32], so a wavefront's K block
+// (32 x D) and V^T block (D x 32) are each one contiguous 64*D-byte run.
 //
 // Work decomposition (balanced split-K over 32-token blocks):
 //   A "unit" is one 32-token block of one (sequence, kv-head) segment.  The
@@ -45,11 +47,15 @@ constexpr int kBlockTokens = 32;
 #ifndef VOOM_GQA_WAVES_PER_EU_128
 #define VOOM_GQA_WAVES_PER_EU_128 1
 #endif
+// Cache policy (buffer-load aux bits) of the K and V streams.  Every byte of
+// a block is read exactly once and the blocks are contiguous, so both streams
+// load non-temporal (aux bit 1): measured 6.37 TB/s for the partials kernel
+// against 5.6 TB/s with ordinary loads at the Llama-3-8B 32k shape.
 #ifndef VOOM_GQA_K_CACHE_POLICY
-#define VOOM_GQA_K_CACHE_POLICY 0
+#define VOOM_GQA_K_CACHE_POLICY 2
 #endif
 #ifndef VOOM_GQA_CACHE_POLICY
-#define VOOM_GQA_CACHE_POLICY 0
+#define VOOM_GQA_CACHE_POLICY 2
 #endif
 #ifndef VOOM_GQA_SPLITS_PER_CU
 #define VOOM_GQA_SPLITS_PER_CU 4
@@ -155,8 +161,8 @@ __device__ __forceinline__ void load_block(BlockRegs<D>& r, const SegmentArgs& a
                                                         k_sub, VOOM_GQA_K_CACHE_POLICY);
     }
   }
-  const int v_sub = sub * kBlockTokens * 2;
-  const int v_tile = (16 << a.pt_shift) * 2;
+  const int v_sub = k_sub;  // V^T blocks are [D, 32]: same bytes per block as K
+  const int v_tile = 16 * kBlockTokens * 2;
 #pragma unroll
   for (int n = 0; n < D / 16; ++n) {
     r.v[n] = __builtin_amdgcn_raw_buffer_load_b128(vr, lo.v, v_sub + n * v_tile,
@@ -288,7 +294,7 @@ __global__ __launch_bounds__(kThreads, WAVES_PER_EU) void gqa_decode_kernel(
   const bool head_ok = i16 < G;
   LaneOffsets lofs;
   lofs.k = ((8 * (i16 >> 2) + (i16 & 3)) * D + 8 * g) * 2;
-  lofs.v = ((i16 << pt_shift) + 8 * g) * 2;
+  lofs.v = ((i16 * kBlockTokens) + 8 * g) * 2;
 
   while (true) {
     const long long send = S + nb;

@@ -1,15 +1,25 @@
 // Page writes (append) and logical gathers for the device page pools.
 //
-// K pool [slots, NKV, PT, D] is token-major; V pool [slots, NKV, D, PT] keeps
-// each page transposed so decode attention can feed V^T straight into MFMA
-// operands.  Appending is therefore a 16-byte row store for K and a strided
-// column store for V; both are tiny next to attention (one token per step).
+// K pool [slots, NKV, PT, D] is token-major; V pool [slots, NKV, PT/VB, D, VB]
+// with VB = min(PT, 32) keeps each 32-token block of a page transposed (V^T,
+// one 64-byte row of 32 tokens per dim) so decode attention reads every block
+// of K and V as one contiguous run and feeds V^T straight into MFMA operands.  Appending is a
+// 16-byte row store for K and a 32-element-strided column store for V; both
+// are tiny next to attention (one token per step).
 #include "common.h"
 
 namespace voom {
 namespace {
 
 constexpr int kThreads = 256;
+
+// Element offset of V(token off, dim d) inside the V^T blocks of one head
+// page: block off / VB of [D, VB], VB = 1 << vb_shift = min(PT, 32).
+__device__ __forceinline__ size_t v_offset(size_t head_page, int pt_shift, int vb_shift,
+                                           int off, int D, int d) {
+  const size_t blk = (head_page << (pt_shift - vb_shift)) + (off >> vb_shift);
+  return ((blk * D + d) << vb_shift) + (off & ((1 << vb_shift) - 1));
+}
 
 // One thread per (b, h, t, 8-dim chunk) of the new tokens.
 __global__ __launch_bounds__(kThreads) void append_kernel(
@@ -41,11 +51,12 @@ __global__ __launch_bounds__(kThreads) void append_kernel(
       *reinterpret_cast<const u32x4*>(k_new + src);
   // V column store (transposed page).
   const u32x4 v = *reinterpret_cast<const u32x4*>(v_new + src);
-  uint16_t* vcol = v_pool + ((head_page * D + c * 8) << pt_shift) + off;
+  const int vb_shift = pt_shift < 5 ? pt_shift : 5;
+  uint16_t* vcol = v_pool + v_offset(head_page, pt_shift, vb_shift, off, D, c * 8);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint32_t w = v[e >> 1];
-    vcol[static_cast<size_t>(e) << pt_shift] = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffff));
+    vcol[e << vb_shift] = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffff));
   }
 }
 
@@ -78,12 +89,13 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(
   const size_t head_page = static_cast<size_t>(slot) * NKV + h;
   *reinterpret_cast<u32x4*>(k_out + dst) =
       *reinterpret_cast<const u32x4*>(k_pool + ((head_page << pt_shift) + off) * D + c * 8);
-  const uint16_t* vcol = v_pool + ((head_page * D + c * 8) << pt_shift) + off;
+  const int vb_shift = pt_shift < 5 ? pt_shift : 5;
+  const uint16_t* vcol = v_pool + v_offset(head_page, pt_shift, vb_shift, off, D, c * 8);
   u32x4 v;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    v[w] = static_cast<uint32_t>(vcol[static_cast<size_t>(2 * w) << pt_shift]) |
-           (static_cast<uint32_t>(vcol[static_cast<size_t>(2 * w + 1) << pt_shift]) << 16);
+    v[w] = static_cast<uint32_t>(vcol[(2 * w) << vb_shift]) |
+           (static_cast<uint32_t>(vcol[(2 * w + 1) << vb_shift]) << 16);
   }
   *reinterpret_cast<u32x4*>(v_out + dst) = v;
 }

@@ -49,7 +49,7 @@ from . import ops
 from . import page_file
 from . import zstd as _zstd
 from .host_arena import HostArena, HostBlock
-from .page_pool import DevicePagePool
+from .page_pool import DevicePagePool, v_pages_to_tokens
 
 
 @dataclass
@@ -581,7 +581,7 @@ class PagedKVCache:
         def place(p, idx, stage):
             k_all[:, :, p.index * PT:(p.index + 1) * PT] = stage.k.index_select(0, idx)
             v_all[:, :, p.index * PT:(p.index + 1) * PT] = \
-                stage.v.index_select(0, idx).transpose(2, 3)
+                v_pages_to_tokens(stage.v.index_select(0, idx))
 
         self._place_spilled(layer, place)
         return k_all, v_all
@@ -1035,7 +1035,7 @@ class PagedKVCache:
     def _slot_contents(self, pool: DevicePagePool, idx: torch.Tensor):
         if self._geom[0] == "kv":
             return (pool.k.index_select(0, idx),
-                    pool.v.index_select(0, idx).transpose(2, 3).contiguous())
+                    v_pages_to_tokens(pool.v.index_select(0, idx)).contiguous())
         return (pool.lat.index_select(0, idx),)
 
     def _page_tensors(self, p: _Page):

@@ -7,7 +7,8 @@ built.
 
 Pool layouts (per layer):
   k_pool  [slots, num_kv_heads, page_tokens, head_dim]  bf16, token-major
-  v_pool  [slots, num_kv_heads, head_dim, page_tokens]  bf16, transposed pages
+  v_pool  [slots, num_kv_heads, page_tokens/VB, head_dim, VB]  bf16, V^T in blocks
+          of VB = min(page_tokens, 32) tokens (page_pool.v_slot_shape)
 """
 
 from __future__ import annotations
@@ -15,6 +16,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .page_pool import v_slot_shape
 
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
@@ -66,6 +68,12 @@ def gqa_workspace_bytes(batch: int, num_q_heads: int, num_kv_heads: int, head_di
                                                         head_dim, num_splits))
 
 
+def _check_v_pool(v_pool, slots, NKV, D, PT):
+    want = (slots,) + v_slot_shape(NKV, D, PT)
+    _require(tuple(v_pool.shape) == want,
+             f"v_pool must be [slots, NKV, PT/VB, D, VB] = {want}, got {tuple(v_pool.shape)}")
+
+
 def _gqa_plan(q, k_pool, v_pool, block_table, ctx_lens, out, scale, num_splits, ws):
     """Validate a paged GQA decode call; returns (q3, dims tuple, scale, splits, ws, need)."""
     if q.dim() == 4:
@@ -74,11 +82,10 @@ def _gqa_plan(q, k_pool, v_pool, block_table, ctx_lens, out, scale, num_splits, 
     _require(q.dim() == 3, "q must be [B, NQ, D]")
     dev = _require_device(q, k_pool, v_pool, block_table, ctx_lens, out)
     B, NQ, D = q.shape
-    _require(k_pool.dim() == 4 and v_pool.dim() == 4, "pools must be 4-D")
+    _require(k_pool.dim() == 4, "k_pool must be [slots, NKV, PT, D]")
     slots, NKV, PT, Dk = k_pool.shape
     _require(Dk == D, f"k_pool head_dim {Dk} != q head_dim {D}")
-    _require(tuple(v_pool.shape) == (slots, NKV, D, PT),
-             f"v_pool must be [slots, NKV, D, PT] = {(slots, NKV, D, PT)}, got {tuple(v_pool.shape)}")
+    _check_v_pool(v_pool, slots, NKV, D, PT)
     _require(q.dtype == k_pool.dtype == v_pool.dtype == torch.bfloat16,
              "q and pools must be bfloat16")
     _require(block_table.dtype == torch.int32 and ctx_lens.dtype == torch.int32,
@@ -185,7 +192,7 @@ def append_kv(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
     slots, NKVp, PT, Dp = k_pool.shape
     _require(v_new.shape == k_new.shape, "k_new and v_new shapes differ")
     _require(NKVp == NKV and Dp == D, "pool geometry does not match new K/V")
-    _require(tuple(v_pool.shape) == (slots, NKV, D, PT), "v_pool must be [slots, NKV, D, PT]")
+    _check_v_pool(v_pool, slots, NKV, D, PT)
     _require(k_new.dtype == v_new.dtype == k_pool.dtype == v_pool.dtype == torch.bfloat16,
              "K/V and pools must be bfloat16")
     _require(block_table.dtype == torch.int32 and positions.dtype == torch.int32,
@@ -203,7 +210,7 @@ def gather_kv(k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Ten
     dev = _require_device(k_pool, v_pool, block_table)
     slots, NKV, PT, D = k_pool.shape
     B = block_table.shape[0]
-    _require(tuple(v_pool.shape) == (slots, NKV, D, PT), "v_pool must be [slots, NKV, D, PT]")
+    _check_v_pool(v_pool, slots, NKV, D, PT)
     _require(block_table.dtype == torch.int32, "block_table must be int32")
     k = torch.empty((B, NKV, seq_len, D), dtype=k_pool.dtype, device=dev)
     v = torch.empty_like(k)

@@ -4,11 +4,16 @@ The framing is vpack's (formats/packed.py:8-11, 57-59): an 8-byte
 little-endian header length, a JSON header, then per tensor its high byte
 plane (zstd level 1 when compressed, raw otherwise) followed by its raw low
 byte plane.  A page file holds every tensor of one page of one layer (K and
-V^T, or the latent rows) in the device page layout, B slots after each other:
+V^T blocks, or the latent rows) in the device page layout, B slots after each
+other:
 
-    {"format": "voom-kv-page", "version": 1, "layer": L, "page": P,
+    {"format": "voom-kv-page", "version": 2, "layer": L, "page": P,
      "tensors": [{"name": "k", "dtype": "BF16", "shape": [B, NKV, PT, D],
-                  "lo": n, "hi": n, "hi_z": m | null}, ...]}
+                  "lo": n, "hi": n, "hi_z": m | null},
+                 {"name": "v", "dtype": "BF16", "shape": [B, NKV, PT/VB, D, VB], ...}]}
+
+Version 2 stores V as V^T blocks of VB = min(PT, 32) tokens (version 1 held
+one [D, PT] V^T per page).
 
 ``hi_z`` is the compressed length of the high plane, or null when it is
 stored raw (``hi`` bytes).  Writing goes through a temporary name and an
@@ -27,7 +32,7 @@ import numpy as np
 from . import zstd as _zstd
 
 FORMAT = "voom-kv-page"
-VERSION = 1
+VERSION = 2
 
 
 def page_path(spill_dir: Path, layer: int, page: int) -> Path:

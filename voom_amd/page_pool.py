@@ -3,7 +3,8 @@
 A slot holds one page of one sequence for one layer, as one or more tensors
 that share the slot index:
   KV pool      k [capacity, num_kv_heads, page_tokens, head_dim]   token-major
-               v [capacity, num_kv_heads, head_dim, page_tokens]   transposed (V^T)
+               v [capacity, num_kv_heads, page_tokens/VB, head_dim, VB]
+                 V^T in blocks of VB = min(page_tokens, 32) tokens
   latent pool  lat [capacity, page_tokens, latent_dim]             token-major
 Allocation, recycling and 25 % geometric growth follow the reference's
 PositionFreePagePool (runtime/kv_cache.py:316-414), with page_tokens-wide slots
@@ -16,6 +17,28 @@ from __future__ import annotations
 import math
 
 import torch
+
+
+V_BLOCK = 32  # tokens per transposed V block inside a page
+
+
+def v_slot_shape(num_kv_heads: int, head_dim: int, page_tokens: int) -> tuple[int, ...]:
+    """Shape of one V slot: [NKV, page_tokens / VB, head_dim, VB], VB = min(PT, 32)."""
+    vb = min(page_tokens, V_BLOCK)
+    return (num_kv_heads, page_tokens // vb, head_dim, vb)
+
+
+def v_pages_to_tokens(v: torch.Tensor) -> torch.Tensor:
+    """Blocked V^T pages [n, NKV, PT/VB, D, VB] -> token-major view [n, NKV, PT, D]."""
+    n, nkv, nb, d, vb = v.shape
+    return v.permute(0, 1, 2, 4, 3).reshape(n, nkv, nb * vb, d)
+
+
+def v_tokens_to_pages(v: torch.Tensor) -> torch.Tensor:
+    """Token-major [n, NKV, PT, D] -> contiguous blocked V^T pages [n, NKV, PT/VB, D, VB]."""
+    n, nkv, pt, d = v.shape
+    vb = min(pt, V_BLOCK)
+    return v.reshape(n, nkv, pt // vb, vb, d).transpose(3, 4).contiguous()
 
 
 class DevicePagePool:
@@ -35,8 +58,8 @@ class DevicePagePool:
 
     @classmethod
     def kv(cls, num_kv_heads: int, head_dim: int, page_tokens: int, **kw) -> "DevicePagePool":
-        return cls([(num_kv_heads, page_tokens, head_dim), (num_kv_heads, head_dim, page_tokens)],
-                   **kw)
+        return cls([(num_kv_heads, page_tokens, head_dim),
+                    v_slot_shape(num_kv_heads, head_dim, page_tokens)], **kw)
 
     @classmethod
     def rows(cls, page_tokens: int, row_elems: int, **kw) -> "DevicePagePool":

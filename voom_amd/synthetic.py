@@ -18,12 +18,14 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
+from .page_pool import v_pages_to_tokens, v_slot_shape, v_tokens_to_pages
+
 
 @dataclass
 class PagedGQAInputs:
     q: torch.Tensor            # [B, NQ, D] bf16
     k_pool: torch.Tensor       # [slots, NKV, PT, D] bf16
-    v_pool: torch.Tensor       # [slots, NKV, D, PT] bf16 (transposed pages)
+    v_pool: torch.Tensor       # [slots, NKV, PT/32, D, 32] bf16 (V^T blocks)
     block_table: torch.Tensor  # [B, max_pages] int32
     ctx_lens: torch.Tensor     # [B] int32
     ctx_host: np.ndarray
@@ -94,7 +96,7 @@ def gqa_decode_inputs(*, batch: int = 16, num_q_heads: int = 32, num_kv_heads: i
     gen.manual_seed(3 + seed_base if data_seed is None else data_seed)
     NKV, D, PT = num_kv_heads, head_dim, page_tokens
     k_pool = torch.empty((slots, NKV, PT, D), dtype=torch.bfloat16, device=dev)
-    v_pool = torch.empty((slots, NKV, D, PT), dtype=torch.bfloat16, device=dev)
+    v_pool = torch.empty((slots,) + v_slot_shape(NKV, D, PT), dtype=torch.bfloat16, device=dev)
     pos_rng = np.random.default_rng(4 + seed_base if data_seed is None else data_seed + 1)
     # Fill page by page in slot order, rotating K at random positions.
     chunk = 256
@@ -109,7 +111,7 @@ def gqa_decode_inputs(*, batch: int = 16, num_q_heads: int = 32, num_kv_heads: i
         sin = sin.view(n, 1, PT, D // 2)
         kr = apply_rope_neox(kr, cos, sin)
         k_pool[s0:s1] = kr.to(torch.bfloat16)
-        v_pool[s0:s1] = vr.to(torch.bfloat16).transpose(2, 3)
+        v_pool[s0:s1] = v_tokens_to_pages(vr.to(torch.bfloat16))
     q = torch.randn((batch, num_q_heads, D), generator=gen, device=dev,
                     dtype=torch.float32).to(torch.bfloat16)
     return PagedGQAInputs(
@@ -122,7 +124,7 @@ def gqa_decode_inputs(*, batch: int = 16, num_q_heads: int = 32, num_kv_heads: i
 def to_reference_layout(inp: PagedGQAInputs):
     """Host fp32 copies in the reference page layout [P, NKV, PT, D] for K and V."""
     k = inp.k_pool.float().cpu().numpy()
-    v = inp.v_pool.transpose(2, 3).float().cpu().numpy()
+    v = v_pages_to_tokens(inp.v_pool).float().cpu().numpy()
     q = inp.q.float().cpu().numpy()
     return q, k, v
 
