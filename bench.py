@@ -36,6 +36,34 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def graph_seconds(calls, reps: int) -> float:
+    """Seconds per call of the launches in `calls` (a list of no-argument
+    functions), captured once into a HIP graph and replayed `reps` times
+    between two events.  Replaying keeps the GPU busy back to back, so the
+    events measure the device, not the rate at which Python issues launches
+    (which, for calls of a few tens of microseconds, is the slower of the two).
+    Every call must already have run eagerly once, so its workspaces exist."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for fn in calls:
+                fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (reps * len(calls))
+
+
 def profiled_traffic(name: str) -> int | None:
     """HBM bytes per launch recorded by rocprofv3 PMC runs in profiles/<name>.md.
 
@@ -463,7 +491,8 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
 
     Four input sets (4 x 151 MB > 512 MB) rotate so the 256 MB Infinity Cache
     cannot hold the working set; the latent kernel (+ its reduce) is timed
-    with HIP events, the absorption GEMMs separately.
+    with HIP events around replays of a captured graph of the four steps,
+    the absorption GEMMs separately.
     """
     import numpy as np
     import torch
@@ -486,16 +515,11 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
         ops.mla_latent_decode(q_lats[i % 4], s_.lat_pool, s_.block_table, s_.ctx_lens,
                               scale=s_.scale, out=out, ws=ws)
 
-    for i in range(warmup):
+    for i in range(max(warmup, 4)):
         step(i)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(steps):
-        step(i)
-    e1.record()
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / steps / 1e3
+    # one graph of the four rotating steps, replayed
+    t = graph_seconds([lambda i=i: step(i) for i in range(4)], max(1, steps // 4))
     nbytes = inp.latent_bytes() + 8 * 128 * 576 * 2 + 8 * 128 * 512 * 2
     flops = inp.latent_flops()
     # absorption GEMMs (q_nope . W_UK, weighted_c . W_UV) on their own
@@ -580,16 +604,10 @@ def bench_position_free(steps: int, warmup: int, cpu_sample: bool) -> dict:
         return ops.position_free_paged_attention(q, kp, vp, table, kpos, qpos, cos, sin,
                                                  scale=scale)
 
-    for i in range(warmup):
+    for i in range(max(warmup, 4)):
         step(i)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(steps):
-        step(i)
-    e1.record()
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) / steps / 1e3
+    t = graph_seconds([lambda i=i: step(i) for i in range(4)], max(1, steps // 4))
     nbytes = TK * (2 * NKV * D * 2 + 8 + D * 4) + 2 * NQ * D * 2
     res = {
         "workload": "position-free decode: B=1, 32q/8kv, D=128, 32768 keys in one-token pages "
@@ -633,9 +651,10 @@ def bench_dsa(steps: int, warmup: int, cpu_sample: bool) -> dict:
     keys [131072, 128] bf16, 32 index heads, top-2048, then the absorbed-MLA
     contraction (128 heads, latent 576 in 64-token pages) over the selected
     rows only.  Eight rotating index-key sets (8 x 33.5 MB) keep the scoring
-    kernel's reads out of the Infinity Cache.  Timed per kernel with HIP
-    events; the scoring kernel's algorithmic bytes are the index keys (256 B
-    per token) plus q, w and the scores it writes (4 B per token)."""
+    kernel's reads out of the Infinity Cache.  Each stage is timed with HIP
+    events around replays of its own captured graph; the scoring kernel's
+    algorithmic bytes are the index keys (256 B per token) plus q, w and the
+    scores it writes (4 B per token)."""
     import numpy as np
     import torch
 
@@ -656,37 +675,38 @@ def bench_dsa(steps: int, warmup: int, cpu_sample: bool) -> dict:
     q_lat = torch.cat([q_abs, inp.q_rope], -1).contiguous()
     out_c = torch.empty((1, H, 512), dtype=torch.bfloat16, device="cuda")
 
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    t_sc = t_tk = t_mla = 0.0
-    sel = sel_lens = None
-    for i in range(warmup + steps):
-        ev[0].record()
+    sel = torch.empty((1, K), dtype=torch.int32, device="cuda")
+    sel_lens = torch.empty((1,), dtype=torch.int32, device="cuda")
+
+    def scores_of(i):
         ops.dsa_index_scores(q_idx, w_head, keys[i % 8], lens, scale=128 ** -0.5, out=scores)
-        ev[1].record()
-        sel, sel_lens = ops.dsa_topk(scores, lens, K)
-        ev[2].record()
+
+    def select():
+        ops.dsa_topk(scores, lens, K, sel=sel, sel_lens=sel_lens)
+
+    def contract():
         ops.mla_sparse_decode(q_lat, inp.lat_pool, inp.block_table, sel, sel_lens,
                               scale=inp.scale, out=out_c)
-        ev[3].record()
-        if i >= warmup:
-            torch.cuda.synchronize()
-            t_sc += ev[0].elapsed_time(ev[1]) / 1e3
-            t_tk += ev[1].elapsed_time(ev[2]) / 1e3
-            t_mla += ev[2].elapsed_time(ev[3]) / 1e3
-    t_sc, t_tk, t_mla = t_sc / steps, t_tk / steps, t_mla / steps
+
+    for i in range(max(warmup, 8)):
+        scores_of(i)
+        select()
+        contract()
+    torch.cuda.synchronize()
+    # each stage from its own graph (eight rotating key sets for the scores)
+    reps = max(1, steps // 8)
+    t_sc = graph_seconds([lambda i=i: scores_of(i) for i in range(8)], reps)
+    t_tk = graph_seconds([select], 8 * reps)
+    t_mla = graph_seconds([contract], 8 * reps)
     sc_bytes = S * 128 * 2 + NH * 128 * 2 + NH * 4 + S * 4
     sel_bytes = K * 576 * 2 + H * 576 * 2 + H * 512 * 2 + K * 4
     # the dense contraction the selection replaces, same cache
-    d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens, scale=inp.scale,
-                          out=out_c)
-    d0.record()
-    for _ in range(steps):
+    def dense():
         ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
                               scale=inp.scale, out=out_c)
-    d1.record()
-    torch.cuda.synchronize()
-    t_dense = d0.elapsed_time(d1) / steps / 1e3
+
+    dense()
+    t_dense = graph_seconds([dense], max(1, steps))
     res = {
         "workload": "DSA decode: B=1, 131072 cached tokens, index 32 heads x 128 bf16, top-2048, "
                     "absorbed MLA 128 heads over the selected latent rows (64-token pages)",

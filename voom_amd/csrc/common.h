@@ -56,6 +56,16 @@ __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
 // Marks a wave-uniform value as such (v_readfirstlane_b32 into an SGPR).
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// Waits until every vector-memory load of this wave has landed (vmcnt(0);
+// expcnt and lgkmcnt untouched).  Emitted through the s_waitcnt builtin so
+// the compiler's wait-count pass sees it: after an inline-asm wait that pass
+// still counts older loads (say, operands loaded before a loop) as pending
+// and inserts waits of its own before their uses, which then also wait for
+// every load issued since.
+__device__ __forceinline__ void wait_vmem_all() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15
+}
+
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
 // operations, then s_barrier.  Unlike __syncthreads() it does not drain
 // outstanding global loads, so register prefetches stay in flight across it.

@@ -29,9 +29,10 @@
 // after the last tile.  The C^T operand comes from the token-major tile through
 // ds_read_b64_tr_b16: in each 16-lane group, lane l receives element l%4 of
 // the 8-byte rows addressed by lanes 4c + l/4 (c = 0..3), so two transposed
-// reads give a lane the 8 tokens of one latent dim.  LDS rows are padded to
-// 73 sixteen-byte chunks, which spreads both the row reads of the score MFMA
-// and the transposed reads over all banks.
+// reads give a lane the 8 tokens of one latent dim.  LDS rows are unpadded
+// (72 sixteen-byte chunks) with chunk bits 1-2 XOR-swizzled by row bits 1-3
+// (tile_swizzle), which keeps both the row reads of the score MFMA and the
+// transposed reads free of bank conflicts.
 #include "common.h"
 
 namespace voom {
@@ -42,13 +43,24 @@ constexpr int kLat = 576;          // kv_lora_rank 512 + rope dim 64
 constexpr int kC = 512;
 constexpr int kTile = 64;          // tokens per tile
 constexpr int kChunksPerRow = kLat * 2 / 16;  // 72 sixteen-byte chunks per token
-constexpr int kRowChunks = kChunksPerRow + 1;  // padded LDS row: 73 chunks = 1168 B
-constexpr int kRow = kRowChunks * 8;           // LDS row stride in bf16 elements
-constexpr int kTileChunks = kTile * kRowChunks;  // 4672 = 73 x 64
-constexpr int kLoadsPerTile = kTileChunks / 64;  // 73 wave-wide 16-byte loads
+constexpr int kRow = kChunksPerRow * 8;        // LDS row stride in bf16 elements
+constexpr int kTileChunks = kTile * kChunksPerRow;  // 4608 = 72 x 64
+constexpr int kLoadsPerTile = kTileChunks / 64;     // 72 wave-wide 16-byte loads
 constexpr int kQSteps = kLat / 32;  // 18 k-steps of the score MFMA
-constexpr int kPRow = kTile + 8;    // P row stride (144 B): the 16 head rows of a lane
-                                    // group start on 16 different 4-bank groups
+constexpr int kPRow = kTile + 16;   // P row stride (160 B = 10 chunks): the 16 head rows
+                                    // of a 32-lane read phase fall on distinct banks
+
+// LDS tile swizzle: chunk c of token row r is stored at chunk c ^ tile_swizzle(r)
+// of the row (row bits 1-3 flip chunk bits 1-2; chunks 64..71 stay in place
+// as a group).  Measured on gfx950: ds_read_b128 serves 32 lanes per phase
+// in 8-byte halves over 128 four-byte banks, ds_read_b64_tr_b16 32 lanes per
+// phase over 64 banks.  With this swizzle the score reads (rows 16x + 0..15,
+// chunks 4s + g) and the transposed reads (rows 8g + 0..3 of two lane groups,
+// 32 bytes each) both touch every bank once per phase; a row padded to 73
+// chunks cost 4 and 2 conflict cycles per instruction respectively.
+__device__ __forceinline__ int tile_swizzle(int r) {
+  return ((((r >> 1) ^ (r >> 2)) & 1) << 1) | (((r >> 3) & 1) << 2);
+}
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -173,15 +185,14 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
   }
 
   // Lane-constant source offsets of this wave's direct-to-LDS loads: load i
-  // (i = w, w+8, ...) fills LDS chunks 64i..64i+63 of the padded tile; chunk
-  // (row, col) holds bytes 16*col of token row; the padding chunk of a row
-  // reads past the buffer end and lands as zeros.
+  // (i = w, w+8, ...) fills LDS chunks 64i..64i+63 of the tile; LDS chunk
+  // (row, col) holds bytes 16 * (col ^ tile_swizzle(row)) of token row.
   // Source offset of load k.
   auto src_off_of = [&](int k) {
     const int j = 64 * (w + kMlaWaves * k) + lane;
-    const int row = j / kRowChunks;
-    const int col = j - row * kRowChunks;
-    return col < kChunksPerRow ? (row * kChunksPerRow + col) * 16 : 0x40000000;
+    const int row = j / kChunksPerRow;
+    const int col = j - row * kChunksPerRow;
+    return (row * kChunksPerRow + (col ^ tile_swizzle(row))) * 16;
   };
   int src_off[kLoadsPerWave];
 #pragma unroll
@@ -241,12 +252,12 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
       for (int k = 0; k < kLoadsPerWave; ++k) {
         const int i = w + kMlaWaves * k;
         const int j = 64 * i + lane;
-        const int row = j / kRowChunks;
-        const int col = j - row * kRowChunks;
-        const uint32_t base = pre_off[(t - t_lo) & (kPre - 1)][row & 63];
-        const uint32_t off =
-            (row < kTile && col < kChunksPerRow && base != 0xFFFFFFF0u) ? base + col * 16
-                                                                         : 0xFFFFFFF0u;
+        const int row = j / kChunksPerRow;  // < kTile: the loads cover the tile exactly
+        const int col = j - row * kChunksPerRow;
+        const uint32_t base = pre_off[(t - t_lo) & (kPre - 1)][row];
+        const uint32_t off = base != 0xFFFFFFF0u
+                                 ? base + static_cast<uint32_t>(col ^ tile_swizzle(row)) * 16
+                                 : 0xFFFFFFF0u;
         if (i < kLoadsPerTile) {
           __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + i * 64 * 8), 16,
                                                    static_cast<int>(off), 0, 0, 0);
@@ -280,8 +291,12 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
   // One tile of work on LDS buffer `tile` while tile t+1 streams into `next`.
   auto step = [&](int t, const uint16_t* tile, uint16_t* next) {
     // This wave's loads of tile t have landed; after the barrier every wave's
-    // have, and every wave is done with the other buffer (tile t-1).
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // have, and every wave is done with the other buffer (tile t-1).  The
+    // wait is the builtin (wait_vmem_all), not inline asm: with an asm wait
+    // the compiler still counted the q operand loads from before the loop as
+    // pending and waited before every score MFMA -- in effect for the whole
+    // next tile, which is issued just before (7 % of the kernel).
+    wait_vmem_all();
     lds_barrier();
     if (t + 1 < t_hi) load_tile(t + 1, next);
 
@@ -292,19 +307,26 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
       // The latent rows of k-step s + kAhead are read while the MFMAs of
       // step s run, so no MFMA waits on a read issued just before it.
       constexpr int kAhead = 2;
+      // Row 16x + i16, logical chunk 4s + g sits at chunk 4(s ^ flip) + lo:
+      // the swizzle of rows 16x + i16 depends on i16 only.
+      const int sw = tile_swizzle(i16);
+      const int lo = g ^ (sw & 2);
+      const int flip = sw >> 2;
       const uint16_t* arow[TTW];
       f32x4 sc[TTW][HTW];
       u32x4 ring[kAhead + 1][TTW];
 #pragma unroll
       for (int j = 0; j < TTW; ++j) {
-        arow[j] = tile + (16 * (wg * TTW + j) + i16) * kRow + 8 * g;
+        arow[j] = tile + (16 * (wg * TTW + j) + i16) * kRow + 8 * lo;
 #pragma unroll
         for (int k = 0; k < HTW; ++k) sc[j][k] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
+      // element offset of k-step s: 32 * (s ^ flip)
+      auto kstep = [&](int s) { return 32 * s + ((s & 1) ? -32 : 32) * flip; };
 #pragma unroll
       for (int s = 0; s < kAhead; ++s) {
 #pragma unroll
-        for (int j = 0; j < TTW; ++j) ring[s][j] = *reinterpret_cast<const u32x4*>(arow[j] + 32 * s);
+        for (int j = 0; j < TTW; ++j) ring[s][j] = *reinterpret_cast<const u32x4*>(arow[j] + kstep(s));
       }
 #pragma unroll
       for (int s = 0; s < kQSteps; ++s) {
@@ -312,7 +334,7 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
 #pragma unroll
           for (int j = 0; j < TTW; ++j) {
             ring[(s + kAhead) % (kAhead + 1)][j] =
-                *reinterpret_cast<const u32x4*>(arow[j] + 32 * (s + kAhead));
+                *reinterpret_cast<const u32x4*>(arow[j] + kstep(s + kAhead));
           }
         }
 #pragma unroll
@@ -398,6 +420,10 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
     // 8g + (k/4) (+4 for the second read) at dims 4*(k%4) of the dim tile.
     const int trow_tok = 8 * g + (i16 >> 2);
     const int tcol = 4 * (i16 & 3);
+    // The swizzle of those rows permutes the four 16-dim tiles of the wave's
+    // 64 dims: tile dt is stored at dt ^ x.
+    const int x_lo = tile_swizzle(trow_tok) >> 1;
+    const int x_hi = tile_swizzle(trow_tok + 4) >> 1;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8 pb[NHT];
@@ -411,9 +437,9 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (lds_bf16x4*)(trb + 16 * dt));
+            (lds_bf16x4*)(trb + 16 * (dt ^ x_lo)));
         const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (lds_bf16x4*)(trb + 4 * kRow + 16 * dt));
+            (lds_bf16x4*)(trb + 4 * kRow + 16 * (dt ^ x_hi)));
         const bf16x8 av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int ht = 0; ht < NHT; ++ht) {

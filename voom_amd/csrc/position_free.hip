@@ -223,7 +223,7 @@ void pf_attention_kernel(PfArgs a) {
   }
   // nothing of the prologue stays in flight into the loop, so the loop's
   // waits count only its own loads
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wait_vmem_all();
   lds_barrier();
 
   for (int bi = blo; bi < bhi; ++bi) {

@@ -388,17 +388,23 @@ def dsa_index_scores(q_idx: torch.Tensor, w_head: torch.Tensor, k_idx: torch.Ten
 
 
 def dsa_topk(scores: torch.Tensor, lens: torch.Tensor, k: int, *,
+             sel: torch.Tensor | None = None, sel_lens: torch.Tensor | None = None,
              stream: torch.cuda.Stream | None = None):
     """Top-k of each row's first lens[b] scores as ascending int32 indices
     (runtime/glm_dsa.py:151-160).  Returns (sel [B, k], sel_lens [B]);
-    sel_lens[b] = min(lens[b], k), entries past it are unspecified."""
-    dev = _require_device(scores, lens)
+    sel_lens[b] = min(lens[b], k), entries past it are unspecified.  sel and
+    sel_lens may be given (int32, those shapes) to be written in place."""
+    dev = _require_device(scores, lens, sel, sel_lens)
     _require(scores.dim() == 2 and scores.dtype == torch.float32, "scores [B, cap] fp32")
     _require(lens.dtype == torch.int32 and tuple(lens.shape) == (scores.shape[0],), "lens [B] int32")
     _require(int(k) > 0, "k must be positive")
     B, cap = scores.shape
-    sel = torch.empty((B, int(k)), dtype=torch.int32, device=dev)
-    sel_lens = torch.empty((B,), dtype=torch.int32, device=dev)
+    if sel is None:
+        sel = torch.empty((B, int(k)), dtype=torch.int32, device=dev)
+    if sel_lens is None:
+        sel_lens = torch.empty((B,), dtype=torch.int32, device=dev)
+    _require(sel.dtype == sel_lens.dtype == torch.int32 and tuple(sel.shape) == (B, int(k))
+             and tuple(sel_lens.shape) == (B,), "sel [B, k] and sel_lens [B] int32")
     need = int(_lib.lib().voom_dsa_topk_workspace_bytes(B, cap))
     ws = workspace(dev, need, tag=4)
     _lib.call("voom_dsa_topk", _ptr(scores), _ptr(lens), _ptr(sel), _ptr(sel_lens), _ptr(ws),
