@@ -146,12 +146,15 @@ void pf_attention_kernel(PfArgs a) {
     }
   }
 
+  // K and V rows are read once per call: non-temporal loads (measured 37.7 ->
+  // 36.7 us per call at 32,768 keys).
   auto load_k = [&](int rlo, int rhi, u32x4 (&kk)[2][KS]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const uint16_t* krow = a.k_pages + pf_row_of(rlo, rhi, 16 * t + i16) * D;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kk[t][s] = *reinterpret_cast<const u32x4*>(krow + 32 * s + 8 * g);
+      for (int s = 0; s < KS; ++s)
+        kk[t][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow + 32 * s + 8 * g));
     }
   };
   auto load_v = [&](int rlo, int rhi, u32x4 (&vv)[kVLoads]) {
@@ -160,7 +163,8 @@ void pf_attention_kernel(PfArgs a) {
       const int c = u * kWave + lane;
       const int r = c / (D / 8);
       const int col = c - r * (D / 8);
-      vv[u] = *reinterpret_cast<const u32x4*>(a.v_pages + pf_row_of(rlo, rhi, r) * D + 8 * col);
+      vv[u] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(a.v_pages + pf_row_of(rlo, rhi, r) * D + 8 * col));
     }
   };
   // V rows, coalesced 16-byte chunks, into this wave's LDS slice
