@@ -58,9 +58,12 @@ int voom_abi_version(void);
  *   lse_out  [batch, num_q_heads] fp32 natural-log sum-exp of the scaled
  *            scores, or NULL.  Lets two calls over disjoint page sets be merged
  *            with voom_merge_attn_states.
- *   num_splits  number of wavefronts sharing the work (0 = library default);
- *            the workspace must hold voom_paged_gqa_workspace_bytes(...) bytes
- *            for the same value.
+ *   num_splits  number of wavefronts sharing the work (0 = library choice:
+ *            a block table of at most 4096 tokens per sequence then runs one
+ *            workgroup per (sequence, kv head) that merges its own waves and
+ *            writes out directly -- one launch, workspace untouched; longer
+ *            tables split-K over the default count); the workspace must hold
+ *            voom_paged_gqa_workspace_bytes(...) bytes for the same value.
  * head_dim in {64, 128}; num_q_heads / num_kv_heads <= 16; page_tokens a power
  * of two >= 32.  Sequences with ctx_len 0 produce zeros (lse = -inf).
  * ------------------------------------------------------------------------- */
@@ -82,7 +85,8 @@ int voom_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
  *   voom_paged_gqa_combine   merges each head's partial states into out and
  *                            lse_out (the online-softmax merge of
  *                            runtime/pic_attention.py:106-129).
- * voom_paged_gqa_decode(...) is exactly partials followed by combine. */
+ * voom_paged_gqa_decode(...) with num_splits > 0, or a table longer than 4096
+ * tokens, is exactly partials followed by combine. */
 int voom_paged_gqa_partials(const void* q, const void* k_pool, const void* v_pool,
                             const int32_t* block_table, const int32_t* ctx_lens,
                             void* workspace, size_t ws_bytes, int batch, int num_q_heads,
@@ -227,6 +231,16 @@ int voom_rope_split(const void* qkv, const float* cos_table, const float* sin_ta
                     int head_dim, hipStream_t stream);
 int voom_silu_mul(const void* gate_up, void* out, int rows, int intermediate,
                   hipStream_t stream);
+
+/* voom_gemv_bf16: one-token projection y [n] = bf16(weight [n, k] . x [k]),
+ * fp32 sums -- the _linear calls of a decode step (runtime/layer_runner.py:73,
+ * 182, 186-190) at one row of activations.  With swiglu != 0, weight is the
+ * fused [gate; up] projection [2n, k] and y [n] = bf16(bf16(silu(g)) * u) of
+ * the bf16-rounded projections g (row r) and u (row n + r): the gate/up
+ * projections and _silu_mul (layer_runner.py:186-188) in one launch.
+ * k a multiple of 8 up to 2048; weight and x 16-byte aligned. */
+int voom_gemv_bf16(const void* weight, const void* x, void* y, int n, int k, int swiglu,
+                   hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Page writes and reads.

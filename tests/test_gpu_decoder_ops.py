@@ -72,3 +72,48 @@ def test_silu_mul(rows, inter):
     got = ops.silu_mul(gu)
     torch.cuda.synchronize()
     ulp_close(got, ref)
+
+
+@pytest.mark.parametrize("n,k", [(1, 8), (5, 576), (960, 576), (576, 1536), (3072, 576),
+                                 (7, 2048), (130, 520), (49152, 576)])
+def test_gemv_is_the_fp32_product_rounded(n, k):
+    # fp32 sums in a different order than the reference: within bf16 rounding of
+    # the exact product, plus a term for cancellation near zero
+    print(f"[decoder-ops] gemv n={n} k={k}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(n * 7 + k)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    x = torch.randn((1, 1, k), generator=g, device="cuda").to(torch.bfloat16)
+    got = ops.gemv(x, w)
+    torch.cuda.synchronize()
+    assert got.shape == (1, 1, n) and got.dtype == torch.bfloat16
+    exact = (w.double() @ x.reshape(k).double())
+    scale = (w.double().abs() @ x.reshape(k).double().abs())
+    err = (got.reshape(n).double() - exact).abs()
+    assert bool((err <= exact.abs() * 2.0 ** -8 + scale * 1e-6).all())
+
+
+@pytest.mark.parametrize("inter,k", [(1, 8), (3, 576), (1536, 576), (7, 1544)])
+def test_gemv_swiglu_is_projection_then_silu_mul(inter, k):
+    print(f"[decoder-ops] gemv swiglu I={inter} k={k}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(inter * 3 + k)
+    w = (torch.randn((2 * inter, k), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    x = torch.randn((k,), generator=g, device="cuda").to(torch.bfloat16)
+    got = ops.gemv(x, w, swiglu=True)
+    # the unfused path: projection rounded to bf16, then silu_mul's math
+    gu = (w.float() @ x.float()).to(torch.bfloat16)
+    ref = F.silu(gu[:inter]) * gu[inter:]
+    torch.cuda.synchronize()
+    assert got.shape == (inter,)
+    torch.testing.assert_close(got.float(), ref.float(), rtol=2e-2, atol=2e-3)
+
+
+def test_gemv_rejects_unsupported_shapes():
+    w = torch.zeros((4, 576), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        ops.gemv(torch.zeros((2, 576), dtype=torch.bfloat16, device="cuda"), w)  # two rows
+    with pytest.raises(ValueError):
+        ops.gemv(torch.zeros((4096,), dtype=torch.bfloat16, device="cuda"),
+                 torch.zeros((4, 4096), dtype=torch.bfloat16, device="cuda"))  # K too large
+    with pytest.raises(ValueError):
+        ops.gemv(torch.zeros((12,), dtype=torch.bfloat16, device="cuda"),
+                 torch.zeros((4, 12), dtype=torch.bfloat16, device="cuda"))  # K % 8

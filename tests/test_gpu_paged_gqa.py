@@ -53,15 +53,16 @@ def test_split_counts_agree(splits):
              num_q_heads=32, num_kv_heads=8, head_dim=128, page_tokens=64, num_splits=splits)
 
 
-@pytest.mark.parametrize("D,splits", [(128, None), (64, 5)])
+@pytest.mark.parametrize("D,splits", [(128, 96), (64, 5)])
 def test_partials_then_combine_is_the_decode_bitwise(D, splits):
+    # with an explicit split count the decode is exactly the two halves
     print(f"[gqa] case partials+combine D={D} splits={splits}", flush=True)
     inp = synthetic.gqa_decode_inputs(batch=3, ctx_lens=[0, 700, 2500], num_q_heads=16,
                                       num_kv_heads=4, head_dim=D, device="cuda")
     whole, lse = ops.paged_gqa_decode(inp.q, inp.k_pool, inp.v_pool, inp.block_table,
                                       inp.ctx_lens, scale=inp.scale, return_lse=True,
                                       num_splits=splits)
-    n = splits if splits is not None else min(ops.default_splits(), 3 * 4 * inp.block_table.shape[1] * 2)
+    n = splits
     ws = torch.empty(ops.gqa_workspace_bytes(3, 16, 4, D, n), dtype=torch.uint8, device="cuda")
     ops.paged_gqa_partials(inp.q, inp.k_pool, inp.v_pool, inp.block_table, inp.ctx_lens,
                            scale=inp.scale, num_splits=n, ws=ws)
@@ -72,6 +73,33 @@ def test_partials_then_combine_is_the_decode_bitwise(D, splits):
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), whole.view(torch.int16))
     assert torch.equal(lse2, lse)
+
+
+@pytest.mark.parametrize("D,G", [(128, 4), (64, 3), (128, 16)])
+def test_short_tables_take_the_segment_kernel_and_match(D, G):
+    # a block table of <= 4096 tokens with the default split count runs one
+    # workgroup per (sequence, kv head); it must agree with the oracle and with
+    # split-K (same math, another merge order), LSE included, empty rows zero
+    print(f"[gqa] case segment kernel D={D} G={G}", flush=True)
+    NKV = 2 if G == 16 else 4
+    inp = synthetic.gqa_decode_inputs(batch=4, ctx_lens=[0, 1, 700, 4000], num_q_heads=NKV * G,
+                                      num_kv_heads=NKV, head_dim=D, device="cuda")
+    assert inp.block_table.shape[1] * 64 <= 4096
+    seg, lse_s = ops.paged_gqa_decode(inp.q, inp.k_pool, inp.v_pool, inp.block_table,
+                                      inp.ctx_lens, scale=inp.scale, return_lse=True)
+    spl, lse_k = ops.paged_gqa_decode(inp.q, inp.k_pool, inp.v_pool, inp.block_table,
+                                      inp.ctx_lens, scale=inp.scale, return_lse=True,
+                                      num_splits=64)
+    torch.cuda.synchronize()
+    q, k, v = synthetic.to_reference_layout(inp)
+    ref = opa.paged_decode(q, k, v, inp.table_host, inp.ctx_host, inp.scale)
+    np.testing.assert_allclose(seg.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(seg.float().cpu().numpy(), spl.float().cpu().numpy(),
+                               atol=ATOL, rtol=RTOL)
+    assert torch.equal(seg[0], torch.zeros_like(seg[0]))
+    assert bool(torch.isneginf(lse_s[0]).all())
+    # fp32 normalisers summed in another order: a few 1e-5 relative apart
+    torch.testing.assert_close(lse_s[1:], lse_k[1:], rtol=1e-4, atol=1e-4)
 
 
 def test_empty_sequence_gives_zeros():

@@ -1,7 +1,8 @@
 // Fused per-token ops of the config-1 decoder harness (a Llama-style block
 // around the paged attention), so that one decode step is a short chain of
 // launches: the residual add + RMSNorm, RoPE of q and k together with the
-// split of the fused qkv projection into the attention layouts, and SwiGLU.
+// split of the fused qkv projection into the attention layouts, SwiGLU, and
+// the one-token projections (GEMV, optionally with SwiGLU fused).
 // They restate the block math of runtime/layer_runner.py (rms_norm :263,309,
 // rope :99-103, _silu_mul :43-46 and :188) with Hugging Face LlamaForCausalLM's
 // cast order -- the reference its parity tests use:
@@ -156,10 +157,137 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(
   *reinterpret_cast<u32x4*>(out + static_cast<size_t>(row) * inter + c) = o;
 }
 
+// One-token projection: y[r] = bf16(sum_k W[r][k] x[k]) with W [N, K] bf16
+// row-major (a torch Linear weight), x [K], fp32 sums.  Decode runs these at
+// one row of activations, where a GEMM tiling reads the weights at a fraction
+// of the bandwidth; here each wavefront takes 4 weight rows, every lane holds
+// KC 16-byte chunks of x (chunks lane, lane + 64, ...) in registers and reads
+// the same chunks of its 4 rows (coalesced 1 KB per row per step, all 4 x KC
+// loads in flight, non-temporal: each weight byte is used once per token),
+// and the 4 dot products are summed across the lanes.
+// SWIGLU: W is the fused [gate; up] weight [2I, K] and y [I] is
+// bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections of rows r
+// and I + r -- the projection followed by silu_mul_kernel's math; a wave then
+// takes 2 gate and the 2 matching up rows.
+template <int KC, bool SWIGLU>
+__global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, int n, int k) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * (kRowThreads / kWave) + (threadIdx.x / kWave);
+  const int chunks = k / 8;
+  // rows of this wave: plain 4r..4r+3; SwiGLU gate 2r, 2r+1 and up n + 2r, n + 2r + 1
+  int rows[4];
+  if (SWIGLU) {
+    rows[0] = 2 * wave;
+    rows[1] = 2 * wave + 1;
+    rows[2] = n + 2 * wave;
+    rows[3] = n + 2 * wave + 1;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rows[i] = 4 * wave + i;
+  }
+  const int first = SWIGLU ? 2 * wave : 4 * wave;
+  if (first >= n) return;
+  float xv[KC][8];
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    const int c = lane + kWave * j;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (c < chunks) v = *reinterpret_cast<const u32x4*>(x + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xv[j][2 * e] = bf2f(static_cast<uint16_t>(v[e] & 0xffffu));
+      xv[j][2 * e + 1] = bf2f(static_cast<uint16_t>(v[e] >> 16));
+    }
+  }
+  u32x4 wv[4][KC];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int local = SWIGLU ? (i & 1) : i;
+    const bool ok = first + local < n;
+    const uint16_t* wr = w + static_cast<size_t>(ok ? rows[i] : rows[0]) * k;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      const int c = lane + kWave * j;
+      wv[i][j] = c < chunks ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 8 * c))
+                            : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  float acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s += bf2f(static_cast<uint16_t>(wv[i][j][e] & 0xffffu)) * xv[j][2 * e];
+        s += bf2f(static_cast<uint16_t>(wv[i][j][e] >> 16)) * xv[j][2 * e + 1];
+      }
+    }
+#pragma unroll
+    for (int o = kWave / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+    acc[i] = s;
+  }
+  if (lane == 0) {
+    if (SWIGLU) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (first + i < n) {
+          const float g = bf2f(f2bf(acc[i]));
+          const float u = bf2f(f2bf(acc[2 + i]));
+          const float sg = bf2f(f2bf(g / (1.f + expf(-g))));
+          y[first + i] = f2bf(sg * u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (first + i < n) y[first + i] = f2bf(acc[i]);
+      }
+    }
+  }
+}
+
+template <bool SWIGLU>
+int launch_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, int n, int k,
+                hipStream_t stream) {
+  const int rows_per_wave = SWIGLU ? 2 : 4;
+  const long long waves = (static_cast<long long>(n) + rows_per_wave - 1) / rows_per_wave;
+  const dim3 grid(static_cast<unsigned>((waves + kRowThreads / kWave - 1) / (kRowThreads / kWave)));
+  const int kc = (k / 8 + kWave - 1) / kWave;
+  switch (kc) {
+    case 1: hipLaunchKernelGGL((gemv_kernel<1, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<2, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
+    case 3: hipLaunchKernelGGL((gemv_kernel<3, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
+    default: hipLaunchKernelGGL((gemv_kernel<4, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
+  }
+  return VOOM_LAUNCH_CHECK("gemv: kernel launch");
+}
+
 }  // namespace
 }  // namespace voom
 
 using namespace voom;
+
+extern "C" int voom_gemv_bf16(const void* weight, const void* x, void* y, int n, int k,
+                              int swiglu, hipStream_t stream) {
+  const char* who = "gemv_bf16";
+  VOOM_REQUIRE(weight && x && y, "%s: null pointer argument", who);
+  VOOM_REQUIRE(n > 0 && k > 0 && k % 8 == 0 && k <= 8 * kWave * 4,
+               "%s: k %d must be a positive multiple of 8 up to %d", who, k, 8 * kWave * 4);
+  VOOM_REQUIRE(n < (1 << 28), "%s: n %d too large", who, n);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(y) % 2 == 0,
+               "%s: weight and x must be 16-byte aligned", who);
+  const auto* w = static_cast<const uint16_t*>(weight);
+  const auto* xv = static_cast<const uint16_t*>(x);
+  auto* yv = static_cast<uint16_t*>(y);
+  return swiglu ? launch_gemv<true>(w, xv, yv, n, k, stream)
+                : launch_gemv<false>(w, xv, yv, n, k, stream);
+}
 
 extern "C" int voom_add_rms_norm(void* x, const void* delta, const void* weight, void* out,
                                  int rows, int hidden, float eps, hipStream_t stream) {

@@ -380,6 +380,124 @@ __global__ __launch_bounds__(kThreads, WAVES_PER_EU) void gqa_decode_kernel(
   }
 }
 
+// Short contexts: one workgroup per (sequence, kv head) segment.  Its four
+// wavefronts take a quarter of the segment's 32-token blocks each with the
+// partials kernel's block loop, leave their softmax states in LDS, and merge
+// them into the bf16 output (and LSE) themselves -- one launch and no
+// workspace, where the split-K pair of kernels costs two launches of
+// mostly fixed latency when a segment has only a few dozen blocks.
+template <int D, int NBUF>
+__global__ __launch_bounds__(kThreads) void gqa_segment_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ ctx_lens, uint16_t* __restrict__ out,
+    float* __restrict__ lse_out, int NKV, int G, int max_pages, int pt_shift, int num_slots,
+    float scale_log2e) {
+  __shared__ float red_o[kWavesPerBlock][16][D];
+  __shared__ float red_m[kWavesPerBlock][16];
+  __shared__ float red_l[kWavesPerBlock][16];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wl = uniform(threadIdx.x / kWave);
+  const int b = blockIdx.x / NKV;
+  const int kvh = blockIdx.x - b * NKV;
+  const int NQ = NKV * G;
+  const int cap_tokens = max_pages << pt_shift;
+  int ctx = uniform(ctx_lens[b]);
+  ctx = ctx < 0 ? 0 : (ctx > cap_tokens ? cap_tokens : ctx);
+  const int nb = (ctx + kBlockTokens - 1) / kBlockTokens;
+  const int blo = wl * nb / kWavesPerBlock;
+  const int bhi = (wl + 1) * nb / kWavesPerBlock;
+
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const bool head_ok = i16 < G;
+  LaneOffsets lofs;
+  lofs.k = ((8 * (i16 >> 2) + (i16 & 3)) * D + 8 * g) * 2;
+  lofs.v = ((i16 * kBlockTokens) + 8 * g) * 2;
+  SegmentArgs a;
+  a.k_pool = k_pool;
+  a.v_pool = v_pool;
+  a.table_row = block_table + static_cast<size_t>(b) * max_pages;
+  a.n_pages = max_pages;
+  a.kvh = kvh;
+  a.nkv = NKV;
+  a.pt_shift = pt_shift;
+  a.num_slots = num_slots;
+  a.ctx = ctx;
+
+  SoftmaxState<D> st;
+#pragma unroll
+  for (int n = 0; n < D / 16; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.l = 0.f;
+  if (blo < bhi) {
+    u32x4 qop[D / 32];
+    const uint16_t* qh = q + (static_cast<size_t>(b) * NQ + kvh * G + (head_ok ? i16 : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qop[s] = head_ok ? *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g) : z;
+    }
+    int tab_base = -(1 << 30);
+    int tab = 0;
+    BlockRegs<D> ring[NBUF];
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; ++j) {
+      load_block<D>(ring[j], a, blo + j, bhi, tab_base, tab, lane, lofs);
+    }
+    int bi = blo;
+    bool done = false;
+    while (!done) {
+#pragma unroll
+      for (int j = 0; j < NBUF; ++j) {
+        if (!done) {
+          const int pf = bi + NBUF - 1;
+          load_block<D>(ring[(j + NBUF - 1) % NBUF], a, pf, bhi, tab_base, tab, lane, lofs);
+          compute_block<D>(ring[j], qop, st, a.ctx - bi * kBlockTokens, scale_log2e, lane);
+          done = ++bi >= bhi;
+        }
+      }
+    }
+  }
+  const float l_tot = wave_sum_across_groups(st.l);
+  if (head_ok) {
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red_o[wl][i16][16 * n + 4 * g + r] = st.acc[n][r];
+    }
+    if (g == 0) {
+      red_m[wl][i16] = st.m;
+      red_l[wl][i16] = l_tot;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int h = idx / D;
+    const int d = idx - h * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) M = fmaxf(M, red_m[w][h]);
+    const size_t row = static_cast<size_t>(b) * NQ + kvh * G + h;
+    if (M == -INFINITY) {  // no tokens
+      out[row * D + d] = 0;
+      if (lse_out != nullptr && d == 0) lse_out[row] = -INFINITY;
+      continue;
+    }
+    float L = 0.f;
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      const float mw = red_m[w][h];
+      const float wt = mw == -INFINITY ? 0.f : fast_exp2(mw - M);
+      L += red_l[w][h] * wt;
+      o += red_o[w][h][d] * wt;
+    }
+    out[row * D + d] = f2bf(o * (1.f / L));
+    if (lse_out != nullptr && d == 0) lse_out[row] = (M + __log2f(L)) * 0.6931471805599453f;
+  }
+}
+
 // Wavefront of the split holding unit u (the last w with w*U/W <= u).
 __device__ __forceinline__ long long wave_of_unit(long long u, long long U, int W) {
   return ((u + 1) * W - 1) / U;
@@ -619,6 +737,32 @@ int launch_partials(const GqaPlan& p, const void* q, const void* k_pool, const v
   return VOOM_LAUNCH_CHECK("paged_gqa: partials kernel launch");
 }
 
+// Block tables of at most this many tokens per sequence use the one-launch
+// segment kernel when the caller leaves the split count to the library
+// (32 blocks per wavefront at most).
+constexpr long long kSegmentKernelTokens = 4096;
+
+int launch_segments(const GqaPlan& p, const void* q, const void* k_pool, const void* v_pool,
+                    const int32_t* block_table, const int32_t* ctx_lens, int num_slots,
+                    float scale, void* out, float* lse_out, hipStream_t stream) {
+  const float scale_log2e = scale * 1.4426950408889634f;
+  const dim3 grid(static_cast<unsigned>(p.B * p.NKV));
+  const auto* qq = static_cast<const uint16_t*>(q);
+  const auto* kp = static_cast<const uint16_t*>(k_pool);
+  const auto* vp = static_cast<const uint16_t*>(v_pool);
+  auto* oo = static_cast<uint16_t*>(out);
+  if (p.D == 128) {
+    hipLaunchKernelGGL((gqa_segment_kernel<128, kNbuf128>), grid, dim3(kThreads), 0, stream, qq,
+                       kp, vp, block_table, ctx_lens, oo, lse_out, p.NKV, p.G, p.max_pages,
+                       p.pt_shift, num_slots, scale_log2e);
+  } else {
+    hipLaunchKernelGGL((gqa_segment_kernel<64, kNbuf64>), grid, dim3(kThreads), 0, stream, qq,
+                       kp, vp, block_table, ctx_lens, oo, lse_out, p.NKV, p.G, p.max_pages,
+                       p.pt_shift, num_slots, scale_log2e);
+  }
+  return VOOM_LAUNCH_CHECK("paged_gqa: segment kernel launch");
+}
+
 int launch_combine(const GqaPlan& p, const int32_t* ctx_lens, void* out, float* lse_out,
                    hipStream_t stream) {
   const dim3 grid((p.B * p.NQ + kWavesPerBlock - 1) / kWavesPerBlock);
@@ -662,10 +806,15 @@ extern "C" int voom_paged_gqa_decode(const void* q, const void* k_pool, const vo
   int rc = check_partials_args(who, q, k_pool, v_pool, block_table, ctx_lens, num_slots);
   if (rc) return rc;
   VOOM_REQUIRE(out != nullptr, "%s: null output", who);
+  const bool auto_splits = num_splits <= 0;
   GqaPlan p;
   rc = plan_gqa(who, workspace, ws_bytes, batch, num_q_heads, num_kv_heads, head_dim,
                 page_tokens, max_pages, num_splits, &p);
   if (rc) return rc;
+  if (auto_splits && static_cast<long long>(max_pages) * page_tokens <= kSegmentKernelTokens) {
+    return launch_segments(p, q, k_pool, v_pool, block_table, ctx_lens, num_slots, scale,
+                           out, lse_out, stream);
+  }
   rc = launch_partials(p, q, k_pool, v_pool, block_table, ctx_lens, num_slots, scale, stream);
   if (rc) return rc;
   return launch_combine(p, ctx_lens, out, lse_out, stream);

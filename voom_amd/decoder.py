@@ -125,8 +125,21 @@ class PagedDecoder:
 
     @staticmethod
     def _linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        """x . weight^T: one row of activations (a decode step) through the
+        one-token GEMV kernel, more rows (prefill, batches) through the library
+        GEMM."""
         shape = x.shape
+        if x.numel() == shape[-1] and shape[-1] <= ops.GEMV_MAX_K:
+            return ops.gemv(x.contiguous(), weight)
         return F.linear(x.reshape(-1, shape[-1]), weight).reshape(*shape[:-1], weight.shape[0])
+
+    def _mlp(self, h: torch.Tensor, lw: dict) -> torch.Tensor:
+        """down(bf16(silu(gate(h))) * up(h)); one row fuses gate/up and SwiGLU."""
+        if h.numel() == h.shape[-1] and h.shape[-1] <= ops.GEMV_MAX_K:
+            act = ops.gemv(h.contiguous(), lw["gate_up"], swiglu=True)
+        else:
+            act = ops.silu_mul(self._linear(h, lw["gate_up"]))
+        return self._linear(act, lw["down"])
 
     def _rope_tables(self, positions: torch.Tensor):
         """fp32 cos/sin [L, head_dim] at integer positions [L] (NeoX layout)."""
@@ -155,7 +168,7 @@ class PagedDecoder:
                     else kv.attend_prefill(layer, q, scale=hd ** -0.5))
         o = self._linear(attn.transpose(1, 2).reshape(B, L, nq * hd), lw["o"])
         h = self._norm(x, lw["ln2"], o)
-        return self._linear(ops.silu_mul(self._linear(h, lw["gate_up"])), lw["down"])
+        return self._mlp(h, lw)
 
     # ---- model --------------------------------------------------------------
 

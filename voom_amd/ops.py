@@ -98,9 +98,9 @@ def _gqa_plan(q, k_pool, v_pool, block_table, ctx_lens, out, scale, num_splits, 
     if scale is None:
         scale = D ** -0.5
     if num_splits is None:
-        # Never more wavefronts than 32-token units can exist.
-        bound = max(1, B * NKV * max_pages * max(1, PT // 32))
-        num_splits = min(default_splits(), bound)
+        # the library's choice: short block tables take the one-launch segment
+        # kernel, longer ones split-K over the default number of wavefronts
+        num_splits = 0
     need = gqa_workspace_bytes(B, NQ, NKV, D, num_splits)
     if ws is None:
         ws = workspace(dev, need, tag=1)
@@ -455,6 +455,28 @@ def silu_mul(gate_up: torch.Tensor, stream: torch.cuda.Stream | None = None) -> 
     _lib.call("voom_silu_mul", _ptr(gate_up), _ptr(out), gate_up.numel() // (2 * inter), inter,
               _stream(stream))
     return out
+
+
+GEMV_MAX_K = 2048
+
+
+def gemv(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
+         stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """One-token projection: x [..., K] holding one row, weight [N, K] bf16 ->
+    y [..., N] = x . weight^T (fp32 sums, bf16 out).  swiglu: weight is the
+    fused [gate; up] [2I, K] and y [..., I] = bf16(silu(gate)) * up."""
+    dev = _require_device(x, weight)
+    _require(x.dtype == weight.dtype == torch.bfloat16, "bf16 x and weight")
+    _require(weight.dim() == 2 and x.shape[-1] == weight.shape[1], "weight [N, K] with K = x's")
+    _require(x.numel() == x.shape[-1], "gemv takes one row of activations")
+    K = weight.shape[1]
+    _require(K % 8 == 0 and K <= GEMV_MAX_K, f"K must be a multiple of 8 up to {GEMV_MAX_K}")
+    n = weight.shape[0] // 2 if swiglu else weight.shape[0]
+    _require(not swiglu or weight.shape[0] % 2 == 0, "swiglu weight rows must be even")
+    y = torch.empty((*x.shape[:-1], n), dtype=x.dtype, device=dev)
+    _lib.call("voom_gemv_bf16", _ptr(weight), _ptr(x), _ptr(y), n, K, int(swiglu),
+              _stream(stream))
+    return y
 
 
 def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
