@@ -242,6 +242,20 @@ int voom_silu_mul(const void* gate_up, void* out, int rows, int intermediate,
 int voom_gemv_bf16(const void* weight, const void* x, void* y, int n, int k, int swiglu,
                    hipStream_t stream);
 
+/* voom_qkv_rope_append: one decode token of one sequence through the fused
+ * qkv projection, RoPE and the page write -- voom_gemv_bf16 with w_qkv
+ * [(nq + 2 nkv) * head_dim, k], voom_rope_split with the fp32 rows cos_row /
+ * sin_row [head_dim] of the token's position, and voom_append_kv at
+ * *position (a device int) through table_row [max_pages], in one launch and
+ * bit-identical to the three in sequence (runtime/layer_runner.py:73-103 and
+ * the cache update at :158).  q [num_q_heads, head_dim] out; k and v into the
+ * pools (layouts of voom_append_kv).  head_dim a multiple of 4. */
+int voom_qkv_rope_append(const void* w_qkv, const void* x, const float* cos_row,
+                         const float* sin_row, void* q, void* k_pool, void* v_pool,
+                         const int32_t* table_row, const int32_t* position, int num_q_heads,
+                         int num_kv_heads, int head_dim, int k, int page_tokens, int max_pages,
+                         int num_slots, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Page writes and reads.
  *

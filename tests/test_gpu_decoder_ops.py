@@ -117,3 +117,34 @@ def test_gemv_rejects_unsupported_shapes():
     with pytest.raises(ValueError):
         ops.gemv(torch.zeros((12,), dtype=torch.bfloat16, device="cuda"),
                  torch.zeros((4, 12), dtype=torch.bfloat16, device="cuda"))  # K % 8
+
+
+@pytest.mark.parametrize("nq,nkv,hd,K,PT,pos", [(9, 3, 64, 576, 64, 100), (32, 8, 128, 2048, 32, 63),
+                                                (4, 4, 64, 520, 64, 0), (6, 2, 64, 576, 16, 47)])
+def test_qkv_rope_append_is_the_three_ops_bitwise(nq, nkv, hd, K, PT, pos):
+    # the fused decode-token path against gemv -> rope_split -> append_kv
+    from voom_amd.page_pool import v_slot_shape
+    print(f"[decoder-ops] qkv_rope_append nq={nq} nkv={nkv} hd={hd} K={K} PT={PT} pos={pos}",
+          flush=True)
+    g = torch.Generator(device="cuda").manual_seed(nq + hd + K + pos)
+    N = (nq + 2 * nkv) * hd
+    w = (torch.randn((N, K), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    x = torch.randn((1, 1, K), generator=g, device="cuda").to(torch.bfloat16)
+    inv = 1.0 / (10000.0 ** (torch.arange(hd // 2, device="cuda", dtype=torch.float32) / (hd // 2)))
+    ang = pos * inv
+    cos = torch.cat([ang.cos(), ang.cos()]).reshape(1, hd).contiguous()
+    sin = torch.cat([ang.sin(), ang.sin()]).reshape(1, hd).contiguous()
+    slots = 4
+    table = torch.tensor([[2, 0, 3, 1]], dtype=torch.int32, device="cuda")
+    position = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    kp = [torch.zeros((slots, nkv, PT, hd), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    vp = [torch.zeros((slots,) + v_slot_shape(nkv, hd, PT), dtype=torch.bfloat16, device="cuda")
+          for _ in range(2)]
+    q1 = ops.qkv_rope_append(x, w, cos, sin, kp[0], vp[0], table, position, nq, nkv, hd)
+    q2, k2, v2 = ops.rope_split(ops.gemv(x, w), cos, sin, nq, nkv, hd)
+    ops.append_kv(k2, v2, kp[1], vp[1], table, position)
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(kp[0].view(torch.int16), kp[1].view(torch.int16))
+    assert torch.equal(vp[0].view(torch.int16), vp[1].view(torch.int16))
+    assert bool(kp[0].abs().sum() > 0) and bool(vp[0].abs().sum() > 0)

@@ -169,27 +169,10 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(
 // bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections of rows r
 // and I + r -- the projection followed by silu_mul_kernel's math; a wave then
 // takes 2 gate and the 2 matching up rows.
-template <int KC, bool SWIGLU>
-__global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __restrict__ w,
-                                                          const uint16_t* __restrict__ x,
-                                                          uint16_t* __restrict__ y, int n, int k) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = blockIdx.x * (kRowThreads / kWave) + (threadIdx.x / kWave);
-  const int chunks = k / 8;
-  // rows of this wave: plain 4r..4r+3; SwiGLU gate 2r, 2r+1 and up n + 2r, n + 2r + 1
-  int rows[4];
-  if (SWIGLU) {
-    rows[0] = 2 * wave;
-    rows[1] = 2 * wave + 1;
-    rows[2] = n + 2 * wave;
-    rows[3] = n + 2 * wave + 1;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rows[i] = 4 * wave + i;
-  }
-  const int first = SWIGLU ? 2 * wave : 4 * wave;
-  if (first >= n) return;
-  float xv[KC][8];
+// x [k] into registers: lane holds chunks lane, lane + 64, ... as fp32.
+template <int KC>
+__device__ __forceinline__ void gemv_load_x(const uint16_t* __restrict__ x, int chunks, int lane,
+                                            float (&xv)[KC][8]) {
 #pragma unroll
   for (int j = 0; j < KC; ++j) {
     const int c = lane + kWave * j;
@@ -201,12 +184,18 @@ __global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __res
       xv[j][2 * e + 1] = bf2f(static_cast<uint16_t>(v[e] >> 16));
     }
   }
+}
+
+// Dot products of 4 weight rows with x, summed over the wave (every lane
+// gets the 4 sums).  All 4 x KC row loads are issued before the first use.
+template <int KC>
+__device__ __forceinline__ void gemv_dot4(const uint16_t* __restrict__ w, const int (&rows)[4],
+                                          int k, int chunks, int lane, const float (&xv)[KC][8],
+                                          float (&acc)[4]) {
   u32x4 wv[4][KC];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int local = SWIGLU ? (i & 1) : i;
-    const bool ok = first + local < n;
-    const uint16_t* wr = w + static_cast<size_t>(ok ? rows[i] : rows[0]) * k;
+    const uint16_t* wr = w + static_cast<size_t>(rows[i]) * k;
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
       const int c = lane + kWave * j;
@@ -214,7 +203,6 @@ __global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __res
                             : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  float acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float s = 0.f;
@@ -230,6 +218,30 @@ __global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __res
     for (int o = kWave / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o);
     acc[i] = s;
   }
+}
+
+template <int KC, bool SWIGLU>
+__global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, int n, int k) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * (kRowThreads / kWave) + (threadIdx.x / kWave);
+  const int chunks = k / 8;
+  // rows of this wave: plain 4r..4r+3; SwiGLU gate 2r, 2r+1 and up n + 2r, n + 2r + 1
+  // (rows past the end read row `first` again; their sums are not stored)
+  const int first = SWIGLU ? 2 * wave : 4 * wave;
+  if (first >= n) return;
+  int rows[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int local = SWIGLU ? (i & 1) : i;
+    const int r = first + local < n ? first + local : first;
+    rows[i] = SWIGLU && i >= 2 ? n + r : r;
+  }
+  float xv[KC][8];
+  gemv_load_x<KC>(x, chunks, lane, xv);
+  float acc[4];
+  gemv_dot4<KC>(w, rows, k, chunks, lane, xv, acc);
   if (lane == 0) {
     if (SWIGLU) {
 #pragma unroll
@@ -247,6 +259,81 @@ __global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __res
         if (first + i < n) y[first + i] = f2bf(acc[i]);
       }
     }
+  }
+}
+
+// The fused qkv projection of one decode token [(nq + 2 nkv) hd, k] . x, the
+// RoPE of its q and k heads and the page write of k and v: wave w of head h
+// takes rows d, d + 1, d + hd/2, d + hd/2 + 1 of the head (d = 2 (w % (hd/4))),
+// so both halves of each rotated pair are in the wave.  The projection is
+// rounded to bf16 before the rotation and the rotation rounds each product
+// and the sum (rope_split_kernel's formula), so q, k and v are bit-identical
+// to the projection, voom_rope_split and voom_append_kv in sequence.  k and v
+// land at position *pos of the sequence through its block-table row, in the
+// pool layouts of voom_append_kv.
+template <int KC>
+__global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, uint16_t* __restrict__ q,
+    uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    const int32_t* __restrict__ table_row, const int32_t* __restrict__ pos_ptr, int nq, int nkv,
+    int hd, int k, int pt_shift, int max_pages, int num_slots) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * (kRowThreads / kWave) + (threadIdx.x / kWave);
+  const int half = hd / 2;
+  const int per_head = half / 2;
+  const int h = wave / per_head;
+  if (h >= nq + 2 * nkv) return;
+  const int d = 2 * (wave - h * per_head);
+  const int chunks = k / 8;
+  const int rows[4] = {h * hd + d, h * hd + d + 1, h * hd + d + half, h * hd + d + half + 1};
+  float xv[KC][8];
+  gemv_load_x<KC>(x, chunks, lane, xv);
+  float acc[4];
+  gemv_dot4<KC>(w, rows, k, chunks, lane, xv, acc);
+  if (lane >= 2) return;
+  // lane e handles dims d + e and d + e + half
+  const float x1 = bf2f(f2bf(acc[lane]));
+  const float x2 = bf2f(f2bf(acc[2 + lane]));
+  const int i = d + lane;
+  uint16_t o1, o2;
+  if (h < nq + nkv) {
+#pragma clang fp contract(off)
+    const float a0 = x1 * cos_t[i];
+    const float b0 = -x2 * sin_t[i];
+    const float a1 = x2 * cos_t[i + half];
+    const float b1 = x1 * sin_t[i + half];
+    o1 = f2bf(a0 + b0);
+    o2 = f2bf(a1 + b1);
+  } else {
+    o1 = f2bf(x1);
+    o2 = f2bf(x2);
+  }
+  if (h < nq) {
+    q[static_cast<size_t>(h) * hd + i] = o1;
+    q[static_cast<size_t>(h) * hd + i + half] = o2;
+    return;
+  }
+  const int pos = *pos_ptr;
+  if (pos < 0) return;
+  const int page = pos >> pt_shift;
+  if (page >= max_pages) return;
+  const int slot = table_row[page];
+  if (static_cast<unsigned>(slot) >= static_cast<unsigned>(num_slots)) return;
+  const int off = pos & ((1 << pt_shift) - 1);
+  const bool is_k = h < nq + nkv;
+  const int kvh = is_k ? h - nq : h - nq - nkv;
+  const size_t head_page = static_cast<size_t>(slot) * nkv + kvh;
+  if (is_k) {
+    uint16_t* kr = k_pool + ((head_page << pt_shift) + off) * hd;
+    kr[i] = o1;
+    kr[i + half] = o2;
+  } else {
+    const int vb_shift = pt_shift < 5 ? pt_shift : 5;
+    const size_t blk = (head_page << (pt_shift - vb_shift)) + (off >> vb_shift);
+    const int col = off & ((1 << vb_shift) - 1);
+    v_pool[((blk * hd + i) << vb_shift) + col] = o1;
+    v_pool[((blk * hd + i + half) << vb_shift) + col] = o2;
   }
 }
 
@@ -270,6 +357,47 @@ int launch_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, int n, int k,
 }  // namespace voom
 
 using namespace voom;
+
+extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const float* cos_row,
+                                    const float* sin_row, void* q, void* k_pool, void* v_pool,
+                                    const int32_t* table_row, const int32_t* position,
+                                    int num_q_heads, int num_kv_heads, int head_dim, int k,
+                                    int page_tokens, int max_pages, int num_slots,
+                                    hipStream_t stream) {
+  const char* who = "qkv_rope_append";
+  VOOM_REQUIRE(w_qkv && x && cos_row && sin_row && q && k_pool && v_pool && table_row && position,
+               "%s: null pointer argument", who);
+  VOOM_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 4 == 0,
+               "%s: bad head geometry", who);
+  VOOM_REQUIRE(k > 0 && k % 8 == 0 && k <= 8 * kWave * 4,
+               "%s: k %d must be a positive multiple of 8 up to %d", who, k, 8 * kWave * 4);
+  VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens <= 4096 && max_pages > 0 && num_slots > 0,
+               "%s: bad page geometry", who);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w_qkv) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(x) % 16 == 0,
+               "%s: weight and x must be 16-byte aligned", who);
+  const long long waves = static_cast<long long>(num_q_heads + 2 * num_kv_heads) * (head_dim / 4);
+  const dim3 grid(static_cast<unsigned>((waves + kRowThreads / kWave - 1) / (kRowThreads / kWave)));
+  const int kc = (k / 8 + kWave - 1) / kWave;
+  const auto* wq = static_cast<const uint16_t*>(w_qkv);
+  const auto* xv = static_cast<const uint16_t*>(x);
+  auto* qo = static_cast<uint16_t*>(q);
+  auto* kp = static_cast<uint16_t*>(k_pool);
+  auto* vp = static_cast<uint16_t*>(v_pool);
+  const int pts = ilog2(page_tokens);
+#define VOOM_QRA(KC_)                                                                       \
+  hipLaunchKernelGGL((qkv_rope_append_kernel<KC_>), grid, dim3(kRowThreads), 0, stream, wq, xv, \
+                     cos_row, sin_row, qo, kp, vp, table_row, position, num_q_heads,            \
+                     num_kv_heads, head_dim, k, pts, max_pages, num_slots)
+  switch (kc) {
+    case 1: VOOM_QRA(1); break;
+    case 2: VOOM_QRA(2); break;
+    case 3: VOOM_QRA(3); break;
+    default: VOOM_QRA(4); break;
+  }
+#undef VOOM_QRA
+  return VOOM_LAUNCH_CHECK("qkv_rope_append: kernel launch");
+}
 
 extern "C" int voom_gemv_bf16(const void* weight, const void* x, void* y, int n, int k,
                               int swiglu, hipStream_t stream) {

@@ -380,22 +380,22 @@ __global__ __launch_bounds__(kThreads, WAVES_PER_EU) void gqa_decode_kernel(
   }
 }
 
-// Short contexts: one workgroup per (sequence, kv head) segment.  Its four
-// wavefronts take a quarter of the segment's 32-token blocks each with the
+// Short contexts: one workgroup per (sequence, kv head) segment.  Its SW
+// wavefronts take an equal share of the segment's 32-token blocks with the
 // partials kernel's block loop, leave their softmax states in LDS, and merge
 // them into the bf16 output (and LSE) themselves -- one launch and no
 // workspace, where the split-K pair of kernels costs two launches of
 // mostly fixed latency when a segment has only a few dozen blocks.
-template <int D, int NBUF>
-__global__ __launch_bounds__(kThreads) void gqa_segment_kernel(
+template <int D, int NBUF, int SW>
+__global__ __launch_bounds__(SW * kWave) void gqa_segment_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ ctx_lens, uint16_t* __restrict__ out,
     float* __restrict__ lse_out, int NKV, int G, int max_pages, int pt_shift, int num_slots,
     float scale_log2e) {
-  __shared__ float red_o[kWavesPerBlock][16][D];
-  __shared__ float red_m[kWavesPerBlock][16];
-  __shared__ float red_l[kWavesPerBlock][16];
+  __shared__ float red_o[SW][16][D];
+  __shared__ float red_m[SW][16];
+  __shared__ float red_l[SW][16];
   const int lane = threadIdx.x & (kWave - 1);
   const int wl = uniform(threadIdx.x / kWave);
   const int b = blockIdx.x / NKV;
@@ -405,8 +405,8 @@ __global__ __launch_bounds__(kThreads) void gqa_segment_kernel(
   int ctx = uniform(ctx_lens[b]);
   ctx = ctx < 0 ? 0 : (ctx > cap_tokens ? cap_tokens : ctx);
   const int nb = (ctx + kBlockTokens - 1) / kBlockTokens;
-  const int blo = wl * nb / kWavesPerBlock;
-  const int bhi = (wl + 1) * nb / kWavesPerBlock;
+  const int blo = wl * nb / SW;
+  const int bhi = (wl + 1) * nb / SW;
 
   const int i16 = lane & 15;
   const int g = lane >> 4;
@@ -472,12 +472,12 @@ __global__ __launch_bounds__(kThreads) void gqa_segment_kernel(
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < G * D; idx += SW * kWave) {
     const int h = idx / D;
     const int d = idx - h * D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) M = fmaxf(M, red_m[w][h]);
+    for (int w = 0; w < SW; ++w) M = fmaxf(M, red_m[w][h]);
     const size_t row = static_cast<size_t>(b) * NQ + kvh * G + h;
     if (M == -INFINITY) {  // no tokens
       out[row * D + d] = 0;
@@ -487,7 +487,7 @@ __global__ __launch_bounds__(kThreads) void gqa_segment_kernel(
     float L = 0.f;
     float o = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) {
+    for (int w = 0; w < SW; ++w) {
       const float mw = red_m[w][h];
       const float wt = mw == -INFINITY ? 0.f : fast_exp2(mw - M);
       L += red_l[w][h] * wt;
@@ -741,6 +741,11 @@ int launch_partials(const GqaPlan& p, const void* q, const void* k_pool, const v
 // segment kernel when the caller leaves the split count to the library
 // (32 blocks per wavefront at most).
 constexpr long long kSegmentKernelTokens = 4096;
+// Wavefronts per segment workgroup.
+#ifndef VOOM_GQA_SEGMENT_WAVES
+#define VOOM_GQA_SEGMENT_WAVES 4
+#endif
+constexpr int kSegmentWaves = VOOM_GQA_SEGMENT_WAVES;
 
 int launch_segments(const GqaPlan& p, const void* q, const void* k_pool, const void* v_pool,
                     const int32_t* block_table, const int32_t* ctx_lens, int num_slots,
@@ -751,13 +756,14 @@ int launch_segments(const GqaPlan& p, const void* q, const void* k_pool, const v
   const auto* kp = static_cast<const uint16_t*>(k_pool);
   const auto* vp = static_cast<const uint16_t*>(v_pool);
   auto* oo = static_cast<uint16_t*>(out);
+  constexpr int SW = kSegmentWaves;
   if (p.D == 128) {
-    hipLaunchKernelGGL((gqa_segment_kernel<128, kNbuf128>), grid, dim3(kThreads), 0, stream, qq,
-                       kp, vp, block_table, ctx_lens, oo, lse_out, p.NKV, p.G, p.max_pages,
+    hipLaunchKernelGGL((gqa_segment_kernel<128, kNbuf128, SW>), grid, dim3(SW * kWave), 0, stream,
+                       qq, kp, vp, block_table, ctx_lens, oo, lse_out, p.NKV, p.G, p.max_pages,
                        p.pt_shift, num_slots, scale_log2e);
   } else {
-    hipLaunchKernelGGL((gqa_segment_kernel<64, kNbuf64>), grid, dim3(kThreads), 0, stream, qq,
-                       kp, vp, block_table, ctx_lens, oo, lse_out, p.NKV, p.G, p.max_pages,
+    hipLaunchKernelGGL((gqa_segment_kernel<64, kNbuf64, SW>), grid, dim3(SW * kWave), 0, stream,
+                       qq, kp, vp, block_table, ctx_lens, oo, lse_out, p.NKV, p.G, p.max_pages,
                        p.pt_shift, num_slots, scale_log2e);
   }
   return VOOM_LAUNCH_CHECK("paged_gqa: segment kernel launch");

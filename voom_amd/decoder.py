@@ -158,11 +158,15 @@ class PagedDecoder:
         B, L, _ = x.shape
         nq, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         h = self._norm(x, lw["ln1"], delta)
-        q, k, v = ops.rope_split(self._linear(h, lw["qkv"]), cos, sin, nq, nkv, hd)
-        if graph:
+        if graph and B * L == 1 and h.shape[-1] <= ops.GEMV_MAX_K:
+            q = kv.project_append_at(layer, h, lw["qkv"], cos, sin, nq)
+            attn = kv.attend_at(layer, q, hd ** -0.5)
+        elif graph:
+            q, k, v = ops.rope_split(self._linear(h, lw["qkv"]), cos, sin, nq, nkv, hd)
             kv.append_at(layer, k, v)
             attn = kv.attend_at(layer, q, hd ** -0.5)
         else:
+            q, k, v = ops.rope_split(self._linear(h, lw["qkv"]), cos, sin, nq, nkv, hd)
             kv.append(layer, k, v)
             attn = (kv.attend(layer, q, scale=hd ** -0.5) if L == 1
                     else kv.attend_prefill(layer, q, scale=hd ** -0.5))

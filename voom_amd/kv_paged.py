@@ -524,6 +524,17 @@ class PagedKVCache:
         ops.append_kv(k.contiguous(), v.contiguous(), pool.k, pool.v, self._tables[layer],
                       self._pos_dev)
 
+    def project_append_at(self, layer: int, h: torch.Tensor, w_qkv: torch.Tensor,
+                          cos: torch.Tensor, sin: torch.Tensor, num_q_heads: int) -> torch.Tensor:
+        """One token of one sequence: the fused qkv projection of h, its RoPE
+        and the K/V write at the device position counter in one launch;
+        returns q [1, NQ, 1, D] (``append_at`` with the projection and rotation
+        folded in)."""
+        pool = self._pool(layer)
+        _, NKV, _, D = pool.k.shape
+        return ops.qkv_rope_append(h, w_qkv, cos, sin, pool.k, pool.v, self._tables[layer],
+                                   self._pos_dev, num_q_heads, NKV, D)
+
     def attend_at(self, layer: int, q: torch.Tensor, scale: float) -> torch.Tensor:
         """Decode attention of q [B, NQ, 1, D] over the device context counter
         (all pages resident, as ``reserve`` guarantees)."""

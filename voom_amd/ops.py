@@ -479,6 +479,35 @@ def gemv(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
     return y
 
 
+def qkv_rope_append(x: torch.Tensor, w_qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                    k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
+                    position: torch.Tensor, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                    *, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """One decode token of one sequence: q [1, nq, 1, hd] of the fused qkv
+    projection of x (one row of K), rotated with the fp32 rows cos/sin [.., hd]
+    of its position; k, v rotated/written into the pools at position[0]
+    (int32 device tensor) through block_table row 0.  Bit-identical to gemv,
+    rope_split and append_kv in sequence."""
+    dev = _require_device(x, w_qkv, cos, sin, k_pool, v_pool, block_table, position)
+    nq, nkv, hd = int(num_q_heads), int(num_kv_heads), int(head_dim)
+    K = w_qkv.shape[1]
+    _require(x.numel() == K == x.shape[-1], "x must be one row of the projection's K")
+    _require(w_qkv.shape[0] == (nq + 2 * nkv) * hd, "w_qkv rows must be (nq + 2 nkv) * hd")
+    _require(x.dtype == w_qkv.dtype == k_pool.dtype == v_pool.dtype == torch.bfloat16, "bf16")
+    _require(cos.dtype == sin.dtype == torch.float32 and cos.shape[-1] == sin.shape[-1] == hd,
+             "fp32 cos/sin rows of head_dim")
+    slots, NKVp, PT, Dp = k_pool.shape
+    _require(NKVp == nkv and Dp == hd, "pool geometry does not match the heads")
+    _check_v_pool(v_pool, slots, nkv, hd, PT)
+    _require(block_table.dtype == position.dtype == torch.int32 and block_table.dim() == 2,
+             "int32 block_table [B, max_pages] and position")
+    q = torch.empty((1, nq, 1, hd), dtype=x.dtype, device=dev)
+    _lib.call("voom_qkv_rope_append", _ptr(w_qkv), _ptr(x), _ptr(cos), _ptr(sin), _ptr(q),
+              _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(position), nq, nkv, hd, K, PT,
+              block_table.shape[1], slots, _stream(stream))
+    return q
+
+
 def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
     """kv_b_proj weight [H*(dn+dv), C] -> (W_UK [H, dn, C], W_UV^T [H, C, dv]), contiguous.
 
