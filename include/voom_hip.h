@@ -242,6 +242,20 @@ int voom_silu_mul(const void* gate_up, void* out, int rows, int intermediate,
 int voom_gemv_bf16(const void* weight, const void* x, void* y, int n, int k, int swiglu,
                    hipStream_t stream);
 
+/* voom_add_rms_norm_gemv: voom_add_rms_norm of one row followed by
+ * voom_gemv_bf16 on its output, in one launch: the projection's input is
+ * bf16(ln_weight * bf16(v * rsqrt(mean(v^2) + eps))) with v = bf16(x + delta)
+ * (v = x when delta is NULL), and v is stored to x_out when x_out is not NULL
+ * (x_out must not alias x or delta: the residual stream ping-pongs between two
+ * buffers instead of being updated in place).  Bit-identical to the two ops in
+ * sequence: every row statistic is summed in the same fixed order.  With
+ * ln_weight NULL (and delta, x_out NULL) it is voom_gemv_bf16.  The residual
+ * add and pre-norm of the dense block feeding its projections,
+ * runtime/layer_runner.py:338-344. */
+int voom_add_rms_norm_gemv(const void* x, const void* delta, const void* ln_weight, float eps,
+                           void* x_out, const void* weight, void* y, int n, int k, int swiglu,
+                           hipStream_t stream);
+
 /* voom_qkv_rope_append: one decode token of one sequence through the fused
  * qkv projection, RoPE and the page write -- voom_gemv_bf16 with w_qkv
  * [(nq + 2 nkv) * head_dim, k], voom_rope_split with the fp32 rows cos_row /
@@ -249,8 +263,11 @@ int voom_gemv_bf16(const void* weight, const void* x, void* y, int n, int k, int
  * *position (a device int) through table_row [max_pages], in one launch and
  * bit-identical to the three in sequence (runtime/layer_runner.py:73-103 and
  * the cache update at :158).  q [num_q_heads, head_dim] out; k and v into the
- * pools (layouts of voom_append_kv).  head_dim a multiple of 4. */
-int voom_qkv_rope_append(const void* w_qkv, const void* x, const float* cos_row,
+ * pools (layouts of voom_append_kv).  head_dim a multiple of 4.  delta,
+ * ln_weight, eps and x_out are the optional residual-add + RMSNorm prologue of
+ * voom_add_rms_norm_gemv (ln_weight NULL: x is the projection input). */
+int voom_qkv_rope_append(const void* w_qkv, const void* x, const void* delta,
+                         const void* ln_weight, float eps, void* x_out, const float* cos_row,
                          const float* sin_row, void* q, void* k_pool, void* v_pool,
                          const int32_t* table_row, const int32_t* position, int num_q_heads,
                          int num_kv_heads, int head_dim, int k, int page_tokens, int max_pages,

@@ -148,3 +148,70 @@ def test_qkv_rope_append_is_the_three_ops_bitwise(nq, nkv, hd, K, PT, pos):
     assert torch.equal(kp[0].view(torch.int16), kp[1].view(torch.int16))
     assert torch.equal(vp[0].view(torch.int16), vp[1].view(torch.int16))
     assert bool(kp[0].abs().sum() > 0) and bool(vp[0].abs().sum() > 0)
+
+
+@pytest.mark.parametrize("n,k,swiglu,with_delta", [(960, 576, False, True), (1536, 576, True, True),
+                                                   (7, 2048, False, False), (3, 1544, True, True),
+                                                   (130, 8, False, True), (49152, 576, False, True)])
+def test_norm_prologue_gemv_is_add_rms_norm_then_gemv_bitwise(n, k, swiglu, with_delta):
+    # the residual-add + RMSNorm folded into the projection against the two ops
+    print(f"[decoder-ops] norm gemv n={n} k={k} swiglu={swiglu} delta={with_delta}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(n + 3 * k + int(swiglu))
+    rows = 2 * n if swiglu else n
+    w = (torch.randn((rows, k), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    x = torch.randn((1, 1, k), generator=g, device="cuda").to(torch.bfloat16)
+    d = torch.randn((1, 1, k), generator=g, device="cuda").to(torch.bfloat16) if with_delta else None
+    ln = (1 + 0.1 * torch.randn((k,), generator=g, device="cuda")).to(torch.bfloat16)
+    x_before = x.clone()
+    x_out = torch.full_like(x, 7.0) if with_delta else None
+    got = ops.gemv(x, w, swiglu=swiglu, ln_weight=ln, eps=1e-5, delta=d, x_out=x_out)
+    resid = x.clone()
+    h = ops.add_rms_norm(resid, ln, 1e-5, delta=d)
+    ref = ops.gemv(h, w, swiglu=swiglu)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(x.view(torch.int16), x_before.view(torch.int16))   # input untouched
+    if with_delta:
+        assert torch.equal(x_out.view(torch.int16), resid.view(torch.int16))
+
+
+@pytest.mark.parametrize("nq,nkv,hd,K,PT,pos", [(9, 3, 64, 576, 64, 100), (32, 8, 128, 2048, 32, 63)])
+def test_qkv_rope_append_norm_prologue_is_add_rms_norm_first_bitwise(nq, nkv, hd, K, PT, pos):
+    from voom_amd.page_pool import v_slot_shape
+    print(f"[decoder-ops] norm qkv_rope_append nq={nq} hd={hd} K={K}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(nq * hd + K)
+    N = (nq + 2 * nkv) * hd
+    w = (torch.randn((N, K), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    x = torch.randn((1, 1, K), generator=g, device="cuda").to(torch.bfloat16)
+    d = torch.randn((1, 1, K), generator=g, device="cuda").to(torch.bfloat16)
+    ln = (1 + 0.1 * torch.randn((K,), generator=g, device="cuda")).to(torch.bfloat16)
+    ang = pos / (10000.0 ** (torch.arange(hd // 2, device="cuda", dtype=torch.float32) / (hd // 2)))
+    cos = torch.cat([ang.cos(), ang.cos()]).reshape(1, hd).contiguous()
+    sin = torch.cat([ang.sin(), ang.sin()]).reshape(1, hd).contiguous()
+    table = torch.tensor([[2, 0, 3, 1]], dtype=torch.int32, device="cuda")
+    position = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    kp = [torch.zeros((4, nkv, PT, hd), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    vp = [torch.zeros((4,) + v_slot_shape(nkv, hd, PT), dtype=torch.bfloat16, device="cuda")
+          for _ in range(2)]
+    x_out = torch.empty_like(x)
+    q1 = ops.qkv_rope_append(x, w, cos, sin, kp[0], vp[0], table, position, nq, nkv, hd,
+                             ln_weight=ln, eps=1e-5, delta=d, x_out=x_out)
+    resid = x.clone()
+    h = ops.add_rms_norm(resid, ln, 1e-5, delta=d)
+    q2 = ops.qkv_rope_append(h, w, cos, sin, kp[1], vp[1], table, position, nq, nkv, hd)
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(kp[0].view(torch.int16), kp[1].view(torch.int16))
+    assert torch.equal(vp[0].view(torch.int16), vp[1].view(torch.int16))
+    assert torch.equal(x_out.view(torch.int16), resid.view(torch.int16))
+
+
+def test_norm_prologue_rejects_aliased_residual_output():
+    x = torch.zeros((1, 1, 576), dtype=torch.bfloat16, device="cuda")
+    d = torch.zeros_like(x)
+    w = torch.zeros((4, 576), dtype=torch.bfloat16, device="cuda")
+    ln = torch.ones((576,), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        ops.gemv(x, w, ln_weight=ln, delta=d, x_out=x)
+    with pytest.raises(ValueError):
+        ops.gemv(x, w, delta=d)   # delta without ln_weight

@@ -49,8 +49,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_rope_split": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P]),
     "voom_silu_mul": (c_int, [_P, _P, c_int, c_int, _P]),
     "voom_gemv_bf16": (c_int, [_P, _P, _P, c_int, c_int, c_int, _P]),
-    "voom_qkv_rope_append": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int,
-                                     c_int, c_int, c_int, c_int, _P]),
+    "voom_qkv_rope_append": (c_int, [_P, _P, _P, _P, c_float, _P, _P, _P, _P, _P, _P, _P, _P,
+                                     c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
+    "voom_add_rms_norm_gemv": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int, c_int,
+                                       _P]),
     "voom_position_free_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "voom_position_free_attention": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_size_t,
                                              c_int, c_int, c_int, c_int, c_int, c_int, c_int,

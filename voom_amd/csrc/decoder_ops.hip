@@ -17,67 +17,83 @@ namespace {
 
 constexpr int kRowThreads = 256;
 
+// 16-byte chunk at col of bf16(x + delta) (of x alone without delta).
+__device__ __forceinline__ u32x4 add_chunk(const uint16_t* __restrict__ x,
+                                           const uint16_t* __restrict__ delta, int col) {
+  u32x4 a = *reinterpret_cast<const u32x4*>(x + col);
+  if (delta) {
+    const u32x4 d = *reinterpret_cast<const u32x4*>(delta + col);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = bf2f(static_cast<uint16_t>(a[w] & 0xffffu)) +
+                       bf2f(static_cast<uint16_t>(d[w] & 0xffffu));
+      const float hi = bf2f(static_cast<uint16_t>(a[w] >> 16)) +
+                       bf2f(static_cast<uint16_t>(d[w] >> 16));
+      a[w] = pack_bf16x2(lo, hi);
+    }
+  }
+  return a;
+}
+
+// Sum of squares of one chunk's 8 values added to ss, in element order with
+// explicit fused multiply-adds.  The row statistics of every kernel here are
+// built the same way -- lane l of one wavefront takes chunks l, l + 64, ...
+// in order, then the lanes are summed by xor shuffles 32, 16, ..., 1 (and
+// 1 / sqrt(ss / hidden + eps)) -- so a fused normalisation is bit-identical
+// to add_rms_norm_kernel's.
+__device__ __forceinline__ float chunk_sumsq(u32x4 a, float ss) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float lo = bf2f(static_cast<uint16_t>(a[w] & 0xffffu));
+    const float hi = bf2f(static_cast<uint16_t>(a[w] >> 16));
+    ss = __builtin_fmaf(lo, lo, ss);
+    ss = __builtin_fmaf(hi, hi, ss);
+  }
+  return ss;
+}
+__device__ __forceinline__ float rms_inv(float ss_lane, int hidden, float eps) {
+#pragma unroll
+  for (int o = kWave / 2; o >= 1; o >>= 1) ss_lane += __shfl_xor(ss_lane, o);
+  return 1.f / sqrtf(ss_lane / static_cast<float>(hidden) + eps);
+}
+// bf16(w * bf16(v * inv)) for one chunk, as packed bf16.
+__device__ __forceinline__ u32x4 norm_chunk(u32x4 a, u32x4 wv, float inv) {
+  u32x4 o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float n0 = bf2f(f2bf(bf2f(static_cast<uint16_t>(a[w] & 0xffffu)) * inv));
+    const float n1 = bf2f(f2bf(bf2f(static_cast<uint16_t>(a[w] >> 16)) * inv));
+    o[w] = pack_bf16x2(bf2f(static_cast<uint16_t>(wv[w] & 0xffffu)) * n0,
+                       bf2f(static_cast<uint16_t>(wv[w] >> 16)) * n1);
+  }
+  return o;
+}
+
 // One workgroup per row of `hidden` bf16 values (hidden % 8 == 0, <= 8192).
 // With delta, the row first becomes bf16(x + delta) and is written back.
+// Wavefront 0 computes the row statistics in the canonical order above.
 __global__ __launch_bounds__(kRowThreads) void add_rms_norm_kernel(
     uint16_t* __restrict__ x, const uint16_t* __restrict__ delta,
     const uint16_t* __restrict__ weight, uint16_t* __restrict__ out, int hidden, float eps) {
-  __shared__ float partial[kRowThreads / kWave];
+  __shared__ float s_inv;
   const size_t row = blockIdx.x;
   uint16_t* xr = x + row * hidden;
   const uint16_t* dr = delta ? delta + row * hidden : nullptr;
   uint16_t* orow = out + row * hidden;
-  constexpr int kMaxPer = 8192 / (kRowThreads * 8);  // 16-byte chunks per thread
-  float v[kMaxPer][8];
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < kMaxPer; ++c) {
-    const int col = (c * kRowThreads + threadIdx.x) * 8;
-    if (col < hidden) {
-      u32x4 a = *reinterpret_cast<const u32x4*>(xr + col);
-      if (dr) {
-        const u32x4 d = *reinterpret_cast<const u32x4*>(dr + col);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float lo = bf2f(static_cast<uint16_t>(a[w] & 0xffffu)) +
-                           bf2f(static_cast<uint16_t>(d[w] & 0xffffu));
-          const float hi = bf2f(static_cast<uint16_t>(a[w] >> 16)) +
-                           bf2f(static_cast<uint16_t>(d[w] >> 16));
-          a[w] = pack_bf16x2(lo, hi);
-        }
-        *reinterpret_cast<u32x4*>(xr + col) = a;
-      }
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        v[c][2 * w] = bf2f(static_cast<uint16_t>(a[w] & 0xffffu));
-        v[c][2 * w + 1] = bf2f(static_cast<uint16_t>(a[w] >> 16));
-        ss += v[c][2 * w] * v[c][2 * w] + v[c][2 * w + 1] * v[c][2 * w + 1];
-      }
-    }
+  const int chunks = hidden / 8;
+  if (threadIdx.x < kWave) {
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < chunks; c += kWave) ss = chunk_sumsq(add_chunk(xr, dr, 8 * c), ss);
+    const float inv = rms_inv(ss, hidden, eps);
+    if (threadIdx.x == 0) s_inv = inv;
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-  if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = ss;
-  __syncthreads();
-  float tot = 0.f;
-#pragma unroll
-  for (int k = 0; k < kRowThreads / kWave; ++k) tot += partial[k];
-  const float inv = 1.f / sqrtf(tot / static_cast<float>(hidden) + eps);
-#pragma unroll
-  for (int c = 0; c < kMaxPer; ++c) {
-    const int col = (c * kRowThreads + threadIdx.x) * 8;
-    if (col < hidden) {
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(weight + col);
-      u32x4 o;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float n0 = bf2f(f2bf(v[c][2 * w] * inv));
-        const float n1 = bf2f(f2bf(v[c][2 * w + 1] * inv));
-        o[w] = pack_bf16x2(bf2f(static_cast<uint16_t>(wv[w] & 0xffffu)) * n0,
-                           bf2f(static_cast<uint16_t>(wv[w] >> 16)) * n1);
-      }
-      *reinterpret_cast<u32x4*>(orow + col) = o;
-    }
+  __syncthreads();  // every read of the unmodified row is done
+  const float inv = s_inv;
+  for (int c = threadIdx.x; c < chunks; c += kRowThreads) {
+    const u32x4 a = add_chunk(xr, dr, 8 * c);
+    if (dr) *reinterpret_cast<u32x4*>(xr + 8 * c) = a;
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(weight + 8 * c);
+    *reinterpret_cast<u32x4*>(orow + 8 * c) = norm_chunk(a, wv, inv);
   }
 }
 
@@ -169,45 +185,116 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_kernel(
 // bf16(bf16(silu(g)) * u) with g, u the bf16-rounded projections of rows r
 // and I + r -- the projection followed by silu_mul_kernel's math; a wave then
 // takes 2 gate and the 2 matching up rows.
-// x [k] into registers: lane holds chunks lane, lane + 64, ... as fp32.
+// The projection input of one lane: chunks lane, lane + 64, ... of x (and of
+// delta and ln when the residual-add + RMSNorm prologue is on).  The raw
+// loads are issued first, then the weight loads, then the input is finished
+// while the weights are still in flight: the prologue costs no second memory
+// round trip.
 template <int KC>
-__device__ __forceinline__ void gemv_load_x(const uint16_t* __restrict__ x, int chunks, int lane,
-                                            float (&xv)[KC][8]) {
+struct GemvInput {
+  u32x4 x[KC], d[KC], ln[KC];
+};
+
+template <int KC, bool NORM>
+__device__ __forceinline__ void gemv_fetch_x(const uint16_t* __restrict__ x,
+                                             const uint16_t* __restrict__ delta,
+                                             const uint16_t* __restrict__ ln, int chunks, int lane,
+                                             GemvInput<KC>& in) {
+  // every lane loads (lanes past the row reread its last chunk and are
+  // masked later): straight-line loads let the compiler wait for exactly
+  // the ones it needs
+  const uint16_t* d = delta ? delta : x;
 #pragma unroll
   for (int j = 0; j < KC; ++j) {
-    const int c = lane + kWave * j;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (c < chunks) v = *reinterpret_cast<const u32x4*>(x + 8 * c);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xv[j][2 * e] = bf2f(static_cast<uint16_t>(v[e] & 0xffffu));
-      xv[j][2 * e + 1] = bf2f(static_cast<uint16_t>(v[e] >> 16));
+    const int c = min(lane + kWave * j, chunks - 1);
+    in.x[j] = *reinterpret_cast<const u32x4*>(x + 8 * c);
+    if (NORM) {
+      in.d[j] = *reinterpret_cast<const u32x4*>(d + 8 * c);
+      in.ln[j] = *reinterpret_cast<const u32x4*>(ln + 8 * c);
     }
   }
 }
 
-// Dot products of 4 weight rows with x, summed over the wave (every lane
-// gets the 4 sums).  All 4 x KC row loads are issued before the first use.
+// Plain (ln == nullptr): the input is x.  Otherwise it is add_rms_norm_kernel's
+// output, bit for bit: v = bf16(x + delta) (x without delta), input =
+// bf16(ln * bf16(v * rsqrt(mean(v^2) + eps))), with v also stored to x_out
+// (when given) by one wavefront of the grid.
+template <int KC, bool NORM>
+__device__ __forceinline__ void gemv_finish_x(const GemvInput<KC>& in, bool has_delta, float eps,
+                                              uint16_t* __restrict__ x_out, bool writer, int k,
+                                              int lane, float (&xv)[KC][8]) {
+  const int chunks = k / 8;
+  u32x4 v[KC];
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    v[j] = lane + kWave * j < chunks ? in.x[j] : u32x4{0u, 0u, 0u, 0u};
+    if (NORM) {
+      // the sum is formed either way and selected: a branch here lets the
+      // compiler sink the delta loads into it, behind a wait for the weights
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float lo = bf2f(static_cast<uint16_t>(v[j][w] & 0xffffu)) +
+                         bf2f(static_cast<uint16_t>(in.d[j][w] & 0xffffu));
+        const float hi = bf2f(static_cast<uint16_t>(v[j][w] >> 16)) +
+                         bf2f(static_cast<uint16_t>(in.d[j][w] >> 16));
+        const uint32_t sum = pack_bf16x2(lo, hi);
+        v[j][w] = has_delta ? sum : v[j][w];
+      }
+    }
+  }
+  if (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      if (lane + kWave * j < chunks) ss = chunk_sumsq(v[j], ss);
+    }
+    const float inv = rms_inv(ss, k, eps);
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      const int c = lane + kWave * j;
+      if (c < chunks) {
+        if (writer && x_out) *reinterpret_cast<u32x4*>(x_out + 8 * c) = v[j];
+        v[j] = norm_chunk(v[j], in.ln[j], inv);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xv[j][2 * e] = bf2f(static_cast<uint16_t>(v[j][e] & 0xffffu));
+      xv[j][2 * e + 1] = bf2f(static_cast<uint16_t>(v[j][e] >> 16));
+    }
+  }
+}
+
+// Loads of 4 weight rows (non-temporal: each weight byte is read once per
+// token).
 template <int KC>
-__device__ __forceinline__ void gemv_dot4(const uint16_t* __restrict__ w, const int (&rows)[4],
-                                          int k, int chunks, int lane, const float (&xv)[KC][8],
-                                          float (&acc)[4]) {
-  u32x4 wv[4][KC];
+__device__ __forceinline__ void gemv_fetch_w(const uint16_t* __restrict__ w, const int (&rows)[4],
+                                             int k, int chunks, int lane, u32x4 (&wv)[4][KC]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint16_t* wr = w + static_cast<size_t>(rows[i]) * k;
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
-      const int c = lane + kWave * j;
-      wv[i][j] = c < chunks ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 8 * c))
-                            : u32x4{0u, 0u, 0u, 0u};
+      const int c = min(lane + kWave * j, chunks - 1);  // see gemv_fetch_x
+      wv[i][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + 8 * c));
     }
   }
+}
+
+// Dot products of the 4 weight rows with x, summed over the wave (every lane
+// gets the 4 sums); chunks past the row (lane + 64 j >= chunks) add nothing.
+template <int KC>
+__device__ __forceinline__ void gemv_dot4(const u32x4 (&wv)[4][KC], const float (&xv)[KC][8],
+                                          int chunks, int lane, float (&acc)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
+      if (lane + kWave * j >= chunks) continue;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         s += bf2f(static_cast<uint16_t>(wv[i][j][e] & 0xffffu)) * xv[j][2 * e];
@@ -220,13 +307,33 @@ __device__ __forceinline__ void gemv_dot4(const uint16_t* __restrict__ w, const 
   }
 }
 
-template <int KC, bool SWIGLU>
-__global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __restrict__ w,
-                                                          const uint16_t* __restrict__ x,
-                                                          uint16_t* __restrict__ y, int n, int k) {
+// One wavefront's projection of rows[0..3]: input fetch, weight fetch, input
+// finish, dot products.
+template <int KC, bool NORM>
+__device__ __forceinline__ void gemv_rows(const uint16_t* __restrict__ w,
+                                          const uint16_t* __restrict__ x,
+                                          const uint16_t* __restrict__ delta,
+                                          const uint16_t* __restrict__ ln, float eps,
+                                          uint16_t* __restrict__ x_out, bool writer,
+                                          const int (&rows)[4], int k, int lane,
+                                          float (&acc)[4]) {
+  const int chunks = k / 8;
+  GemvInput<KC> in;
+  gemv_fetch_x<KC, NORM>(x, delta, ln, chunks, lane, in);
+  u32x4 wv[4][KC];
+  gemv_fetch_w<KC>(w, rows, k, chunks, lane, wv);
+  float xv[KC][8];
+  gemv_finish_x<KC, NORM>(in, delta != nullptr, eps, x_out, writer, k, lane, xv);
+  gemv_dot4<KC>(wv, xv, chunks, lane, acc);
+}
+
+template <int KC, bool SWIGLU, bool NORM>
+__global__ __launch_bounds__(kRowThreads) void gemv_kernel(
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+    const uint16_t* __restrict__ delta, const uint16_t* __restrict__ ln, float eps,
+    uint16_t* __restrict__ x_out, uint16_t* __restrict__ y, int n, int k) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = blockIdx.x * (kRowThreads / kWave) + (threadIdx.x / kWave);
-  const int chunks = k / 8;
   // rows of this wave: plain 4r..4r+3; SwiGLU gate 2r, 2r+1 and up n + 2r, n + 2r + 1
   // (rows past the end read row `first` again; their sums are not stored)
   const int first = SWIGLU ? 2 * wave : 4 * wave;
@@ -238,10 +345,8 @@ __global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __res
     const int r = first + local < n ? first + local : first;
     rows[i] = SWIGLU && i >= 2 ? n + r : r;
   }
-  float xv[KC][8];
-  gemv_load_x<KC>(x, chunks, lane, xv);
   float acc[4];
-  gemv_dot4<KC>(w, rows, k, chunks, lane, xv, acc);
+  gemv_rows<KC, NORM>(w, x, delta, ln, eps, x_out, wave == 0, rows, k, lane, acc);
   if (lane == 0) {
     if (SWIGLU) {
 #pragma unroll
@@ -271,9 +376,11 @@ __global__ __launch_bounds__(kRowThreads) void gemv_kernel(const uint16_t* __res
 // to the projection, voom_rope_split and voom_append_kv in sequence.  k and v
 // land at position *pos of the sequence through its block-table row, in the
 // pool layouts of voom_append_kv.
-template <int KC>
+template <int KC, bool NORM>
 __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+    const uint16_t* __restrict__ delta, const uint16_t* __restrict__ ln, float eps,
+    uint16_t* __restrict__ x_out,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, uint16_t* __restrict__ q,
     uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
     const int32_t* __restrict__ table_row, const int32_t* __restrict__ pos_ptr, int nq, int nkv,
@@ -285,12 +392,9 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
   const int h = wave / per_head;
   if (h >= nq + 2 * nkv) return;
   const int d = 2 * (wave - h * per_head);
-  const int chunks = k / 8;
   const int rows[4] = {h * hd + d, h * hd + d + 1, h * hd + d + half, h * hd + d + half + 1};
-  float xv[KC][8];
-  gemv_load_x<KC>(x, chunks, lane, xv);
   float acc[4];
-  gemv_dot4<KC>(w, rows, k, chunks, lane, xv, acc);
+  gemv_rows<KC, NORM>(w, x, delta, ln, eps, x_out, wave == 0, rows, k, lane, acc);
   if (lane >= 2) return;
   // lane e handles dims d + e and d + e + half
   const float x1 = bf2f(f2bf(acc[lane]));
@@ -337,19 +441,33 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
   }
 }
 
+template <bool SWIGLU, bool NORM>
+void launch_gemv_kc(int kc, dim3 grid, const uint16_t* w, const uint16_t* x, const uint16_t* delta,
+                    const uint16_t* ln, float eps, uint16_t* x_out, uint16_t* y, int n, int k,
+                    hipStream_t stream) {
+#define VOOM_GEMV(KC_)                                                                       \
+  hipLaunchKernelGGL((gemv_kernel<KC_, SWIGLU, NORM>), grid, dim3(kRowThreads), 0, stream, w, x, \
+                     delta, ln, eps, x_out, y, n, k)
+  switch (kc) {
+    case 1: VOOM_GEMV(1); break;
+    case 2: VOOM_GEMV(2); break;
+    case 3: VOOM_GEMV(3); break;
+    default: VOOM_GEMV(4); break;
+  }
+#undef VOOM_GEMV
+}
+
 template <bool SWIGLU>
-int launch_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, int n, int k,
-                hipStream_t stream) {
+int launch_gemv(const uint16_t* w, const uint16_t* x, const uint16_t* delta, const uint16_t* ln,
+                float eps, uint16_t* x_out, uint16_t* y, int n, int k, hipStream_t stream) {
   const int rows_per_wave = SWIGLU ? 2 : 4;
   const long long waves = (static_cast<long long>(n) + rows_per_wave - 1) / rows_per_wave;
   const dim3 grid(static_cast<unsigned>((waves + kRowThreads / kWave - 1) / (kRowThreads / kWave)));
   const int kc = (k / 8 + kWave - 1) / kWave;
-  switch (kc) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<1, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<2, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
-    case 3: hipLaunchKernelGGL((gemv_kernel<3, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
-    default: hipLaunchKernelGGL((gemv_kernel<4, SWIGLU>), grid, dim3(kRowThreads), 0, stream, w, x, y, n, k); break;
-  }
+  if (ln)
+    launch_gemv_kc<SWIGLU, true>(kc, grid, w, x, delta, ln, eps, x_out, y, n, k, stream);
+  else
+    launch_gemv_kc<SWIGLU, false>(kc, grid, w, x, delta, ln, eps, x_out, y, n, k, stream);
   return VOOM_LAUNCH_CHECK("gemv: kernel launch");
 }
 
@@ -358,15 +476,33 @@ int launch_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, int n, int k,
 
 using namespace voom;
 
-extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const float* cos_row,
-                                    const float* sin_row, void* q, void* k_pool, void* v_pool,
-                                    const int32_t* table_row, const int32_t* position,
-                                    int num_q_heads, int num_kv_heads, int head_dim, int k,
-                                    int page_tokens, int max_pages, int num_slots,
-                                    hipStream_t stream) {
+namespace {
+// Shared checks of the residual-add + RMSNorm prologue arguments.
+int check_norm_prologue(const char* who, const void* x, const void* delta, const void* ln_weight,
+                        const void* x_out) {
+  VOOM_REQUIRE(ln_weight != nullptr || (delta == nullptr && x_out == nullptr),
+               "%s: delta and x_out need ln_weight", who);
+  VOOM_REQUIRE(x_out == nullptr || (x_out != x && x_out != delta),
+               "%s: x_out must not alias x or delta", who);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(delta) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(ln_weight) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(x_out) % 16 == 0,
+               "%s: delta, ln_weight and x_out must be 16-byte aligned", who);
+  return 0;
+}
+}  // namespace
+
+extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const void* delta,
+                                    const void* ln_weight, float eps, void* x_out,
+                                    const float* cos_row, const float* sin_row, void* q,
+                                    void* k_pool, void* v_pool, const int32_t* table_row,
+                                    const int32_t* position, int num_q_heads, int num_kv_heads,
+                                    int head_dim, int k, int page_tokens, int max_pages,
+                                    int num_slots, hipStream_t stream) {
   const char* who = "qkv_rope_append";
   VOOM_REQUIRE(w_qkv && x && cos_row && sin_row && q && k_pool && v_pool && table_row && position,
                "%s: null pointer argument", who);
+  if (int rc = check_norm_prologue(who, x, delta, ln_weight, x_out)) return rc;
   VOOM_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 4 == 0,
                "%s: bad head geometry", who);
   VOOM_REQUIRE(k > 0 && k % 8 == 0 && k <= 8 * kWave * 4,
@@ -384,11 +520,20 @@ extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const floa
   auto* qo = static_cast<uint16_t*>(q);
   auto* kp = static_cast<uint16_t*>(k_pool);
   auto* vp = static_cast<uint16_t*>(v_pool);
+  const auto* dv = static_cast<const uint16_t*>(delta);
+  const auto* lw = static_cast<const uint16_t*>(ln_weight);
+  auto* xo = static_cast<uint16_t*>(x_out);
   const int pts = ilog2(page_tokens);
-#define VOOM_QRA(KC_)                                                                       \
-  hipLaunchKernelGGL((qkv_rope_append_kernel<KC_>), grid, dim3(kRowThreads), 0, stream, wq, xv, \
-                     cos_row, sin_row, qo, kp, vp, table_row, position, num_q_heads,            \
-                     num_kv_heads, head_dim, k, pts, max_pages, num_slots)
+#define VOOM_QRA_N(KC_, NORM_)                                                             \
+  hipLaunchKernelGGL((qkv_rope_append_kernel<KC_, NORM_>), grid, dim3(kRowThreads), 0, stream, \
+                     wq, xv, dv, lw, eps, xo, cos_row, sin_row, qo, kp, vp, table_row,         \
+                     position, num_q_heads, num_kv_heads, head_dim, k, pts, max_pages,         \
+                     num_slots)
+#define VOOM_QRA(KC_)      \
+  if (lw)                  \
+    VOOM_QRA_N(KC_, true); \
+  else                     \
+    VOOM_QRA_N(KC_, false)
   switch (kc) {
     case 1: VOOM_QRA(1); break;
     case 2: VOOM_QRA(2); break;
@@ -396,13 +541,22 @@ extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const floa
     default: VOOM_QRA(4); break;
   }
 #undef VOOM_QRA
+#undef VOOM_QRA_N
   return VOOM_LAUNCH_CHECK("qkv_rope_append: kernel launch");
 }
 
 extern "C" int voom_gemv_bf16(const void* weight, const void* x, void* y, int n, int k,
                               int swiglu, hipStream_t stream) {
+  return voom_add_rms_norm_gemv(x, nullptr, nullptr, 0.f, nullptr, weight, y, n, k, swiglu,
+                                stream);
+}
+
+extern "C" int voom_add_rms_norm_gemv(const void* x, const void* delta, const void* ln_weight,
+                                      float eps, void* x_out, const void* weight, void* y, int n,
+                                      int k, int swiglu, hipStream_t stream) {
   const char* who = "gemv_bf16";
   VOOM_REQUIRE(weight && x && y, "%s: null pointer argument", who);
+  if (int rc = check_norm_prologue(who, x, delta, ln_weight, x_out)) return rc;
   VOOM_REQUIRE(n > 0 && k > 0 && k % 8 == 0 && k <= 8 * kWave * 4,
                "%s: k %d must be a positive multiple of 8 up to %d", who, k, 8 * kWave * 4);
   VOOM_REQUIRE(n < (1 << 28), "%s: n %d too large", who, n);
@@ -413,8 +567,11 @@ extern "C" int voom_gemv_bf16(const void* weight, const void* x, void* y, int n,
   const auto* w = static_cast<const uint16_t*>(weight);
   const auto* xv = static_cast<const uint16_t*>(x);
   auto* yv = static_cast<uint16_t*>(y);
-  return swiglu ? launch_gemv<true>(w, xv, yv, n, k, stream)
-                : launch_gemv<false>(w, xv, yv, n, k, stream);
+  const auto* dv = static_cast<const uint16_t*>(delta);
+  const auto* lw = static_cast<const uint16_t*>(ln_weight);
+  auto* xo = static_cast<uint16_t*>(x_out);
+  return swiglu ? launch_gemv<true>(w, xv, dv, lw, eps, xo, yv, n, k, stream)
+                : launch_gemv<false>(w, xv, dv, lw, eps, xo, yv, n, k, stream);
 }
 
 extern "C" int voom_add_rms_norm(void* x, const void* delta, const void* weight, void* out,

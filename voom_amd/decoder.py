@@ -147,6 +147,31 @@ class PagedDecoder:
         return (torch.cat([ang.cos(), ang.cos()], -1).contiguous(),
                 torch.cat([ang.sin(), ang.sin()], -1).contiguous())
 
+    def _block_token(self, x: torch.Tensor, spare: torch.Tensor, delta: torch.Tensor | None,
+                     layer: int, kv: PagedKVCache, cos: torch.Tensor, sin: torch.Tensor):
+        """``_block`` for one token of one sequence in a captured step, with
+        each residual add and RMSNorm folded into the projection that consumes
+        it.  The residual stream moves between two buffers instead of being
+        updated in place: x holds it before the layer (before adding
+        ``delta``), a fused launch reads one buffer and writes the sum to the
+        other.  Returns (the MLP output = the next layer's delta, the buffer
+        holding the stream, the spare buffer)."""
+        cfg = self.cfg
+        lw = self.layers[layer]
+        nq, hd, eps = cfg.num_attention_heads, cfg.head_dim, cfg.rms_norm_eps
+        if delta is None:
+            q = kv.project_append_at(layer, x, lw["qkv"], cos, sin, nq, ln_weight=lw["ln1"],
+                                     eps=eps)
+        else:
+            q = kv.project_append_at(layer, x, lw["qkv"], cos, sin, nq, ln_weight=lw["ln1"],
+                                     eps=eps, delta=delta, x_out=spare)
+            x, spare = spare, x
+        attn = kv.attend_at(layer, q, hd ** -0.5)
+        o = ops.gemv(attn.reshape(1, 1, nq * hd), lw["o"])
+        act = ops.gemv(x, lw["gate_up"], swiglu=True, ln_weight=lw["ln2"], eps=eps, delta=o,
+                       x_out=spare)
+        return ops.gemv(act, lw["down"]), spare, x
+
     def _block(self, x: torch.Tensor, delta: torch.Tensor | None, layer: int,
                kv: PagedKVCache, cos: torch.Tensor, sin: torch.Tensor,
                graph: bool = False) -> torch.Tensor:
@@ -158,10 +183,7 @@ class PagedDecoder:
         B, L, _ = x.shape
         nq, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
         h = self._norm(x, lw["ln1"], delta)
-        if graph and B * L == 1 and h.shape[-1] <= ops.GEMV_MAX_K:
-            q = kv.project_append_at(layer, h, lw["qkv"], cos, sin, nq)
-            attn = kv.attend_at(layer, q, hd ** -0.5)
-        elif graph:
+        if graph:
             q, k, v = ops.rope_split(self._linear(h, lw["qkv"]), cos, sin, nq, nkv, hd)
             kv.append_at(layer, k, v)
             attn = kv.attend_at(layer, q, hd ** -0.5)
@@ -209,8 +231,15 @@ class PagedDecoder:
         cos, sin = self._rope_tables(kv._pos_dev[:1])
         x = self.embed[tok]
         delta = None
-        for layer in range(self.cfg.num_hidden_layers):
-            delta = self._block(x, delta, layer, kv, cos, sin, graph=True)
+        cfg = self.cfg
+        if B == 1 and max(cfg.hidden_size, cfg.intermediate_size,
+                          cfg.num_attention_heads * cfg.head_dim) <= ops.GEMV_MAX_K:
+            spare = torch.empty_like(x)
+            for layer in range(cfg.num_hidden_layers):
+                delta, x, spare = self._block_token(x, spare, delta, layer, kv, cos, sin)
+        else:
+            for layer in range(self.cfg.num_hidden_layers):
+                delta = self._block(x, delta, layer, kv, cos, sin, graph=True)
         x = self._norm(x, self.final_norm, delta)
         logits = self._linear(x, self.embed).float()
         nxt.copy_(logits[:, -1].argmax(-1))

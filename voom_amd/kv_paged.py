@@ -525,15 +525,17 @@ class PagedKVCache:
                       self._pos_dev)
 
     def project_append_at(self, layer: int, h: torch.Tensor, w_qkv: torch.Tensor,
-                          cos: torch.Tensor, sin: torch.Tensor, num_q_heads: int) -> torch.Tensor:
+                          cos: torch.Tensor, sin: torch.Tensor, num_q_heads: int,
+                          **norm) -> torch.Tensor:
         """One token of one sequence: the fused qkv projection of h, its RoPE
         and the K/V write at the device position counter in one launch;
         returns q [1, NQ, 1, D] (``append_at`` with the projection and rotation
-        folded in)."""
+        folded in).  ``norm`` (ln_weight, eps, delta, x_out) puts the
+        residual-add + RMSNorm of h in front, as in ``ops.qkv_rope_append``."""
         pool = self._pool(layer)
         _, NKV, _, D = pool.k.shape
         return ops.qkv_rope_append(h, w_qkv, cos, sin, pool.k, pool.v, self._tables[layer],
-                                   self._pos_dev, num_q_heads, NKV, D)
+                                   self._pos_dev, num_q_heads, NKV, D, **norm)
 
     def attend_at(self, layer: int, q: torch.Tensor, scale: float) -> torch.Tensor:
         """Decode attention of q [B, NQ, 1, D] over the device context counter

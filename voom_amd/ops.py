@@ -460,13 +460,36 @@ def silu_mul(gate_up: torch.Tensor, stream: torch.cuda.Stream | None = None) -> 
 GEMV_MAX_K = 2048
 
 
+def _norm_prologue(x: torch.Tensor, ln_weight, delta, x_out):
+    """Checks of the optional residual-add + RMSNorm prologue arguments."""
+    if ln_weight is None:
+        _require(delta is None and x_out is None, "delta and x_out need ln_weight")
+        return
+    _require(ln_weight.dtype == torch.bfloat16 and tuple(ln_weight.shape) == (x.shape[-1],),
+             "ln_weight bf16 [K]")
+    for t, name in ((delta, "delta"), (x_out, "x_out")):
+        _require(t is None or (t.shape == x.shape and t.dtype == x.dtype and t.is_contiguous()),
+                 f"{name} like x")
+    _require(x_out is None or (x_out.data_ptr() != x.data_ptr() and
+                               (delta is None or x_out.data_ptr() != delta.data_ptr())),
+             "x_out must not alias x or delta")
+
+
 def gemv(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
+         ln_weight: torch.Tensor | None = None, eps: float = 1e-5,
+         delta: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
          stream: torch.cuda.Stream | None = None) -> torch.Tensor:
     """One-token projection: x [..., K] holding one row, weight [N, K] bf16 ->
     y [..., N] = x . weight^T (fp32 sums, bf16 out).  swiglu: weight is the
-    fused [gate; up] [2I, K] and y [..., I] = bf16(silu(gate)) * up."""
-    dev = _require_device(x, weight)
+    fused [gate; up] [2I, K] and y [..., I] = bf16(silu(gate)) * up.
+
+    With ln_weight the projection's input is add_rms_norm's output instead:
+    v = x + delta (x alone without delta) normed with ln_weight and eps, and
+    v is written to x_out (when given; a buffer other than x and delta).
+    Bit-identical to add_rms_norm followed by the projection."""
+    dev = _require_device(x, weight, ln_weight, delta, x_out)
     _require(x.dtype == weight.dtype == torch.bfloat16, "bf16 x and weight")
+    _norm_prologue(x, ln_weight, delta, x_out)
     _require(weight.dim() == 2 and x.shape[-1] == weight.shape[1], "weight [N, K] with K = x's")
     _require(x.numel() == x.shape[-1], "gemv takes one row of activations")
     K = weight.shape[1]
@@ -474,21 +497,26 @@ def gemv(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
     n = weight.shape[0] // 2 if swiglu else weight.shape[0]
     _require(not swiglu or weight.shape[0] % 2 == 0, "swiglu weight rows must be even")
     y = torch.empty((*x.shape[:-1], n), dtype=x.dtype, device=dev)
-    _lib.call("voom_gemv_bf16", _ptr(weight), _ptr(x), _ptr(y), n, K, int(swiglu),
-              _stream(stream))
+    _lib.call("voom_add_rms_norm_gemv", _ptr(x), _ptr(delta), _ptr(ln_weight), float(eps),
+              _ptr(x_out), _ptr(weight), _ptr(y), n, K, int(swiglu), _stream(stream))
     return y
 
 
 def qkv_rope_append(x: torch.Tensor, w_qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                     k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
                     position: torch.Tensor, num_q_heads: int, num_kv_heads: int, head_dim: int,
-                    *, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+                    *, ln_weight: torch.Tensor | None = None, eps: float = 1e-5,
+                    delta: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
+                    stream: torch.cuda.Stream | None = None) -> torch.Tensor:
     """One decode token of one sequence: q [1, nq, 1, hd] of the fused qkv
     projection of x (one row of K), rotated with the fp32 rows cos/sin [.., hd]
     of its position; k, v rotated/written into the pools at position[0]
     (int32 device tensor) through block_table row 0.  Bit-identical to gemv,
-    rope_split and append_kv in sequence."""
-    dev = _require_device(x, w_qkv, cos, sin, k_pool, v_pool, block_table, position)
+    rope_split and append_kv in sequence.  ln_weight, eps, delta, x_out: the
+    residual-add + RMSNorm prologue of ``gemv``."""
+    dev = _require_device(x, w_qkv, cos, sin, k_pool, v_pool, block_table, position,
+                          ln_weight, delta, x_out)
+    _norm_prologue(x, ln_weight, delta, x_out)
     nq, nkv, hd = int(num_q_heads), int(num_kv_heads), int(head_dim)
     K = w_qkv.shape[1]
     _require(x.numel() == K == x.shape[-1], "x must be one row of the projection's K")
@@ -502,7 +530,8 @@ def qkv_rope_append(x: torch.Tensor, w_qkv: torch.Tensor, cos: torch.Tensor, sin
     _require(block_table.dtype == position.dtype == torch.int32 and block_table.dim() == 2,
              "int32 block_table [B, max_pages] and position")
     q = torch.empty((1, nq, 1, hd), dtype=x.dtype, device=dev)
-    _lib.call("voom_qkv_rope_append", _ptr(w_qkv), _ptr(x), _ptr(cos), _ptr(sin), _ptr(q),
+    _lib.call("voom_qkv_rope_append", _ptr(w_qkv), _ptr(x), _ptr(delta), _ptr(ln_weight),
+              float(eps), _ptr(x_out), _ptr(cos), _ptr(sin), _ptr(q),
               _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(position), nq, nkv, hd, K, PT,
               block_table.shape[1], slots, _stream(stream))
     return q
