@@ -44,6 +44,29 @@ __device__ __forceinline__ float wave_sum_across_groups(float v) {
   return v;
 }
 
+// Sum over the 64 lanes, the same value in every lane, in a fixed order:
+// xor 1 and xor 2 within each quad, then the mirrored half of each 8-lane
+// group, then the mirrored half of each 16-lane row (all DPP moves, after
+// which every lane of a row holds the row's sum), then rows 0 + 16 + 32 + 48
+// read out left to right.  Cheaper than a shuffle butterfly, whose six steps
+// each round-trip through the LDS crossbar.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return ((r0 + r1) + r2) + r3;
+}
+
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {

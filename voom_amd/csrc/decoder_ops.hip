@@ -38,7 +38,7 @@ __device__ __forceinline__ u32x4 add_chunk(const uint16_t* __restrict__ x,
 // Sum of squares of one chunk's 8 values added to ss, in element order with
 // explicit fused multiply-adds.  The row statistics of every kernel here are
 // built the same way -- lane l of one wavefront takes chunks l, l + 64, ...
-// in order, then the lanes are summed by xor shuffles 32, 16, ..., 1 (and
+// in order, then the lanes are summed by wave_sum_uniform (and
 // 1 / sqrt(ss / hidden + eps)) -- so a fused normalisation is bit-identical
 // to add_rms_norm_kernel's.
 __device__ __forceinline__ float chunk_sumsq(u32x4 a, float ss) {
@@ -52,9 +52,8 @@ __device__ __forceinline__ float chunk_sumsq(u32x4 a, float ss) {
   return ss;
 }
 __device__ __forceinline__ float rms_inv(float ss_lane, int hidden, float eps) {
-#pragma unroll
-  for (int o = kWave / 2; o >= 1; o >>= 1) ss_lane += __shfl_xor(ss_lane, o);
-  return 1.f / sqrtf(ss_lane / static_cast<float>(hidden) + eps);
+  const float ss = wave_sum_uniform(ss_lane);
+  return 1.f / sqrtf(ss / static_cast<float>(hidden) + eps);
 }
 // bf16(w * bf16(v * inv)) for one chunk, as packed bf16.
 __device__ __forceinline__ u32x4 norm_chunk(u32x4 a, u32x4 wv, float inv) {
@@ -301,9 +300,7 @@ __device__ __forceinline__ void gemv_dot4(const u32x4 (&wv)[4][KC], const float 
         s += bf2f(static_cast<uint16_t>(wv[i][j][e] >> 16)) * xv[j][2 * e + 1];
       }
     }
-#pragma unroll
-    for (int o = kWave / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o);
-    acc[i] = s;
+    acc[i] = wave_sum_uniform(s);
   }
 }
 
