@@ -256,6 +256,18 @@ int voom_add_rms_norm_gemv(const void* x, const void* delta, const void* ln_weig
                            void* x_out, const void* weight, void* y, int n, int k, int swiglu,
                            hipStream_t stream);
 
+/* voom_lm_head_argmax: greedy next token of one row -- the index of the
+ * largest bf16 logit of weight [n, k] . h (the lowest index among equal
+ * logits; -0 equals +0, NaN is largest, as torch.argmax), written to
+ * token[0] and, when not NULL, token_copy[0] (int64).  h is x itself, or,
+ * with ln_weight, the residual-add + RMSNorm of voom_add_rms_norm_gemv (the
+ * final norm).  The logits are not stored.  workspace holds one 8-byte key
+ * per 16 vocabulary rows.  The final norm, lm_head and greedy sample of the
+ * decode loop, runtime/engine.py:8471-8479 (argmax at :6446). */
+int voom_lm_head_argmax(const void* x, const void* delta, const void* ln_weight, float eps,
+                        const void* weight, int n, int k, void* workspace, size_t ws_bytes,
+                        int64_t* token, int64_t* token_copy, hipStream_t stream);
+
 /* voom_qkv_rope_append: one decode token of one sequence through the fused
  * qkv projection, RoPE and the page write -- voom_gemv_bf16 with w_qkv
  * [(nq + 2 nkv) * head_dim, k], voom_rope_split with the fp32 rows cos_row /
@@ -265,13 +277,16 @@ int voom_add_rms_norm_gemv(const void* x, const void* delta, const void* ln_weig
  * the cache update at :158).  q [num_q_heads, head_dim] out; k and v into the
  * pools (layouts of voom_append_kv).  head_dim a multiple of 4.  delta,
  * ln_weight, eps and x_out are the optional residual-add + RMSNorm prologue of
- * voom_add_rms_norm_gemv (ln_weight NULL: x is the projection input). */
+ * voom_add_rms_norm_gemv (ln_weight NULL: x is the projection input).  With
+ * rope_rows > 0, cos_row / sin_row are tables [rope_rows, head_dim] and the
+ * row of *position is used (clamped into the table), so a captured step needs
+ * no per-token table work. */
 int voom_qkv_rope_append(const void* w_qkv, const void* x, const void* delta,
                          const void* ln_weight, float eps, void* x_out, const float* cos_row,
                          const float* sin_row, void* q, void* k_pool, void* v_pool,
                          const int32_t* table_row, const int32_t* position, int num_q_heads,
                          int num_kv_heads, int head_dim, int k, int page_tokens, int max_pages,
-                         int num_slots, hipStream_t stream);
+                         int num_slots, int rope_rows, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Page writes and reads.

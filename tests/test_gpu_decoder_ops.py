@@ -215,3 +215,66 @@ def test_norm_prologue_rejects_aliased_residual_output():
         ops.gemv(x, w, ln_weight=ln, delta=d, x_out=x)
     with pytest.raises(ValueError):
         ops.gemv(x, w, delta=d)   # delta without ln_weight
+
+
+@pytest.mark.parametrize("n,k,with_norm", [(49152, 576, True), (1003, 8, False), (5, 2048, True)])
+def test_lm_head_argmax_is_torch_argmax_of_the_gemv_logits(n, k, with_norm):
+    print(f"[decoder-ops] lm_head_argmax n={n} k={k} norm={with_norm}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(n + k)
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    x = torch.randn((1, 1, k), generator=g, device="cuda").to(torch.bfloat16)
+    d = torch.randn((1, 1, k), generator=g, device="cuda").to(torch.bfloat16) if with_norm else None
+    ln = (1 + 0.1 * torch.randn((k,), generator=g, device="cuda")).to(torch.bfloat16) if with_norm else None
+    tok = torch.full((1,), -1, dtype=torch.int64, device="cuda")
+    tok2 = torch.full((1, 1), -1, dtype=torch.int64, device="cuda")
+    ops.lm_head_argmax(x, w, tok, token_copy=tok2, ln_weight=ln, eps=1e-5, delta=d)
+    h = ops.add_rms_norm(x.clone(), ln, 1e-5, delta=d) if with_norm else x
+    ref = ops.gemv(h, w).float().reshape(n).argmax()
+    torch.cuda.synchronize()
+    assert int(tok[0]) == int(ref) == int(tok2[0, 0])
+
+
+def test_lm_head_argmax_takes_the_lowest_index_among_ties():
+    n, k = 4096, 64
+    w = torch.zeros((n, k), dtype=torch.bfloat16, device="cuda")
+    x = torch.ones((k,), dtype=torch.bfloat16, device="cuda")
+    for r in (3001, 77, 2500):          # equal, largest logits
+        w[r] = 0.5
+    w[10] = -4.0
+    tok = torch.zeros((1,), dtype=torch.int64, device="cuda")
+    ops.lm_head_argmax(x, w, tok)
+    torch.cuda.synchronize()
+    assert int(tok[0]) == 77
+    w[77] = 0.25                        # now 2500 and 3001 tie
+    ops.lm_head_argmax(x, w, tok)
+    torch.cuda.synchronize()
+    assert int(tok[0]) == 2500
+    w.fill_(0.0)
+    w[:5] = -1.0                        # all logits <= 0: first zero logit wins
+    ops.lm_head_argmax(x, w, tok)
+    torch.cuda.synchronize()
+    assert int(tok[0]) == 5 == int(ops.gemv(x, w).float().argmax())
+
+
+def test_qkv_rope_append_reads_the_table_row_of_the_device_position():
+    from voom_amd.page_pool import v_slot_shape
+    nq, nkv, hd, K, PT, pos = 9, 3, 64, 576, 64, 100
+    g = torch.Generator(device="cuda").manual_seed(11)
+    w = (torch.randn(((nq + 2 * nkv) * hd, K), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    x = torch.randn((1, 1, K), generator=g, device="cuda").to(torch.bfloat16)
+    inv = 1.0 / (10000.0 ** (torch.arange(hd // 2, device="cuda", dtype=torch.float32) / (hd // 2)))
+    ang = torch.arange(300, device="cuda", dtype=torch.float32)[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).contiguous()
+    sin = torch.cat([ang.sin(), ang.sin()], -1).contiguous()
+    table = torch.tensor([[2, 0, 3, 1]], dtype=torch.int32, device="cuda")
+    position = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    kp = [torch.zeros((4, nkv, PT, hd), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    vp = [torch.zeros((4,) + v_slot_shape(nkv, hd, PT), dtype=torch.bfloat16, device="cuda")
+          for _ in range(2)]
+    q1 = ops.qkv_rope_append(x, w, cos, sin, kp[0], vp[0], table, position, nq, nkv, hd)
+    q2 = ops.qkv_rope_append(x, w, cos[pos:pos + 1].contiguous(), sin[pos:pos + 1].contiguous(),
+                             kp[1], vp[1], table, position, nq, nkv, hd)
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(kp[0].view(torch.int16), kp[1].view(torch.int16))
+    assert torch.equal(vp[0].view(torch.int16), vp[1].view(torch.int16))

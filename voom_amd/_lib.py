@@ -50,7 +50,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_silu_mul": (c_int, [_P, _P, c_int, c_int, _P]),
     "voom_gemv_bf16": (c_int, [_P, _P, _P, c_int, c_int, c_int, _P]),
     "voom_qkv_rope_append": (c_int, [_P, _P, _P, _P, c_float, _P, _P, _P, _P, _P, _P, _P, _P,
-                                     c_int, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
+                                     c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                     _P]),
+    "voom_lm_head_argmax": (c_int, [_P, _P, _P, c_float, _P, c_int, c_int, _P, c_size_t, _P, _P,
+                                    _P]),
     "voom_add_rms_norm_gemv": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int, c_int,
                                        _P]),
     "voom_position_free_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),

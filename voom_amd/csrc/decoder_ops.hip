@@ -381,7 +381,7 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, uint16_t* __restrict__ q,
     uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
     const int32_t* __restrict__ table_row, const int32_t* __restrict__ pos_ptr, int nq, int nkv,
-    int hd, int k, int pt_shift, int max_pages, int num_slots) {
+    int hd, int k, int pt_shift, int max_pages, int num_slots, int rope_rows) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = blockIdx.x * (kRowThreads / kWave) + (threadIdx.x / kWave);
   const int half = hd / 2;
@@ -400,6 +400,11 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
   uint16_t o1, o2;
   if (h < nq + nkv) {
 #pragma clang fp contract(off)
+    if (rope_rows > 0) {  // tables: the row of the token's position (clamped)
+      const int r = min(max(*pos_ptr, 0), rope_rows - 1);
+      cos_t += static_cast<size_t>(r) * hd;
+      sin_t += static_cast<size_t>(r) * hd;
+    }
     const float a0 = x1 * cos_t[i];
     const float b0 = -x2 * sin_t[i];
     const float a1 = x2 * cos_t[i + half];
@@ -435,6 +440,79 @@ __global__ __launch_bounds__(kRowThreads) void qkv_rope_append_kernel(
     const int col = off & ((1 << vb_shift) - 1);
     v_pool[((blk * hd + i) << vb_shift) + col] = o1;
     v_pool[((blk * hd + i + half) << vb_shift) + col] = o2;
+  }
+}
+
+// Greedy sampling key of one bf16 logit: larger keys are larger logits, and
+// among equal logits the lower index; -0 counts as +0 and every NaN as the
+// largest value, as torch.argmax orders them.
+__device__ __forceinline__ uint64_t logit_key(uint16_t bits, int idx) {
+  if ((bits & 0x7fffu) == 0) bits = 0;
+  if ((bits & 0x7f80u) == 0x7f80u && (bits & 0x7fu)) bits = 0x7fc0u;
+  const uint32_t f = static_cast<uint32_t>(bits) << 16;
+  const uint32_t ordered = f ^ ((f >> 31) ? 0xffffffffu : 0x80000000u);
+  return (static_cast<uint64_t>(ordered) << 32) | (0xffffffffu - static_cast<uint32_t>(idx));
+}
+
+// The lm_head projection of one row with its argmax: each wavefront projects
+// 4 vocabulary rows (the GEMV above, optional final-norm prologue), keys its
+// bf16 logits and the workgroup's best key goes to keys[blockIdx.x].  No
+// logits are stored.
+template <int KC, bool NORM>
+__global__ __launch_bounds__(kRowThreads) void gemv_argmax_kernel(
+    const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+    const uint16_t* __restrict__ delta, const uint16_t* __restrict__ ln, float eps,
+    uint64_t* __restrict__ keys, int n, int k) {
+  __shared__ uint64_t s_key[kRowThreads / kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wib = threadIdx.x / kWave;
+  const int first = 4 * (blockIdx.x * (kRowThreads / kWave) + wib);
+  uint64_t best = 0;  // below every real key
+  if (first < n) {  // uniform over the wavefront
+    int rows[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rows[i] = first + i < n ? first + i : first;
+    float acc[4];
+    gemv_rows<KC, NORM>(w, x, delta, ln, eps, nullptr, false, rows, k, lane, acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (first + i < n) {
+        const uint64_t key = logit_key(f2bf(acc[i]), first + i);
+        best = key > best ? key : best;
+      }
+    }
+  }
+  if (lane == 0) s_key[wib] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t m = s_key[0];
+#pragma unroll
+    for (int i = 1; i < kRowThreads / kWave; ++i) m = s_key[i] > m ? s_key[i] : m;
+    keys[blockIdx.x] = m;
+  }
+}
+
+// One workgroup: the best of nkeys keys; its index goes to token[0] and,
+// when given, token_copy[0].
+__global__ __launch_bounds__(kRowThreads) void argmax_finish_kernel(
+    const uint64_t* __restrict__ keys, int nkeys, int64_t* __restrict__ token,
+    int64_t* __restrict__ token_copy) {
+  __shared__ uint64_t s_key[kRowThreads];
+  uint64_t m = 0;
+  for (int i = threadIdx.x; i < nkeys; i += kRowThreads) m = keys[i] > m ? keys[i] : m;
+  s_key[threadIdx.x] = m;
+  __syncthreads();
+  for (int h = kRowThreads / 2; h >= 1; h >>= 1) {
+    if (threadIdx.x < h) {
+      const uint64_t o = s_key[threadIdx.x + h];
+      if (o > s_key[threadIdx.x]) s_key[threadIdx.x] = o;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int64_t idx = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(s_key[0]));
+    token[0] = idx;
+    if (token_copy) token_copy[0] = idx;
   }
 }
 
@@ -495,7 +573,7 @@ extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const void
                                     void* k_pool, void* v_pool, const int32_t* table_row,
                                     const int32_t* position, int num_q_heads, int num_kv_heads,
                                     int head_dim, int k, int page_tokens, int max_pages,
-                                    int num_slots, hipStream_t stream) {
+                                    int num_slots, int rope_rows, hipStream_t stream) {
   const char* who = "qkv_rope_append";
   VOOM_REQUIRE(w_qkv && x && cos_row && sin_row && q && k_pool && v_pool && table_row && position,
                "%s: null pointer argument", who);
@@ -506,6 +584,7 @@ extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const void
                "%s: k %d must be a positive multiple of 8 up to %d", who, k, 8 * kWave * 4);
   VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens <= 4096 && max_pages > 0 && num_slots > 0,
                "%s: bad page geometry", who);
+  VOOM_REQUIRE(rope_rows >= 0, "%s: rope_rows must be >= 0", who);
   VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w_qkv) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(x) % 16 == 0,
                "%s: weight and x must be 16-byte aligned", who);
@@ -525,7 +604,7 @@ extern "C" int voom_qkv_rope_append(const void* w_qkv, const void* x, const void
   hipLaunchKernelGGL((qkv_rope_append_kernel<KC_, NORM_>), grid, dim3(kRowThreads), 0, stream, \
                      wq, xv, dv, lw, eps, xo, cos_row, sin_row, qo, kp, vp, table_row,         \
                      position, num_q_heads, num_kv_heads, head_dim, k, pts, max_pages,         \
-                     num_slots)
+                     num_slots, rope_rows)
 #define VOOM_QRA(KC_)      \
   if (lw)                  \
     VOOM_QRA_N(KC_, true); \
@@ -569,6 +648,51 @@ extern "C" int voom_add_rms_norm_gemv(const void* x, const void* delta, const vo
   auto* xo = static_cast<uint16_t*>(x_out);
   return swiglu ? launch_gemv<true>(w, xv, dv, lw, eps, xo, yv, n, k, stream)
                 : launch_gemv<false>(w, xv, dv, lw, eps, xo, yv, n, k, stream);
+}
+
+extern "C" int voom_lm_head_argmax(const void* x, const void* delta, const void* ln_weight,
+                                   float eps, const void* weight, int n, int k, void* workspace,
+                                   size_t ws_bytes, int64_t* token, int64_t* token_copy,
+                                   hipStream_t stream) {
+  const char* who = "lm_head_argmax";
+  VOOM_REQUIRE(x && weight && workspace && token, "%s: null pointer argument", who);
+  if (int rc = check_norm_prologue(who, x, delta, ln_weight, nullptr)) return rc;
+  VOOM_REQUIRE(n > 0 && n < (1 << 28) && k > 0 && k % 8 == 0 && k <= 8 * kWave * 4,
+               "%s: k %d must be a positive multiple of 8 up to %d", who, k, 8 * kWave * 4);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(weight) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(workspace) % 8 == 0,
+               "%s: weight and x must be 16-byte aligned, workspace 8-byte", who);
+  const int rows_per_block = 4 * (kRowThreads / kWave);
+  const int blocks = (n + rows_per_block - 1) / rows_per_block;
+  VOOM_REQUIRE(ws_bytes >= static_cast<size_t>(blocks) * 8, "%s: workspace needs %d bytes", who,
+               blocks * 8);
+  const auto* w = static_cast<const uint16_t*>(weight);
+  const auto* xv = static_cast<const uint16_t*>(x);
+  const auto* dv = static_cast<const uint16_t*>(delta);
+  const auto* lw = static_cast<const uint16_t*>(ln_weight);
+  auto* keys = static_cast<uint64_t*>(workspace);
+  const int kc = (k / 8 + kWave - 1) / kWave;
+#define VOOM_GA(KC_, NORM_)                                                                   \
+  hipLaunchKernelGGL((gemv_argmax_kernel<KC_, NORM_>), dim3(blocks), dim3(kRowThreads), 0,      \
+                     stream, w, xv, dv, lw, eps, keys, n, k)
+#define VOOM_GA_KC(KC_) \
+  if (lw)               \
+    VOOM_GA(KC_, true); \
+  else                  \
+    VOOM_GA(KC_, false)
+  switch (kc) {
+    case 1: VOOM_GA_KC(1); break;
+    case 2: VOOM_GA_KC(2); break;
+    case 3: VOOM_GA_KC(3); break;
+    default: VOOM_GA_KC(4); break;
+  }
+#undef VOOM_GA_KC
+#undef VOOM_GA
+  if (int rc = VOOM_LAUNCH_CHECK("lm_head_argmax: projection launch")) return rc;
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(kRowThreads), 0, stream, keys, blocks,
+                     token, token_copy);
+  return VOOM_LAUNCH_CHECK("lm_head_argmax: finish launch");
 }
 
 extern "C" int voom_add_rms_norm(void* x, const void* delta, const void* weight, void* out,

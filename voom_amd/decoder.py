@@ -228,18 +228,26 @@ class PagedDecoder:
         device op with fixed shapes and addresses, so the step can be captured
         and replayed; it computes what ``forward`` computes for one token."""
         B = tok.shape[0]
-        cos, sin = self._rope_tables(kv._pos_dev[:1])
         x = self.embed[tok]
         delta = None
         cfg = self.cfg
         if B == 1 and max(cfg.hidden_size, cfg.intermediate_size,
                           cfg.num_attention_heads * cfg.head_dim) <= ops.GEMV_MAX_K:
+            # whole RoPE tables (capture_decode's, one row per reserved
+            # position, the same elementwise torch ops as _rope_tables): the
+            # qkv kernel reads the row of the device position
+            cos, sin = self._rope_rows
             spare = torch.empty_like(x)
             for layer in range(cfg.num_hidden_layers):
                 delta, x, spare = self._block_token(x, spare, delta, layer, kv, cos, sin)
-        else:
-            for layer in range(self.cfg.num_hidden_layers):
-                delta = self._block(x, delta, layer, kv, cos, sin, graph=True)
+            # final norm, lm_head and argmax in two launches, no logits stored
+            ops.lm_head_argmax(x, self.embed, nxt, token_copy=tok, ln_weight=self.final_norm,
+                               eps=cfg.rms_norm_eps, delta=delta)
+            kv.step_counters()
+            return
+        cos, sin = self._rope_tables(kv._pos_dev[:1])
+        for layer in range(self.cfg.num_hidden_layers):
+            delta = self._block(x, delta, layer, kv, cos, sin, graph=True)
         x = self._norm(x, self.final_norm, delta)
         logits = self._linear(x, self.embed).float()
         nxt.copy_(logits[:, -1].argmax(-1))
@@ -253,6 +261,8 @@ class PagedDecoder:
         step's input token in ``tok`` (a replay leaves its output there);
         after it call ``kv.advance(1)``."""
         kv.reserve(max_len)
+        self._rope_rows = self._rope_tables(torch.arange(max(int(max_len), 1),
+                                                         device=self.device))
         B = kv._batch
         tok = torch.zeros((B, 1), dtype=torch.long, device=self.device)
         nxt = torch.zeros((B,), dtype=torch.long, device=self.device)

@@ -502,6 +502,32 @@ def gemv(x: torch.Tensor, weight: torch.Tensor, *, swiglu: bool = False,
     return y
 
 
+def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, token: torch.Tensor, *,
+                   token_copy: torch.Tensor | None = None,
+                   ln_weight: torch.Tensor | None = None, eps: float = 1e-5,
+                   delta: torch.Tensor | None = None,
+                   stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Greedy next token of one row: token[0] (int64, and token_copy[0] when
+    given) = argmax of the bf16 logits x . weight^T, lowest index among ties,
+    as ``gemv(x, weight).argmax()``; with ln_weight (and delta) the final
+    residual add + RMSNorm of ``gemv`` comes first.  No logits are stored."""
+    dev = _require_device(x, weight, token, token_copy, ln_weight, delta)
+    _require(x.dtype == weight.dtype == torch.bfloat16, "bf16 x and weight")
+    _require(weight.dim() == 2 and x.shape[-1] == weight.shape[1] and x.numel() == x.shape[-1],
+             "one row x [K] and weight [N, K]")
+    _norm_prologue(x, ln_weight, delta, None)
+    N, K = weight.shape
+    _require(K % 8 == 0 and K <= GEMV_MAX_K, f"K must be a multiple of 8 up to {GEMV_MAX_K}")
+    for t in (token, token_copy):
+        _require(t is None or (t.dtype == torch.int64 and t.numel() >= 1), "int64 token outputs")
+    need = 8 * ((N + 15) // 16)
+    ws = workspace(dev, need, tag=3)
+    _lib.call("voom_lm_head_argmax", _ptr(x), _ptr(delta), _ptr(ln_weight), float(eps),
+              _ptr(weight), N, K, _ptr(ws), ws.numel(), _ptr(token), _ptr(token_copy),
+              _stream(stream))
+    return token
+
+
 def qkv_rope_append(x: torch.Tensor, w_qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                     k_pool: torch.Tensor, v_pool: torch.Tensor, block_table: torch.Tensor,
                     position: torch.Tensor, num_q_heads: int, num_kv_heads: int, head_dim: int,
@@ -509,8 +535,8 @@ def qkv_rope_append(x: torch.Tensor, w_qkv: torch.Tensor, cos: torch.Tensor, sin
                     delta: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
                     stream: torch.cuda.Stream | None = None) -> torch.Tensor:
     """One decode token of one sequence: q [1, nq, 1, hd] of the fused qkv
-    projection of x (one row of K), rotated with the fp32 rows cos/sin [.., hd]
-    of its position; k, v rotated/written into the pools at position[0]
+    projection of x (one row of K), rotated with the fp32 rows cos/sin [1, hd]
+    of its position (or, given whole tables [rows, hd], their row position[0]); k, v rotated/written into the pools at position[0]
     (int32 device tensor) through block_table row 0.  Bit-identical to gemv,
     rope_split and append_kv in sequence.  ln_weight, eps, delta, x_out: the
     residual-add + RMSNorm prologue of ``gemv``."""
@@ -522,8 +548,10 @@ def qkv_rope_append(x: torch.Tensor, w_qkv: torch.Tensor, cos: torch.Tensor, sin
     _require(x.numel() == K == x.shape[-1], "x must be one row of the projection's K")
     _require(w_qkv.shape[0] == (nq + 2 * nkv) * hd, "w_qkv rows must be (nq + 2 nkv) * hd")
     _require(x.dtype == w_qkv.dtype == k_pool.dtype == v_pool.dtype == torch.bfloat16, "bf16")
-    _require(cos.dtype == sin.dtype == torch.float32 and cos.shape[-1] == sin.shape[-1] == hd,
-             "fp32 cos/sin rows of head_dim")
+    _require(cos.dtype == sin.dtype == torch.float32 and cos.shape[-1] == sin.shape[-1] == hd
+             and cos.shape == sin.shape, "fp32 cos/sin rows of head_dim")
+    # several rows: whole tables indexed by the device position in the kernel
+    rope_rows = cos.numel() // hd if cos.numel() > hd else 0
     slots, NKVp, PT, Dp = k_pool.shape
     _require(NKVp == nkv and Dp == hd, "pool geometry does not match the heads")
     _check_v_pool(v_pool, slots, nkv, hd, PT)
@@ -533,7 +561,7 @@ def qkv_rope_append(x: torch.Tensor, w_qkv: torch.Tensor, cos: torch.Tensor, sin
     _lib.call("voom_qkv_rope_append", _ptr(w_qkv), _ptr(x), _ptr(delta), _ptr(ln_weight),
               float(eps), _ptr(x_out), _ptr(cos), _ptr(sin), _ptr(q),
               _ptr(k_pool), _ptr(v_pool), _ptr(block_table), _ptr(position), nq, nkv, hd, K, PT,
-              block_table.shape[1], slots, _stream(stream))
+              block_table.shape[1], slots, rope_rows, _stream(stream))
     return q
 
 
