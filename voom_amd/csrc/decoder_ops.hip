@@ -498,8 +498,18 @@ __global__ __launch_bounds__(kRowThreads) void argmax_finish_kernel(
     const uint64_t* __restrict__ keys, int nkeys, int64_t* __restrict__ token,
     int64_t* __restrict__ token_copy) {
   __shared__ uint64_t s_key[kRowThreads];
+  constexpr int kPer = 16;  // loads in flight per thread
   uint64_t m = 0;
-  for (int i = threadIdx.x; i < nkeys; i += kRowThreads) m = keys[i] > m ? keys[i] : m;
+  for (int base = 0; base < nkeys; base += kPer * kRowThreads) {
+    uint64_t v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = base + j * kRowThreads + threadIdx.x;
+      v[j] = i < nkeys ? keys[i] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) m = v[j] > m ? v[j] : m;
+  }
   s_key[threadIdx.x] = m;
   __syncthreads();
   for (int h = kRowThreads / 2; h >= 1; h >>= 1) {
