@@ -67,6 +67,21 @@ __device__ __forceinline__ float wave_sum_uniform(float v) {
   return ((r0 + r1) + r2) + r3;
 }
 
+// Maximum over the 64 lanes, the same value in every lane (the moves of
+// wave_sum_uniform with fmaxf).
+__device__ __forceinline__ float wave_max_uniform(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  v = fmaxf(v, dpp_move<0x140>(v));
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) {

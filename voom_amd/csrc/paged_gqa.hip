@@ -588,22 +588,20 @@ __global__ __launch_bounds__(kThreads) void gqa_reduce_kernel(
     // Keep the scheduler from sinking each load next to its use (which would
     // serialise kBatch round trips): everything above issues first.
     __builtin_amdgcn_sched_barrier(0);
-    float Mc = live ? mi.x : -INFINITY;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, o));
+    // cross-lane work by DPP moves and v_readlane (no LDS crossbar trips)
+    const float Mc = wave_max_uniform(live ? mi.x : -INFINITY);
     const float Mn = fmaxf(M, Mc);
     const float rescale = fast_exp2(M - Mn);
     const float wl = live ? fast_exp2(mi.x - Mn) : 0.f;
-    float Lc = live ? mi.y * wl : 0.f;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) Lc += __shfl_xor(Lc, o);
+    const float Lc = wave_sum_uniform(live ? mi.y * wl : 0.f);
     L = L * rescale + Lc;
     M = Mn;
 #pragma unroll
     for (int d = 0; d < DPL; ++d) acc[d] *= rescale;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const float wk = __shfl(wl, u);
+      const float wk = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), u));
 #pragma unroll
       for (int d = 0; d < DPL; ++d) acc[d] += v[u][d] * wk;
     }
