@@ -512,16 +512,13 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
     const int r = r0 + lane;
     const float2 ml = r < NR ? ml2[(static_cast<size_t>(b) * NR + r) * H + h]
                              : make_float2(-INFINITY, 0.f);
-    float Mc = ml.x;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, o));
+    // cross-lane work by DPP moves and v_readlane (no LDS crossbar trips)
+    const float Mc = wave_max_uniform(ml.x);
     const float Mn = fmaxf(M, Mc);
     if (Mn == -INFINITY) continue;  // no tokens in any range so far
     const float rescale = fast_exp2(M - Mn);
     const float wl = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - Mn);
-    float Lc = ml.y * wl;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) Lc += __shfl_xor(Lc, o);
+    const float Lc = wave_sum_uniform(ml.y * wl);
     L = L * rescale + Lc;
     M = Mn;
 #pragma unroll
@@ -540,7 +537,9 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const float wk = k0 + u < cnt ? __shfl(wl, k0 + u) : 0.f;
+        const float wk = k0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                            __builtin_bit_cast(int, wl), k0 + u))
+                                      : 0.f;
         // a range without tokens has weight 0 and an all-zero row
 #pragma unroll
         for (int c = 0; c < DPL / 4; ++c) acc[c] += v[u][c] * wk;

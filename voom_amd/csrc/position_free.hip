@@ -438,8 +438,7 @@ __global__ __launch_bounds__(kRedWaves * kWave) void pf_reduce_kernel(PfArgs a, 
       const bool live = i0 + u * kRedRows + r < cnt;
       if (live) Mc = fmaxf(Mc, ml[u].x);
     }
-#pragma unroll
-    for (int x = 32; x >= 1; x >>= 1) Mc = fmaxf(Mc, __shfl_xor(Mc, x));
+    Mc = wave_max_uniform(Mc);  // DPP moves + v_readlane, no LDS crossbar trips
     const float Mn = fmaxf(M, Mc);
     if (Mn == -INFINITY) continue;  // wave-uniform: nothing visible yet
     const float rescale = M == -INFINITY ? 0.f : fast_exp2(M - Mn);
@@ -453,9 +452,7 @@ __global__ __launch_bounds__(kRedWaves * kWave) void pf_reduce_kernel(PfArgs a, 
       Lc += ml[u].y * w;
     }
     // each split's l is held by all kRedCols lanes of its row: count lane j == 0
-    Lc = j == 0 ? Lc : 0.f;
-#pragma unroll
-    for (int x = 32; x >= 1; x >>= 1) Lc += __shfl_xor(Lc, x);
+    Lc = wave_sum_uniform(j == 0 ? Lc : 0.f);
     L = L * rescale + Lc;
     M = Mn;
   }
