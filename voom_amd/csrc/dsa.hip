@@ -334,9 +334,11 @@ __host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys -
 
 // 1. Threshold: rows of at most kCandCap keys take every key as a candidate
 // (T0 = 0).  Longer rows: T0 is the key of rank 1.5 x (the sample's share of
-// k) + 32 in a strided sample of kSample keys, found exactly by the radix
+// k) + 32 in a sample of kSample keys (runs of 4 adjacent keys spread evenly
+// over a 16-byte aligned row, else single keys at an even stride), found exactly by the radix
 // select in LDS -- about 1.5 k candidates, with margin, and no more than the
 // sample's ties at T0 allow.
+template <bool VEC>
 __global__ __launch_bounds__(kTopkThreads) void dsa_topk_threshold_kernel(
     const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
     int K) {
@@ -355,13 +357,25 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_threshold_kernel(
   const float* sb = scores + static_cast<size_t>(b) * cap;
   constexpr int kPer = kSample / kTopkThreads;
   float v[kPer];
+  if (VEC) {
+    static_assert(kSample / kTopkThreads == 4, "one float4 of keys per thread");
+    // runs of kPer adjacent keys, one 16-byte load per thread, spread evenly
+    // over the row (n > kCandCap, so every run lies inside it)
+    const int j0 = static_cast<int>(static_cast<long long>(tid) * n / kTopkThreads) & ~(kPer - 1);
+    const float4 f = *reinterpret_cast<const float4*>(sb + j0);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  } else {
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int j = tid + k * kTopkThreads;
-    v[k] = sb[static_cast<int>(static_cast<long long>(j) * n / kSample)];
+    for (int k = 0; k < kPer; ++k) {
+      const int j = tid + k * kTopkThreads;
+      v[k] = sb[static_cast<int>(static_cast<long long>(j) * n / kSample)];
+    }
   }
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) sample[tid + k * kTopkThreads] = order_key(v[k]);
+  for (int k = 0; k < kPer; ++k) sample[tid * kPer + k] = order_key(v[k]);
   __syncthreads();
   long long r = (static_cast<long long>(K) * kSample + n - 1) / n;
   r = r + r / 2 + 32;
@@ -600,12 +614,18 @@ extern "C" int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* 
   ws.counts = reinterpret_cast<int*>(p + t0_bytes);
   ws.cand = reinterpret_cast<uint2*>(
       p + t0_bytes + ((static_cast<size_t>(batch) * ws.chunks * 4 + 255) & ~size_t(255)));
-  hipLaunchKernelGGL(dsa_topk_threshold_kernel, dim3(static_cast<unsigned>(batch)),
-                     dim3(kTopkThreads), 0, stream, scores, lens, ws, cap, k);
+  const bool vec = cap % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0;
+  if (vec) {
+    hipLaunchKernelGGL(dsa_topk_threshold_kernel<true>, dim3(static_cast<unsigned>(batch)),
+                       dim3(kTopkThreads), 0, stream, scores, lens, ws, cap, k);
+  } else {
+    hipLaunchKernelGGL(dsa_topk_threshold_kernel<false>, dim3(static_cast<unsigned>(batch)),
+                       dim3(kTopkThreads), 0, stream, scores, lens, ws, cap, k);
+  }
   int rc = VOOM_LAUNCH_CHECK("dsa_topk: threshold kernel launch");
   if (rc) return rc;
   const dim3 cgrid(static_cast<unsigned>(ws.chunks), static_cast<unsigned>(batch));
-  if (cap % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0) {
+  if (vec) {
     hipLaunchKernelGGL(dsa_topk_compact_kernel<true>, cgrid, dim3(kCompactThreads), 0, stream,
                        scores, lens, ws, cap, k);
   } else {
