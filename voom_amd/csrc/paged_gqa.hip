@@ -401,6 +401,27 @@ __global__ __launch_bounds__(SW * kWave) void gqa_segment_kernel(
   const int b = blockIdx.x / NKV;
   const int kvh = blockIdx.x - b * NKV;
   const int NQ = NKV * G;
+  const int i16 = lane & 15;
+  const int g = lane >> 4;
+  const bool head_ok = i16 < G;
+  // Loads that do not depend on the context length issue before it arrives:
+  // the q operands and, for tables of at most 64 pages, the whole table row
+  // (one memory round trip fewer before the first page load).
+  u32x4 qop[D / 32];
+  {
+    const uint16_t* qh = q + (static_cast<size_t>(b) * NQ + kvh * G + (head_ok ? i16 : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qop[s] = head_ok ? *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g) : z;
+    }
+  }
+  int tab_base = -(1 << 30);
+  int tab = 0;
+  if (max_pages <= kWave) {
+    tab_base = 0;
+    tab = lane < max_pages ? block_table[static_cast<size_t>(b) * max_pages + lane] : 0;
+  }
   const int cap_tokens = max_pages << pt_shift;
   int ctx = uniform(ctx_lens[b]);
   ctx = ctx < 0 ? 0 : (ctx > cap_tokens ? cap_tokens : ctx);
@@ -408,9 +429,6 @@ __global__ __launch_bounds__(SW * kWave) void gqa_segment_kernel(
   const int blo = wl * nb / SW;
   const int bhi = (wl + 1) * nb / SW;
 
-  const int i16 = lane & 15;
-  const int g = lane >> 4;
-  const bool head_ok = i16 < G;
   LaneOffsets lofs;
   lofs.k = ((8 * (i16 >> 2) + (i16 & 3)) * D + 8 * g) * 2;
   lofs.v = ((i16 * kBlockTokens) + 8 * g) * 2;
@@ -431,15 +449,6 @@ __global__ __launch_bounds__(SW * kWave) void gqa_segment_kernel(
   st.m = -INFINITY;
   st.l = 0.f;
   if (blo < bhi) {
-    u32x4 qop[D / 32];
-    const uint16_t* qh = q + (static_cast<size_t>(b) * NQ + kvh * G + (head_ok ? i16 : 0)) * D;
-#pragma unroll
-    for (int s = 0; s < D / 32; ++s) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      qop[s] = head_ok ? *reinterpret_cast<const u32x4*>(qh + 32 * s + 8 * g) : z;
-    }
-    int tab_base = -(1 << 30);
-    int tab = 0;
     BlockRegs<D> ring[NBUF];
 #pragma unroll
     for (int j = 0; j < NBUF - 1; ++j) {

@@ -281,6 +281,9 @@ class PagedDecoder:
         with torch.cuda.graph(graph):
             self._graph_step(tok, nxt, kv)
         torch.cuda.synchronize()
+        # the replays read these tables: they live as long as the graph does,
+        # also after a later capture replaces self._rope_rows
+        graph.voom_rope_rows = self._rope_rows
         return graph, tok, nxt
 
     @torch.no_grad()
