@@ -62,7 +62,10 @@ constexpr int kBlockTokens = 32;
 #endif
 constexpr int kNbuf128 = VOOM_GQA_NBUF_128;
 constexpr int kWavesPerEu128 = VOOM_GQA_WAVES_PER_EU_128;
-constexpr int kNbuf64 = 3;
+#ifndef VOOM_GQA_NBUF_64
+#define VOOM_GQA_NBUF_64 3
+#endif
+constexpr int kNbuf64 = VOOM_GQA_NBUF_64;
 constexpr int kWavesPerEu64 = 2;
 
 // Exclusive prefix sum of per-sequence 32-token block counts into seg[0..B].
@@ -144,6 +147,11 @@ __device__ __forceinline__ void load_block(BlockRegs<D>& r, const SegmentArgs& a
     tab_base = page;
     const int p = tab_base + lane;
     tab = p < a.n_pages ? a.table_row[p] : 0;
+    // Wait here, on this rare path, for the window.  Without it the compiler
+    // cannot tell at the readlane below whether a table load is outstanding,
+    // and waits for every load in flight there -- the blocks the ring has
+    // prefetched included -- on every block.
+    wait_vmem_all();
   }
   int slot = __builtin_amdgcn_readlane(tab, page - tab_base);
   if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
