@@ -107,6 +107,16 @@ int voom_merge_attn_states(const void* o_a, const float* lse_a, const void* o_b,
                            const float* lse_b, void* out, float* lse_out, int rows,
                            int head_dim, hipStream_t stream);
 
+/* voom_mla_head_gemv: y[b, h, n] = bf16(sum_k x[b, h, k] w[h, k, n]), fp32
+ * sums, for the few query rows of a decode step -- the absorption products
+ * q_nope . W_UK (runtime/glm.py:129-132) and weighted_c . W_UV
+ * (runtime/glm.py:200-202) that hipBLASLt runs as batched GEMMs with M =
+ * batch.  x [batch, num_heads, x_stride] (first k used), w [num_heads, k, n]
+ * (16-byte aligned), y [batch, num_heads, y_stride] (first n written);
+ * batch 1..16, k <= 512, n in 8, 16, ..., 512 with n / 8 dividing 64. */
+int voom_mla_head_gemv(const void* x, const void* w, void* y, int batch, int num_heads, int k,
+                       int n, int x_stride, int y_stride, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Absorbed-MLA paged decode: the latent contraction.
  *

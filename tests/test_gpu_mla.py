@@ -103,3 +103,36 @@ def test_config5_full_size_two_sequences():
     print("[mla] config 5 full size", flush=True)
     inp = synthetic.mla_decode_inputs()
     check_latent(inp, batches=[0, 7])
+
+
+@pytest.mark.parametrize("B,H,K,N", [(8, 128, 128, 512), (8, 128, 512, 128), (3, 5, 40, 64),
+                                     (16, 4, 512, 512), (1, 2, 1, 8), (9, 3, 100, 256)])
+def test_head_gemv_is_the_fp32_per_head_product_rounded(B, H, K, N):
+    print(f"[mla] head_gemv B={B} H={H} K={K} N={N}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(B * 1000 + H + K + N)
+    x = torch.randn((B, H, K), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((H, K, N), generator=g, device="cuda") * 0.05).to(torch.bfloat16)
+    got = ops.head_gemv(x, w)
+    # fp32 reference on the CPU (exact products, float64 sums)
+    exact = torch.bmm(x.double().cpu().transpose(0, 1), w.double().cpu()).transpose(0, 1)
+    scale = torch.bmm(x.double().cpu().abs().transpose(0, 1),
+                      w.double().cpu().abs()).transpose(0, 1)
+    torch.cuda.synchronize()
+    err = (got.double().cpu() - exact).abs()
+    assert got.shape == (B, H, N)
+    assert bool((err <= exact.abs() * 2.0 ** -8 + scale * 1e-6).all())
+
+
+def test_head_gemv_writes_into_a_wider_row_and_rejects_bad_shapes():
+    x = torch.randn((2, 3, 64), device="cuda").to(torch.bfloat16)
+    w = torch.randn((3, 64, 32), device="cuda").to(torch.bfloat16)
+    out = torch.full((2, 3, 48), 7.0, dtype=torch.bfloat16, device="cuda")
+    ops.head_gemv(x, w, out=out)
+    ref = ops.head_gemv(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(out[..., :32].view(torch.int16), ref.view(torch.int16))
+    assert bool((out[..., 32:] == 7.0).all())
+    with pytest.raises(ValueError):
+        ops.head_gemv(torch.zeros((17, 3, 64), dtype=torch.bfloat16, device="cuda"), w)
+    with pytest.raises(ValueError):
+        ops.head_gemv(x, torch.zeros((3, 64, 24), dtype=torch.bfloat16, device="cuda"))

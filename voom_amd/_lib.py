@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_qkv_rope_append": (c_int, [_P, _P, _P, _P, c_float, _P, _P, _P, _P, _P, _P, _P, _P,
                                      c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                      _P]),
+    "voom_mla_head_gemv": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
     "voom_lm_head_argmax": (c_int, [_P, _P, _P, c_float, _P, c_int, c_int, _P, c_size_t, _P, _P,
                                     _P]),
     "voom_add_rms_norm_gemv": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int, c_int,

@@ -611,6 +611,102 @@ int sparse_ranges(int B, int H, int sel_stride) {
   return nr < lo ? lo : (nr < 1 ? 1 : nr);
 }
 
+// ------------------------------------------------------ per-head products ----
+// y[b, h, n] = sum_k x[b, h, k] w[h, k, n] for the few query rows of a decode
+// step (B <= 16): q_nope . W_UK and weighted_c . W_UV^T of absorbed MLA.  A
+// batched GEMM with M = B spends most of its time on empty tile rows; this is
+// a weight stream.  One workgroup per (head, column part): x[:, h, :] goes to
+// LDS as fp32, then lane (kk, nl) of each wavefront walks k = 4 KR i + KR
+// wave + kk, loads w[h, k, c0 + 8 nl .. + 7] 16 rows at a time (non-temporal:
+// each weight byte is read once) and accumulates all B rows against them.
+// The partial sums of the (wavefront, kk) groups meet in LDS in a fixed
+// order, so the result does not depend on scheduling.
+constexpr int kHgMaxK = 512;
+constexpr int kHgMaxN = 512;
+
+template <int BM>
+__global__ __launch_bounds__(kThreads) void head_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+    int B, int H, int K, int N, int NW, int x_stride, int y_stride) {
+  // x rows while the weights stream, then the wavefronts' partial sums
+  __shared__ float lds[(kThreads / kWave) * BM * kHgMaxN];
+  static_assert(kHgMaxK <= (kThreads / kWave) * kHgMaxN, "x rows fit the reduction space");
+  float (*xs)[BM] = reinterpret_cast<float (*)[BM]>(lds);
+  const int h = blockIdx.x;
+  const int c0 = blockIdx.y * NW;  // this workgroup's columns c0 .. c0 + NW - 1
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
+  // adjacent threads read adjacent k of one row (coalesced), 8 loads in flight
+#pragma unroll 8
+  for (int i = tid; i < K * BM; i += kThreads) {
+    const int b = i / K;
+    const int k = i - b * K;
+    xs[k][b] = b < B ? bf2f(x[(static_cast<size_t>(b) * H + h) * x_stride + k]) : 0.f;
+  }
+  __syncthreads();
+  const int NL = NW / 8;      // lanes across the workgroup's part of one weight row
+  const int KR = kWave / NL;  // weight rows per wavefront load
+  const int kk = lane / NL;
+  const int n0 = 8 * (lane - kk * NL);
+  float acc[BM][8];
+#pragma unroll
+  for (int b = 0; b < BM; ++b) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[b][e] = 0.f;
+  }
+  const uint16_t* wh = w + static_cast<size_t>(h) * K * N + c0 + n0;
+  const int step = (kThreads / kWave) * KR;
+  constexpr int kInFlight = 16;  // weight loads issued before the first use
+  for (int kb = wv * KR + kk; kb < K; kb += kInFlight * step) {
+    u32x4 q[kInFlight];
+#pragma unroll
+    for (int i = 0; i < kInFlight; ++i) {
+      const int k = kb + i * step;
+      q[i] = k < K ? __builtin_nontemporal_load(
+                         reinterpret_cast<const u32x4*>(wh + static_cast<size_t>(k) * N))
+                   : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < kInFlight; ++i) {
+      const int k = kb + i * step;
+      if (k >= K) break;
+      float wf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        wf[2 * e] = bf2f(static_cast<uint16_t>(q[i][e] & 0xffffu));
+        wf[2 * e + 1] = bf2f(static_cast<uint16_t>(q[i][e] >> 16));
+      }
+#pragma unroll
+      for (int b = 0; b < BM; ++b) {
+        const float xb = xs[k][b];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[b][e] = __builtin_fmaf(xb, wf[e], acc[b][e]);
+      }
+    }
+  }
+  // every (wavefront, kk) group leaves its partial sums in LDS -- 4 KR groups
+  // of [BM][NW], exactly the buffer (KR NW = 512) -- and each output sums
+  // them in group order
+  __syncthreads();  // every wavefront is done with the x rows
+  const int groups = (kThreads / kWave) * KR;
+  float* red = lds;
+  const int grp = wv * KR + kk;
+#pragma unroll
+  for (int b = 0; b < BM; ++b) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[(grp * BM + b) * NW + n0 + e] = acc[b][e];
+  }
+  __syncthreads();
+  for (int i = tid; i < B * NW; i += kThreads) {
+    const int b = i / NW;
+    const int n = i - b * NW;
+    float v = red[b * NW + n];
+    for (int g = 1; g < groups; ++g) v += red[(g * BM + b) * NW + n];
+    y[(static_cast<size_t>(b) * H + h) * y_stride + c0 + n] = f2bf(v);
+  }
+}
+
 }  // namespace
 }  // namespace voom
 
@@ -742,4 +838,34 @@ extern "C" int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool,
   a.pool_bytes = static_cast<uint32_t>(pool);
   a.scale_log2e = scale * 1.4426950408889634f;
   return launch_mla(a, hg, true, grid, static_cast<uint16_t*>(out_c), lse_out, stream);
+}
+
+extern "C" int voom_mla_head_gemv(const void* x, const void* w, void* y, int batch,
+                                  int num_heads, int k, int n, int x_stride, int y_stride,
+                                  hipStream_t stream) {
+  const char* who = "mla_head_gemv";
+  VOOM_REQUIRE(x && w && y, "%s: null pointer argument", who);
+  VOOM_REQUIRE(batch >= 1 && batch <= 16 && num_heads >= 1, "%s: batch must be 1..16", who);
+  VOOM_REQUIRE(k >= 1 && k <= kHgMaxK, "%s: k %d must be 1..%d", who, k, kHgMaxK);
+  VOOM_REQUIRE(n % 8 == 0 && n >= 8 && n <= kHgMaxN && kWave % (n / 8) == 0,
+               "%s: n %d must be 8, 16, ..., 512 (n / 8 dividing 64)", who, n);
+  VOOM_REQUIRE(x_stride >= k && y_stride >= n, "%s: row strides below k / n", who);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w) % 16 == 0, "%s: w must be 16-byte aligned", who);
+  const auto* xv = static_cast<const uint16_t*>(x);
+  const auto* wv = static_cast<const uint16_t*>(w);
+  auto* yv = static_cast<uint16_t*>(y);
+  // split the columns until the grid covers the CUs (each part keeps n / 8
+  // dividing 64 and at least 8 lanes per weight row)
+  int ns = 1;
+  while (static_cast<long long>(num_heads) * ns < 256 && (n / ns) % 16 == 0 && n / ns >= 64) ns *= 2;
+  const int nw = n / ns;
+  const dim3 grid(static_cast<unsigned>(num_heads), static_cast<unsigned>(ns));
+  if (batch <= 8) {
+    hipLaunchKernelGGL(head_gemv_kernel<8>, grid, dim3(kThreads), 0, stream, xv, wv, yv, batch,
+                       num_heads, k, n, nw, x_stride, y_stride);
+  } else {
+    hipLaunchKernelGGL(head_gemv_kernel<16>, grid, dim3(kThreads), 0, stream, xv, wv, yv, batch,
+                       num_heads, k, n, nw, x_stride, y_stride);
+  }
+  return VOOM_LAUNCH_CHECK("mla_head_gemv: kernel launch");
 }

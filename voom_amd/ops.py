@@ -579,16 +579,43 @@ def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
 def mla_absorb_query(q_nope: torch.Tensor, q_rope: torch.Tensor, w_uk: torch.Tensor):
     """q_lat = [q_nope . W_UK | q_rope] [B, H, 576] (runtime/glm.py:129-132).
 
-    q_nope [B, H, dn], q_rope [B, H, 64] bf16, W_UK [H, dn, 512]; a batched
-    GEMM over heads with both operands contiguous.
+    q_nope [B, H, dn], q_rope [B, H, 64] bf16, W_UK [H, dn, 512]; the
+    per-head product runs as one weight stream (``head_gemv``).
     """
-    q_abs = torch.bmm(q_nope.transpose(0, 1).contiguous(), w_uk).transpose(0, 1)
-    return torch.cat([q_abs, q_rope], dim=-1).contiguous()
+    B, H, dn = q_nope.shape
+    C = w_uk.shape[-1]
+    q_lat = torch.empty((B, H, C + q_rope.shape[-1]), dtype=q_nope.dtype, device=q_nope.device)
+    head_gemv(q_nope, w_uk, out=q_lat)      # writes q_lat[..., :C]
+    q_lat[..., C:].copy_(q_rope)
+    return q_lat
 
 
 def mla_project_out(wc: torch.Tensor, w_uv_t: torch.Tensor) -> torch.Tensor:
     """weighted_c [B, H, 512] . W_UV -> [B, H, dv] (runtime/glm.py:200-202)."""
-    return torch.bmm(wc.transpose(0, 1).contiguous(), w_uv_t).transpose(0, 1).contiguous()
+    return head_gemv(wc, w_uv_t)
+
+
+def head_gemv(x: torch.Tensor, w: torch.Tensor, *, out: torch.Tensor | None = None,
+              stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """y [B, H, N] = x [B, H, K] . w [H, K, N] per head (fp32 sums, bf16 out)
+    for decode-sized B (<= 16): the absorbed-MLA products as one weight
+    stream (``voom_mla_head_gemv``).  ``out`` may be wider than N in its last
+    dimension (only the first N columns are written)."""
+    x = x.contiguous()
+    dev = _require_device(x, w)
+    _require(x.dtype == w.dtype == torch.bfloat16 and x.dim() == 3 and w.dim() == 3,
+             "bf16 x [B, H, K] and w [H, K, N]")
+    B, H, K = x.shape
+    _require(w.shape[0] == H and w.shape[1] == K, "w must be [H, K, N] for x [B, H, K]")
+    N = w.shape[2]
+    if out is None:
+        out = torch.empty((B, H, N), dtype=x.dtype, device=dev)
+    _require(out.dtype == x.dtype and out.device == dev and out.dim() == 3 and
+             tuple(out.shape[:2]) == (B, H) and out.shape[2] >= N and out.is_contiguous(),
+             "out [B, H, >= N] contiguous bf16")
+    _lib.call("voom_mla_head_gemv", _ptr(x), _ptr(w), _ptr(out), B, H, K, N, K,
+              out.shape[2], _stream(stream))
+    return out
 
 
 def mla_absorbed_decode(q_nope: torch.Tensor, q_rope: torch.Tensor, lat_pool: torch.Tensor,
@@ -599,8 +626,8 @@ def mla_absorbed_decode(q_nope: torch.Tensor, q_rope: torch.Tensor, lat_pool: to
 
     q_nope [B, H, dn], q_rope [B, H, 64] bf16; W_UK [H, dn, 512] and W_UV^T
     [H, 512, dv] from split_kv_b.  q_nope . W_UK and weighted_c . W_UV run
-    as batched GEMMs (hipBLASLt through torch); the latent contraction runs in
-    the HIP kernel.  Returns the per-head output [B, H, dv] bf16 (before o_proj).
+    in the per-head weight-stream kernel (``head_gemv``); the latent
+    contraction runs in the HIP latent kernel.  Returns the per-head output [B, H, dv] bf16 (before o_proj).
     """
     q_lat = mla_absorb_query(q_nope, q_rope, w_uk)
     wc = mla_latent_decode(q_lat, lat_pool, block_table, ctx_lens, scale=scale,
