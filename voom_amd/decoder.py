@@ -274,8 +274,7 @@ class PagedDecoder:
         with torch.cuda.stream(side):
             self._graph_step(tok, nxt, kv)
         torch.cuda.current_stream().wait_stream(side)
-        kv._pos_dev.sub_(1)
-        kv._ctx_dev.sub_(1)
+        kv._counters_dev.sub_(1)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):

@@ -514,8 +514,11 @@ class PagedKVCache:
                 self._open_slots[layer][page] = cols[page]
             self._set_table_cols(layer, cols)
         self._reserved = int(total_len)
-        self._pos_dev = torch.full((B,), self._offset, dtype=torch.int32, device=self.device)
-        self._ctx_dev = self._pos_dev + 1
+        # one [2, B] tensor, so a step advances both counters in one launch
+        self._counters_dev = torch.tensor([[self._offset] * B, [self._offset + 1] * B],
+                                          dtype=torch.int32, device=self.device)
+        self._pos_dev = self._counters_dev[0]
+        self._ctx_dev = self._counters_dev[1]
 
     def append_at(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """Write one token's k, v [B, NKV, 1, D] at the device position counter
@@ -547,8 +550,7 @@ class PagedKVCache:
     def step_counters(self) -> None:
         """Advance the device position counters by one token (the end of a
         captured step)."""
-        self._pos_dev.add_(1)
-        self._ctx_dev.add_(1)
+        self._counters_dev.add_(1)
 
     def advance(self, L: int = 1) -> None:
         """Host bookkeeping of ``L`` tokens written by ``append_at`` in every
