@@ -637,12 +637,27 @@ __global__ __launch_bounds__(kThreads) void head_gemv_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
-  // adjacent threads read adjacent k of one row (coalesced), 8 loads in flight
-#pragma unroll 8
-  for (int i = tid; i < K * BM; i += kThreads) {
+  // adjacent threads read adjacent k of one row (coalesced).  Every load is
+  // unconditional (dead slots reread row 0, column 0) and all are issued
+  // before the first store: a conditional load is waited for on its own.
+  constexpr int kStage = kHgMaxK * BM / kThreads;
+  uint16_t xr[kStage];
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int i = tid + j * kThreads;
     const int b = i / K;
     const int k = i - b * K;
-    xs[k][b] = b < B ? bf2f(x[(static_cast<size_t>(b) * H + h) * x_stride + k]) : 0.f;
+    const bool live = i < K * BM && b < B;
+    xr[j] = x[(static_cast<size_t>(live ? b : 0) * H + h) * x_stride + (live ? k : 0)];
+  }
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int i = tid + j * kThreads;
+    if (i < K * BM) {
+      const int b = i / K;
+      const int k = i - b * K;
+      xs[k][b] = b < B ? bf2f(xr[j]) : 0.f;
+    }
   }
   __syncthreads();
   const int NL = NW / 8;      // lanes across the workgroup's part of one weight row
