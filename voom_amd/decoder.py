@@ -283,6 +283,10 @@ class PagedDecoder:
         # the replays read these tables: they live as long as the graph does,
         # also after a later capture replaces self._rope_rows
         graph.voom_rope_rows = self._rope_rows
+        # and the library workspaces the captured launches point into: a later
+        # call that grows one replaces it in the cache, and the old buffer
+        # must outlive the graph
+        graph.voom_workspaces = list(ops._WORKSPACES.values())
         return graph, tok, nxt
 
     @torch.no_grad()

@@ -521,7 +521,7 @@ def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, token: torch.Tensor, *
     for t in (token, token_copy):
         _require(t is None or (t.dtype == torch.int64 and t.numel() >= 1), "int64 token outputs")
     need = 8 * ((N + 15) // 16)
-    ws = workspace(dev, need, tag=3)
+    ws = workspace(dev, need, tag=5)
     _lib.call("voom_lm_head_argmax", _ptr(x), _ptr(delta), _ptr(ln_weight), float(eps),
               _ptr(weight), N, K, _ptr(ws), ws.numel(), _ptr(token), _ptr(token_copy),
               _stream(stream))
