@@ -144,3 +144,31 @@ def test_graph_decode_matches_eager_decode():
         logits = dec.forward(torch.tensor([[want]], device="cuda"), kv_e2)
         want = int(logits[0, -1].argmax())
     assert int(nxt[0]) == want
+
+
+def test_captured_step_survives_a_grown_workspace():
+    """A captured decode step points into the library's cached workspaces; a
+    later call that grows one (a larger vocabulary through lm_head_argmax)
+    replaces the cached buffer, and the replays must still be right."""
+    from voom_amd import ops
+    print("[decoder] graph after workspace growth", flush=True)
+    cfg = DecoderConfig(num_hidden_layers=2)
+    dec = PagedDecoder(cfg, random_weights(cfg, seed=9))
+    prompt = torch.randint(0, cfg.vocab_size, (1, 20), generator=torch.Generator().manual_seed(3))
+    kv_e, kv_g = dec.new_cache(), dec.new_cache()
+    eager, _, _ = dec.generate(prompt, 6, kv_e)
+    logits = dec.forward(prompt.cuda(), kv_g, last_only=True)
+    first = int(logits[0, -1].argmax())
+    graph, tok, nxt = dec.capture_decode(kv_g, kv_g.offset + 6)
+    # grow the argmax workspace well past the captured one
+    big = torch.zeros((4 * cfg.vocab_size, cfg.hidden_size), dtype=torch.bfloat16, device="cuda")
+    ops.lm_head_argmax(torch.zeros((cfg.hidden_size,), dtype=torch.bfloat16, device="cuda"),
+                       big, torch.zeros((1,), dtype=torch.int64, device="cuda"))
+    torch.cuda.synchronize()
+    out = [first]
+    tok.fill_(first)
+    while len(out) < 6:
+        graph.replay()
+        kv_g.advance(1)
+        out.append(int(nxt[0]))
+    assert out == eager
