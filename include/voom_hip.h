@@ -107,6 +107,15 @@ int voom_merge_attn_states(const void* o_a, const float* lse_a, const void* o_b,
                            const float* lse_b, void* out, float* lse_out, int rows,
                            int head_dim, hipStream_t stream);
 
+/* Fold a bf16 attention state (o_b [rows, head_dim], lse_b [rows]) over a key
+ * set disjoint from the accumulator's into an fp32 running state (o_acc
+ * [rows, head_dim], lse_acc [rows]) in place; init != 0 sets the state to
+ * (o_b, lse_b).  The running output stays fp32 across any number of folds
+ * (rounded once by the caller), as the reference's online key tiles keep fp32
+ * (max, sum, acc) across tiles (runtime/glm.py:165-196). */
+int voom_fold_attn_state(float* o_acc, float* lse_acc, const void* o_b, const float* lse_b,
+                         int rows, int head_dim, int init, hipStream_t stream);
+
 /* voom_mla_head_gemv: y[b, h, n] = bf16(sum_k x[b, h, k] w[h, k, n]), fp32
  * sums, for the few query rows of a decode step -- the absorption products
  * q_nope . W_UK (runtime/glm.py:129-132) and weighted_c . W_UV

@@ -117,3 +117,19 @@ def project(out_heads: np.ndarray, o_proj: np.ndarray) -> np.ndarray:
     """[B,H,L,dv] -> [B,L,hidden] through o_proj (runtime/glm.py:203-210)."""
     B, H, L, dv = out_heads.shape
     return out_heads.transpose(0, 2, 1, 3).reshape(B, L, H * dv) @ o_proj.T
+
+
+def absorbed_weighted_c_torch(q_lat, lat, dr: int, scale: float):
+    """The dense decode contraction of absorbed_weighted_c (L = 1, bf16 cache) in
+    torch on the CPU, for the timed CPU baseline: fp32 scores of the bf16
+    operands rounded to bf16 as MLX's einsum output (runtime/glm.py:133-141),
+    softmax in fp32 cast to bf16 (:157-161), then P . c rounded to bf16
+    (:162-164).  q_lat [B, H, C + dr] and lat [B, S, C + dr] bf16 CPU tensors;
+    returns weighted_c [B, H, C] as fp32 values of bf16 numbers."""
+    import torch
+
+    c = lat[..., :-dr]
+    s = torch.bmm(q_lat.float(), lat.float().transpose(1, 2))
+    s = s.to(torch.bfloat16).float() * scale
+    p = torch.softmax(s, dim=-1).to(torch.bfloat16).float()
+    return torch.bmm(p, c.float()).to(torch.bfloat16).float()

@@ -88,3 +88,44 @@ def paged_decode_lse(q: np.ndarray, k_pages: np.ndarray, block_table: np.ndarray
             m = s.max()
             lse[b, h] = m + np.log(np.exp(s - m).sum())
     return lse
+
+
+def paged_decode_torch(q, k_pages, v_pages, block_table, ctx_lens, scale: float):
+    """The same decode in torch on the CPU, for the timed CPU baseline.
+
+    The reference's own CPU path: concatenate each sequence's pages in logical
+    order (runtime/kv_paged.py:164-181), then one fp32 scaled-dot-product
+    attention call per sequence with the GQA broadcast inside it
+    (mx.fast.scaled_dot_product_attention, runtime/layer_runner.py:170-180;
+    here torch.nn.functional.scaled_dot_product_attention with enable_gqa).
+    q [B, NQ, D], k_pages / v_pages [P, NKV, BLOCK, D] CPU tensors of any float
+    dtype (bf16 pages are widened to fp32 after the gather), block_table
+    [B, max_pages] and ctx_lens [B] integer arrays.  Returns fp32 [B, NQ, D].
+    """
+    import torch
+
+    B, NQ, D = q.shape
+    BLOCK = k_pages.shape[2]
+    NKV = k_pages.shape[1]
+    out = torch.zeros((B, NQ, D), dtype=torch.float32)
+    for b in range(B):
+        ctx = int(ctx_lens[b])
+        if ctx == 0:
+            continue
+        n_pages = -(-ctx // BLOCK)
+        ids = torch.as_tensor(np.asarray(block_table[b][:n_pages], dtype=np.int64))
+        k = k_pages.index_select(0, ids).transpose(0, 1).reshape(NKV, n_pages * BLOCK, D)
+        v = v_pages.index_select(0, ids).transpose(0, 1).reshape(NKV, n_pages * BLOCK, D)
+        out[b] = sdpa_decode_torch(q[b], k[:, :ctx], v[:, :ctx], scale)
+    return out
+
+
+def sdpa_decode_torch(q, k, v, scale: float):
+    """One query token per head over logical K/V in torch on the CPU:
+    q [NQ, D], k / v [NKV, S, D] -> fp32 [NQ, D] (the reference's SDPA call,
+    runtime/layer_runner.py:179-180, with the GQA broadcast)."""
+    import torch.nn.functional as F
+
+    return F.scaled_dot_product_attention(q.float()[None, :, None, :], k.float()[None],
+                                          v.float()[None], scale=scale,
+                                          enable_gqa=True)[0, :, 0]

@@ -146,3 +146,22 @@ def test_empty_context_gives_zeros():
     k = np.ones((1, 1, 4, 8), dtype=np.float32)
     out = opa.paged_decode(np.ones((1, 2, 8), np.float32), k, k, np.array([[0]]), np.array([0]), 1.0)
     assert np.all(out == 0)
+
+
+@pytest.mark.parametrize("ctx", [[1, 5, 19], [32, 33, 0]])
+def test_torch_cpu_restatement_matches_fp64_numpy(ctx):
+    """The torch-CPU SDPA restatement (the timed CPU baseline) agrees with the
+    numpy restatement evaluated in fp64, itself pinned by the brute force
+    above: a wrong GQA map or page order in either fails here."""
+    import torch
+
+    rng = np.random.default_rng(7 + sum(ctx))
+    P, NKV, BLOCK, D, NQ = 16, 2, 4, 16, 8
+    k, v = make_pages(rng, P, NKV, BLOCK, D)
+    q = rng.standard_normal((3, NQ, D)).astype(np.float32)
+    table = np.stack([rng.permutation(P)[:9] for _ in range(3)])
+    lens = np.array(ctx)
+    ref = opa.paged_decode(q, k, v, table, lens, D ** -0.5, dtype=np.float64)
+    got = opa.paged_decode_torch(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                                 table, lens, D ** -0.5)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=1e-5, atol=1e-6)

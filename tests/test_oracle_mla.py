@@ -86,3 +86,22 @@ def test_bf16_rounding_is_round_to_nearest_even():
     np.testing.assert_array_equal(r, np.array([1.0, 1.0, 1.0 + 2 ** -6, -2.5, np.inf, -np.inf],
                                               np.float32))
     assert np.isnan(obf.round_bf16(np.array([np.nan], np.float32)))[0]
+
+
+def test_torch_cpu_contraction_matches_numpy_restatement():
+    """The torch-CPU dense contraction (the timed CPU baseline) agrees with the
+    pinned numpy restatement in bf16 mode up to one bf16 ulp of rounding-order
+    differences in the fp32 sums."""
+    import torch
+
+    from oracle.bf16 import round_bf16
+
+    rng = np.random.default_rng(3)
+    B, H, S, C, dr = 2, 4, 70, 32, 8
+    q_lat = round_bf16(rng.standard_normal((B, H, C + dr)).astype(np.float32))
+    lat = round_bf16(rng.standard_normal((B, S, C + dr)).astype(np.float32))
+    scale = (16 + dr) ** -0.5
+    ref = mla.absorbed_weighted_c(q_lat[:, :, None], lat, dr, scale, bf16=True)[:, :, 0]
+    got = mla.absorbed_weighted_c_torch(torch.from_numpy(q_lat).to(torch.bfloat16),
+                                         torch.from_numpy(lat).to(torch.bfloat16), dr, scale)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=2 ** -7, atol=1e-3)

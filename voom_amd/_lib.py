@@ -8,6 +8,7 @@ raise ``ValueError`` and device/runtime failures raise ``RuntimeError``.
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import threading
 from ctypes import c_float, c_int, c_size_t, c_void_p
@@ -34,6 +35,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_paged_gqa_combine": (c_int, [_P, _P, _P, _P, c_size_t, c_int, c_int, c_int, c_int,
                                        c_int, c_int, c_int, _P]),
     "voom_merge_attn_states": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, _P]),
+    "voom_fold_attn_state": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),
     "voom_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "voom_mla_absorbed_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int,
                                          c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P]),
@@ -97,7 +99,36 @@ def lib() -> ctypes.CDLL:
                 fn.restype = res
                 fn.argtypes = args
             _lib = handle
+            atexit.register(_teardown)
     return _lib
+
+
+def _teardown() -> None:
+    """At interpreter exit, before the HIP runtime's static finalisers: wait for
+    the device, then drop the cached kernel workspaces and every pinned host
+    arena, so that no device or pinned allocation of this package outlives the
+    Python objects that own it (profiler tools that trace copies finalise
+    their own state at exit too)."""
+    try:
+        import torch
+
+        if not torch.cuda.is_initialized():
+            return
+        torch.cuda.synchronize()
+        from . import host_arena, ops
+
+        ops._WORKSPACES.clear()
+        host_arena.close_all()
+        import gc
+
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        host_empty = getattr(torch._C, "_host_emptyCache", None)
+        if host_empty is not None:
+            host_empty()
+    except Exception:  # pragma: no cover - best effort at exit
+        pass
 
 
 def last_error() -> str:

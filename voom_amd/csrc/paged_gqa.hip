@@ -654,6 +654,40 @@ __global__ __launch_bounds__(kThreads) void merge_states_kernel(
   if (lse_out != nullptr && idx % D == 0) lse_out[row] = lse;
 }
 
+// Folds one bf16 attention state (o_b, lse_b) over a key set disjoint from the
+// accumulator's into an fp32 running state (o_acc, lse_acc), in place.  One
+// wavefront per row: its lanes read the row's running LSE in the same load
+// instruction, before lane 0 stores the new one, so the in-place update has no
+// cross-thread hazard.  With ``init`` the state is set to (o_b, lse_b).  The
+// running output is never re-rounded to bf16, so folding many chunks does not
+// accumulate rounding error; the caller rounds once at the end.
+__global__ __launch_bounds__(kThreads) void fold_state_kernel(
+    float* __restrict__ o_acc, float* __restrict__ lse_acc, const uint16_t* __restrict__ ob,
+    const float* __restrict__ lb, int rows, int D, int init) {
+  const int row = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (row >= rows) return;
+  float* o = o_acc + static_cast<size_t>(row) * D;
+  const uint16_t* b = ob + static_cast<size_t>(row) * D;
+  const float c = lb[row];
+  if (init) {
+    for (int d = lane; d < D; d += kWave) o[d] = bf2f(b[d]);
+    if (lane == 0) lse_acc[row] = c;
+    return;
+  }
+  const float a = lse_acc[row];
+  const float m = fmaxf(a, c);
+  if (m == -INFINITY) {  // both key sets empty: the state stays (0, -inf)
+    for (int d = lane; d < D; d += kWave) o[d] = 0.f;
+    return;
+  }
+  const float wa = __expf(a - m);
+  const float wb = __expf(c - m);
+  const float inv = 1.f / (wa + wb);
+  for (int d = lane; d < D; d += kWave) o[d] = (o[d] * wa + bf2f(b[d]) * wb) * inv;
+  if (lane == 0) lse_acc[row] = m + __logf(wa + wb);
+}
+
 size_t part_slots(int batch, int num_kv_heads, int num_splits) {
   return static_cast<size_t>(batch) * num_kv_heads + static_cast<size_t>(num_splits);
 }
@@ -884,4 +918,16 @@ extern "C" int voom_merge_attn_states(const void* o_a, const float* lse_a, const
                      static_cast<const uint16_t*>(o_b), lse_b, static_cast<uint16_t*>(out),
                      lse_out, rows, head_dim);
   return VOOM_LAUNCH_CHECK("merge_attn_states: launch");
+}
+
+extern "C" int voom_fold_attn_state(float* o_acc, float* lse_acc, const void* o_b,
+                                    const float* lse_b, int rows, int head_dim, int init,
+                                    hipStream_t stream) {
+  VOOM_REQUIRE(o_acc && lse_acc && o_b && lse_b, "fold_attn_state: null pointer");
+  VOOM_REQUIRE(rows >= 0 && head_dim > 0, "fold_attn_state: bad shape");
+  if (rows == 0) return VOOM_OK;
+  const dim3 grid(static_cast<unsigned>((rows + kWavesPerBlock - 1) / kWavesPerBlock));
+  hipLaunchKernelGGL(fold_state_kernel, grid, dim3(kThreads), 0, stream, o_acc, lse_acc,
+                     static_cast<const uint16_t*>(o_b), lse_b, rows, head_dim, init ? 1 : 0);
+  return VOOM_LAUNCH_CHECK("fold_attn_state: launch");
 }

@@ -221,12 +221,14 @@ class PagedDecoder:
 
     # ---- one decode step in a HIP graph ------------------------------------------
 
-    def _graph_step(self, tok: torch.Tensor, nxt: torch.Tensor, kv: PagedKVCache) -> None:
+    def _graph_step(self, tok: torch.Tensor, nxt: torch.Tensor, kv: PagedKVCache,
+                    logits: torch.Tensor | None = None) -> None:
         """One token per sequence from device state only: tok [B, 1] in, the
         greedy next token written to nxt [B] and back into tok, K/V written at
         the cache's device position counter, counters advanced.  Every op is a
         device op with fixed shapes and addresses, so the step can be captured
-        and replayed; it computes what ``forward`` computes for one token."""
+        and replayed; it computes what ``forward`` computes for one token.
+        ``logits`` [B, vocab] fp32, when given, also receives the step's logits."""
         B = tok.shape[0]
         x = self.embed[tok]
         delta = None
@@ -240,6 +242,9 @@ class PagedDecoder:
             spare = torch.empty_like(x)
             for layer in range(cfg.num_hidden_layers):
                 delta, x, spare = self._block_token(x, spare, delta, layer, kv, cos, sin)
+            if logits is not None:
+                logits.copy_(ops.gemv(x, self.embed, ln_weight=self.final_norm,
+                                      eps=cfg.rms_norm_eps, delta=delta).reshape(logits.shape))
             # final norm, lm_head and argmax in two launches, no logits stored
             ops.lm_head_argmax(x, self.embed, nxt, token_copy=tok, ln_weight=self.final_norm,
                                eps=cfg.rms_norm_eps, delta=delta)
@@ -249,17 +254,21 @@ class PagedDecoder:
         for layer in range(self.cfg.num_hidden_layers):
             delta = self._block(x, delta, layer, kv, cos, sin, graph=True)
         x = self._norm(x, self.final_norm, delta)
-        logits = self._linear(x, self.embed).float()
-        nxt.copy_(logits[:, -1].argmax(-1))
+        step_logits = self._linear(x, self.embed).float()
+        if logits is not None:
+            logits.copy_(step_logits[:, -1])
+        nxt.copy_(step_logits[:, -1].argmax(-1))
         tok.copy_(nxt.view(B, 1))
         kv.step_counters()
 
     @torch.no_grad()
-    def capture_decode(self, kv: PagedKVCache, max_len: int):
+    def capture_decode(self, kv: PagedKVCache, max_len: int,
+                       logits: torch.Tensor | None = None):
         """Reserve the cache up to ``max_len`` tokens and capture one decode
         step; returns (graph, tok [B, 1], nxt [B]).  Before each replay put the
         step's input token in ``tok`` (a replay leaves its output there);
-        after it call ``kv.advance(1)``."""
+        after it call ``kv.advance(1)``.  ``logits`` [B, vocab] fp32, when
+        given, receives each replayed step's logits (teacher-forced checks)."""
         kv.reserve(max_len)
         self._rope_rows = self._rope_tables(torch.arange(max(int(max_len), 1),
                                                          device=self.device))
@@ -272,13 +281,13 @@ class PagedDecoder:
         side = torch.cuda.Stream(device=self.device)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            self._graph_step(tok, nxt, kv)
+            self._graph_step(tok, nxt, kv, logits)
         torch.cuda.current_stream().wait_stream(side)
         kv._counters_dev.sub_(1)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            self._graph_step(tok, nxt, kv)
+            self._graph_step(tok, nxt, kv, logits)
         torch.cuda.synchronize()
         # the replays read these tables: they live as long as the graph does,
         # also after a later capture replaces self._rope_rows

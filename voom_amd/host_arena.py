@@ -10,11 +10,16 @@ its slab.  Slabs are never returned to the system before ``close``.
 from __future__ import annotations
 
 import bisect
+import weakref
 from dataclasses import dataclass
 
 import torch
 
 ALIGN = 256
+
+# every open arena, so that process teardown can release the pinned slabs
+# before the runtime's own finalisers run
+_LIVE: "weakref.WeakSet[HostArena]" = weakref.WeakSet()
 
 
 @dataclass
@@ -35,6 +40,7 @@ class HostArena:
         # per slab: sorted list of (offset, size) free extents
         self._free: list[list[tuple[int, int]]] = []
         self.used_bytes = 0
+        _LIVE.add(self)
 
     @property
     def capacity(self) -> int:
@@ -85,3 +91,9 @@ class HostArena:
         self._slabs.clear()
         self._free.clear()
         self.used_bytes = 0
+
+
+def close_all() -> None:
+    """Close every open arena (process teardown)."""
+    for arena in list(_LIVE):
+        arena.close()

@@ -173,6 +173,10 @@ class _StagingRing:
     (2 x 256 MiB): every copy and every cross-stream event costs on the order
     of 0.1 ms of engine idle time on MI355X, so fewer, larger transfers keep
     the host link saturated.
+
+    A buffer is *held* from ``acquire`` until ``release`` (or ``abandon``):
+    ``next_free`` never returns a held buffer, so an upload that landed ahead
+    of its merge keeps its buffer until the merge has been enqueued.
     """
 
     def __init__(self, device: torch.device, nbuf: int = 2, nbytes: int = 256 << 20):
@@ -180,11 +184,25 @@ class _StagingRing:
         self.nbytes = nbytes
         self.bufs: list[torch.Tensor | None] = [None] * nbuf
         self.free_ev: list[torch.cuda.Event | None] = [None] * nbuf
+        self.held: set[int] = set()
         self.i = 0
 
-    def acquire(self, writer: torch.cuda.Stream, nbytes: int):
-        idx = self.i
-        self.i = (self.i + 1) % len(self.bufs)
+    def next_free(self) -> int | None:
+        """The next buffer in round-robin order that nobody holds, or None."""
+        n = len(self.bufs)
+        for k in range(n):
+            idx = (self.i + k) % n
+            if idx not in self.held:
+                return idx
+        return None
+
+    def acquire(self, writer: torch.cuda.Stream, nbytes: int, idx: int | None = None):
+        if idx is None:
+            idx = self.next_free()
+        if idx is None or idx in self.held:
+            raise RuntimeError("staging ring: every buffer is held")
+        self.i = (idx + 1) % len(self.bufs)
+        self.held.add(idx)
         buf = self.bufs[idx]
         if buf is None or buf.numel() < nbytes:
             if self.free_ev[idx] is not None:
@@ -199,6 +217,12 @@ class _StagingRing:
         ev = torch.cuda.Event()
         ev.record(last_user)
         self.free_ev[idx] = ev
+        self.held.discard(idx)
+
+    def abandon(self, idx: int, last_use: torch.cuda.Event) -> None:
+        """Give a held buffer back; the next writer waits for ``last_use``."""
+        self.free_ev[idx] = last_use
+        self.held.discard(idx)
 
 
 def budget_victims(pages: list[list], resident_pages: int, current_bytes: int,
@@ -499,6 +523,11 @@ class PagedKVCache:
         PT = self.page_positions
         B = self._batch
         total_pages = -(-int(total_len) // PT)
+        spilled = sum(1 for pages in self._pages for p in pages if not p.resident)
+        if spilled:
+            # a spilled page's table column is -1; the captured step reads the
+            # table as it is, so every page must be resident first
+            raise ValueError(f"reserve(): {spilled} pages are spilled; reload() them first")
         if total_pages * self.page_nbytes * self.num_layers > self.max_bytes:
             raise ValueError(f"{total_len} tokens exceed max_bytes={self.max_bytes}; "
                              "reserve() cannot spill")
@@ -568,6 +597,69 @@ class PagedKVCache:
                                    self.page_nbytes))
                 self._resident_closed += 1
         self._offset = end
+
+    # ---- rollback ---------------------------------------------------------------
+
+    def layer_lengths(self) -> tuple[int, ...]:
+        """Each layer's token count (KVCache.layer_lengths, runtime/kv_cache.py:139-151)."""
+        return tuple(self._len)
+
+    def trim(self, length: int) -> None:
+        """Roll every layer back to its first ``length`` positions
+        (KVCache.trim, runtime/kv_cache.py:107-137); layers already shorter are
+        left alone, and an attached ``dsa`` state is trimmed with the cache."""
+        if isinstance(length, bool) or not isinstance(length, int) or length < 0:
+            raise ValueError("trim length must be a non-negative integer")
+        self._trim_to([min(n, length) for n in self._len])
+        dsa = getattr(self, "dsa", None)
+        if dsa is not None:
+            dsa.trim(length)
+
+    def trim_layer_lengths(self, lengths) -> None:
+        """Roll each layer back to its own checkpointed length
+        (KVCache.trim_layer_lengths, runtime/kv_cache.py:153-179)."""
+        targets = tuple(int(n) for n in lengths)
+        if len(targets) != self.num_layers or any(n < 0 for n in targets):
+            raise ValueError("invalid per-layer KV rollback lengths")
+        if any(t > n for t, n in zip(targets, self._len)):
+            raise ValueError("cannot grow KV during rollback")
+        self._trim_to(list(targets))
+
+    def _trim_to(self, targets: list[int]) -> None:
+        """Cut layer l to targets[l] tokens.
+
+        Closed pages past the cut become open pages again: a resident page
+        keeps its slots and table column (so a reserved, captured decode
+        step still finds them), the page that now holds the last partial
+        tokens is reloaded first if it was spilled, and any other spilled
+        page past the cut drops its host copy and page file.
+        """
+        PT = self.page_positions
+        self._drop_prefetch()
+        for layer, n in enumerate(targets):
+            if n >= self._len[layer]:
+                continue
+            pages = self._pages[layer]
+            keep = n // PT  # pages wholly below the cut stay closed
+            partial = keep if n % PT else None  # page that holds the last tokens
+            cut = pages[keep:]
+            again = [p for p in cut if p.index == partial and not p.resident]
+            if again:
+                self.reload(again)
+            del pages[keep:]
+            for p in cut:
+                if p.resident:
+                    self._open_slots[layer][p.index] = p.slots
+                    p.slots = None
+                    self._resident_closed -= 1
+                else:
+                    self._drop_host(p)
+            self._len[layer] = n
+        self._offset = targets[0] if targets else 0
+        if getattr(self, "_counters_dev", None) is not None:
+            B = self._batch
+            self._counters_dev.copy_(torch.tensor(
+                [[self._offset] * B, [self._offset + 1] * B], dtype=torch.int32))
 
     def update(self, layer: int, k: torch.Tensor, v: torch.Tensor):
         """Append, then return the layer's full K/V [B, NKV, S, D] (kv_paged.py:143-181).
@@ -874,19 +966,20 @@ class PagedKVCache:
         return tuple((id(p.host), p.host_j, p.path) for p in pages)
 
     def _acquire(self, writer: torch.cuda.Stream, nbytes: int):
-        """Next staging buffer; an upload started ahead into it is given up
-        first (the writer then waits for that copy to land)."""
-        idx = self._ring.i
-        for layer, (_, (pidx, _buf, ev)) in list(self._prefetched.items()):
-            if pidx == idx:
+        """Next staging buffer nobody holds.  When uploads started ahead hold
+        every buffer, the oldest one not yet claimed by a reload is given up
+        (the writer then waits for that copy to land)."""
+        if self._ring.next_free() is None:
+            for layer, (_, (pidx, _buf, ev)) in list(self._prefetched.items()):
                 del self._prefetched[layer]
-                self._ring.free_ev[idx] = ev
+                self._ring.abandon(pidx, ev)
+                break
         return self._ring.acquire(writer, nbytes)
 
     def _drop_prefetch(self) -> None:
         """Forget uploads started ahead; their buffers free once the copy lands."""
         for _, (idx, _buf, ev) in getattr(self, "_prefetched", {}).values():
-            self._ring.free_ev[idx] = ev
+            self._ring.abandon(idx, ev)
         self._prefetched = {}
 
     def _take_prefetch(self, layer: int, pages: list[_Page]):
@@ -899,7 +992,7 @@ class PagedKVCache:
         if sig == self._chunk_sig(pages):
             self.prefetch_hits += 1
             return landed
-        self._ring.free_ev[landed[0]] = landed[2]
+        self._ring.abandon(landed[0], landed[2])
         return None
 
     def _prefetch(self, layer: int) -> None:
@@ -1211,13 +1304,19 @@ class PagedKVCache:
         if open_len > 0:
             res_cols.append(len(self._pages[layer]))
         res_ctx = (len(res_cols) - (1 if open_len > 0 else 0)) * PT + max(open_len, 0)
-        state: list[tuple[torch.Tensor, torch.Tensor]] = []
+        # fp32 running (o, lse): each part's bf16 output is folded in without
+        # re-rounding the running sum, so the error does not grow with the
+        # number of chunks; one rounding to bf16 at the end
+        state: list[torch.Tensor] = []
 
         def fold(o_l):
-            if state:
-                state[0] = ops.merge_attn_states(state[0][0], state[0][1], o_l[0], o_l[1])
+            o, lse = o_l
+            if not state:
+                state.extend((torch.empty(o.shape, dtype=torch.float32, device=o.device),
+                              torch.empty(lse.shape, dtype=torch.float32, device=o.device)))
+                ops.fold_attn_state(state[0], state[1], o, lse, init=True)
             else:
-                state.append(o_l)
+                ops.fold_attn_state(state[0], state[1], o, lse)
 
         if res_cols:
             t_res = self._dev_i32(self._tables_host[layer][:, res_cols], cache=True)
@@ -1233,4 +1332,4 @@ class PagedKVCache:
 
         self._stream_in(layer, spilled, stage, attend_chunk, transient=True)
         self._prefetch((layer + 1) % self.num_layers)
-        return state[0][0]
+        return state[0].to(torch.bfloat16)

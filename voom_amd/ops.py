@@ -183,6 +183,28 @@ def merge_attn_states(o_a: torch.Tensor, lse_a: torch.Tensor, o_b: torch.Tensor,
     return out, lse
 
 
+def fold_attn_state(o_acc: torch.Tensor, lse_acc: torch.Tensor, o_b: torch.Tensor,
+                    lse_b: torch.Tensor, *, init: bool = False,
+                    stream: torch.cuda.Stream | None = None) -> None:
+    """Fold a bf16 result (o_b, lse_b) over a disjoint key set into the fp32
+    running state (o_acc, lse_acc) in place (``init`` sets the state to it).
+
+    The running output stays fp32 however many chunks are folded, as the
+    reference's online key tiles keep fp32 (max, sum, acc) (runtime/glm.py:165-196).
+    """
+    _require_device(o_acc, lse_acc, o_b, lse_b)
+    _require(o_acc.dtype == torch.float32 and lse_acc.dtype == torch.float32,
+             "the running state must be float32")
+    _require(o_b.dtype == torch.bfloat16 and lse_b.dtype == torch.float32,
+             "o_b must be bf16 and lse_b float32")
+    _require(o_acc.numel() == o_b.numel(), "o_acc and o_b sizes differ")
+    D = o_b.shape[-1]
+    rows = o_b.numel() // D
+    _require(lse_acc.numel() == rows == lse_b.numel(), "lse must have one entry per row")
+    _lib.call("voom_fold_attn_state", _ptr(o_acc), _ptr(lse_acc), _ptr(o_b), _ptr(lse_b),
+              rows, D, int(bool(init)), _stream(stream))
+
+
 def append_kv(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
               v_pool: torch.Tensor, block_table: torch.Tensor, positions: torch.Tensor, *,
               stream: torch.cuda.Stream | None = None) -> None:
