@@ -40,7 +40,8 @@ extern "C" {
 /* Thread-local message describing the last non-zero return. */
 const char* voom_last_error(void);
 
-/* ABI version, bumped on any signature or layout change. */
+/* ABI version, bumped on any signature or layout change (2: checksums in the
+ * slot codec). */
 int voom_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -359,12 +360,24 @@ int voom_byteplane_split(const void* src, void* lo, void* hi, size_t n_elems,
                          hipStream_t stream);
 int voom_byteplane_merge(const void* lo, const void* hi, void* dst, size_t n_elems,
                          hipStream_t stream);
+/* sums (NULL = none): per listed slot i, sums[i] += the slot's checksum, a
+ * position-keyed word hash (word j of the slot adds fmix32(word + j *
+ * 0x9E3779B9) mod 2^32, fmix32 = MurmurHash3's finaliser).  The split sums the
+ * slot it reads, the merge the words it writes back, so equal sums mean the
+ * spilled bytes came back unchanged.  The caller zeroes sums first.  The
+ * reference has no spill checksum; this is the pinned-arena and page-file
+ * integrity check of this build. */
 int voom_byteplane_split_slots(const void* pool, const int32_t* slots, int n_slots,
                                size_t slot_bytes, int num_slots, void* lo, void* hi,
-                               hipStream_t stream);
+                               uint32_t* sums, hipStream_t stream);
 int voom_byteplane_merge_slots(const void* lo, const void* hi, void* pool,
                                const int32_t* slots, int n_slots, size_t slot_bytes,
-                               int num_slots, hipStream_t stream);
+                               int num_slots, uint32_t* sums, hipStream_t stream);
+/* Compares n checksums: status[0] += the number of mismatches, and the first
+ * mismatch stores ``tag`` (non-zero) in status[1] if it is still 0.  The
+ * status words are sticky until the caller clears them. */
+int voom_page_sums_verify(const uint32_t* expected, const uint32_t* got, int n, int tag,
+                          int32_t* status, hipStream_t stream);
 
 #ifdef __cplusplus
 }

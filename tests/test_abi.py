@@ -44,7 +44,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query():
     lib = _lib.lib()
-    assert lib.voom_abi_version() == 1
+    assert lib.voom_abi_version() == 2
     assert lib.voom_paged_gqa_workspace_bytes(16, 32, 8, 128, 2048) > 0
     assert lib.voom_paged_gqa_workspace_bytes(0, 32, 8, 128, 2048) == 0
 
@@ -75,8 +75,10 @@ def test_validation_errors_raise_value_error():
     assert rc == _lib.VOOM_EINVAL and "null pointer" in _lib.last_error()
     rc = lib.voom_paged_gqa_combine(fake, fake, None, fake, 16, 1, 4, 2, 128, 64, 1, 64, None)
     assert rc == _lib.VOOM_EINVAL and "workspace" in _lib.last_error()
-    rc = lib.voom_byteplane_split_slots(fake, fake, 1, 100, 1, fake, fake, None)
+    rc = lib.voom_byteplane_split_slots(fake, fake, 1, 100, 1, fake, fake, None, None)
     assert rc == _lib.VOOM_EINVAL and "multiple of 64" in _lib.last_error()
+    rc = lib.voom_page_sums_verify(fake, fake, 4, 0, fake, None)
+    assert rc == _lib.VOOM_EINVAL and "tag" in _lib.last_error()
 
 
 def test_runtime_error_mapping():

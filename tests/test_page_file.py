@@ -63,3 +63,40 @@ def test_rejects_malformed_files(tmp_path):
     trunc.write_bytes(good.read_bytes()[:-2])
     with pytest.raises(ValueError):
         page_file.read(trunc, [np.empty(4, np.uint8)], [np.empty(4, np.uint8)])
+
+
+def test_checksums_ride_in_the_header_and_damage_is_rejected(tmp_path):
+    meta = [{"name": "latent", "dtype": "BF16", "shape": [2, 2, 2]}]
+    lo, hi = np.arange(8, dtype=np.uint8), np.arange(8, 16, dtype=np.uint8)
+    good = tmp_path / "kv_l0_p0.vt"
+    page_file.write(good, 0, 0, meta, [lo], [hi], [False], sums=[[-5, 123456789]])
+    out_lo, out_hi = np.empty(8, np.uint8), np.empty(8, np.uint8)
+    head = page_file.read(good, [out_lo], [out_hi])
+    assert head["sums"] == [[-5, 123456789]]
+    assert np.array_equal(out_lo, lo) and np.array_equal(out_hi, hi)
+    with pytest.raises(ValueError):
+        page_file.write(tmp_path / "x.vt", 0, 0, meta, [lo], [hi], [False], sums=[[1], [2]])
+    longer = tmp_path / "kv_l0_p1.vt"
+    longer.write_bytes(good.read_bytes() + b"\x00")
+    with pytest.raises(ValueError, match="trailing"):
+        page_file.read(longer, [out_lo], [out_hi])
+    broken = tmp_path / "kv_l0_p2.vt"
+    raw = bytearray(good.read_bytes())
+    raw[10] = ord("#")  # inside the JSON header
+    broken.write_bytes(bytes(raw))
+    with pytest.raises(ValueError):
+        page_file.read(broken, [out_lo], [out_hi])
+
+
+def test_truncated_zstd_frame_is_rejected(tmp_path):
+    if not vz.available():
+        pytest.skip("libzstd not present")
+    rng = np.random.default_rng(5)
+    lo = rng.integers(0, 256, size=4096, dtype=np.uint8)
+    hi = np.repeat(np.arange(16, dtype=np.uint8), 256)
+    frame = vz.compress(hi, 1)
+    meta = [{"name": "latent", "dtype": "BF16", "shape": [1, 4, 1024]}]
+    path = tmp_path / "kv_l0_p0.vt"
+    page_file.write(path, 0, 0, meta, [lo], [frame[:-3]], [True])
+    with pytest.raises(ValueError):
+        page_file.read(path, [np.empty(4096, np.uint8)], [np.empty(4096, np.uint8)])

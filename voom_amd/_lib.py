@@ -71,8 +71,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_gather_rows": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
     "voom_byteplane_split": (c_int, [_P, _P, _P, c_size_t, _P]),
     "voom_byteplane_merge": (c_int, [_P, _P, _P, c_size_t, _P]),
-    "voom_byteplane_split_slots": (c_int, [_P, _P, c_int, c_size_t, c_int, _P, _P, _P]),
-    "voom_byteplane_merge_slots": (c_int, [_P, _P, _P, _P, c_int, c_size_t, c_int, _P]),
+    "voom_byteplane_split_slots": (c_int, [_P, _P, c_int, c_size_t, c_int, _P, _P, _P, _P]),
+    "voom_byteplane_merge_slots": (c_int, [_P, _P, _P, _P, c_int, c_size_t, c_int, _P, _P]),
+    "voom_page_sums_verify": (c_int, [_P, _P, c_int, c_int, _P, _P]),
 }
 
 

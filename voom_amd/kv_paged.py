@@ -75,6 +75,12 @@ class KVStats:
         return base
 
 
+class KVIntegrityError(RuntimeError):
+    """Spilled bytes did not come back as they left: a page checksum did not
+    match on reload, a page file is malformed or truncated, or a compressed
+    plane does not decompress to its size."""
+
+
 class _SpillBlock:
     """Host copy of a batch of pages spilled together from one layer.
 
@@ -83,18 +89,23 @@ class _SpillBlock:
     pages (the staging ring's chunk).  A record of m pages is contiguous and
     laid out as the low planes of every tensor, then the high planes, each
     ``m * parts[t]`` long, page i of the record at ``i * parts[t]`` inside its
-    part.  A record therefore moves in one copy each way, exactly as it sits
-    in a staging buffer.  ``ready`` is recorded after the last D2H copy.
+    part, then (when ``nsum`` > 0) the pages' checksums as int32 [T, m * B],
+    page i's B slots at ``i * B`` of each tensor's row.  A record therefore
+    moves in one copy each way, exactly as it sits in a staging buffer.
+    ``ready`` is recorded after the last D2H copy.
     """
 
-    __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "live", "compressed", "pages")
+    __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "live", "compressed", "pages",
+                 "nsum")
 
-    def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int):
+    def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int,
+                 nsum: int = 0):
         self.pages: list = []
         self.block = block
         self.n_pages = n_pages
         self.parts = list(parts)
         self.chunk = chunk
+        self.nsum = nsum  # checksum words per page (T * B), 0 = none
         self.ready: torch.cuda.Event | None = None
         self.live = n_pages
         # per page: zstd frames of the high planes (one per tensor) when compressed
@@ -102,7 +113,7 @@ class _SpillBlock:
 
     @property
     def page_bytes(self) -> int:
-        return 2 * sum(self.parts)
+        return record_page_bytes(self.parts, self.nsum)
 
     def record_pages(self, r: int) -> int:
         return min(self.chunk, self.n_pages - r * self.chunk)
@@ -118,6 +129,28 @@ class _SpillBlock:
         off = r * self.chunk * self.page_bytes + part_offset(self.parts, m, which) + \
             i * self.parts[which % len(self.parts)]
         return self.block.view[off:off + self.parts[which % len(self.parts)]]
+
+    def sums(self, j: int) -> torch.Tensor:
+        """Checksums of page j: int32 [T, B] (a strided view of its record)."""
+        r, i = divmod(j, self.chunk)
+        m = self.record_pages(r)
+        T = len(self.parts)
+        B = self.nsum // T
+        rec = self.record(r)
+        return sums_view(rec, self.parts, m, self.nsum)[:, i * B:(i + 1) * B]
+
+
+def record_page_bytes(parts: list[int], nsum: int) -> int:
+    """Bytes one page takes in a record: both planes of every tensor plus its
+    ``nsum`` int32 checksums."""
+    return 2 * sum(parts) + 4 * nsum
+
+
+def sums_view(buf: torch.Tensor, parts: list[int], m: int, nsum: int) -> torch.Tensor:
+    """The int32 [T, m * B] checksum block of an m-page record/staging buffer."""
+    T = len(parts)
+    off = 2 * sum(parts) * m
+    return buf[off:off + 4 * nsum * m].view(torch.int32).view(T, (nsum // T) * m)
 
 
 def part_offset(parts: list[int], m: int, which: int) -> int:
@@ -259,7 +292,7 @@ class PagedKVCache:
                  page_positions: int = 256, resident_pages: int = 1,
                  compress_spill: bool = False, *, device=None, initial_slots: int = 0,
                  arena: HostArena | None = None, prefetch: bool = True,
-                 host_max_bytes: int | None = None):
+                 host_max_bytes: int | None = None, verify_spills: bool = True):
         if num_layers <= 0:
             raise ValueError("num_layers must be positive")
         if page_positions <= 0 or page_positions & (page_positions - 1):
@@ -290,6 +323,17 @@ class PagedKVCache:
         self.prefetch = prefetch
         self.prefetch_hits = 0
         self._prefetched: dict = {}
+        # Spill integrity: every spilled page carries per-slot checksums made
+        # by the split kernel; the merge recomputes them and a verify kernel
+        # counts mismatches into a sticky device status, which the host reads
+        # after reload() and, without blocking, at later calls.
+        self.verify_spills = verify_spills
+        self._status: torch.Tensor | None = None
+        self._status_host: torch.Tensor | None = None
+        self._status_ev: torch.cuda.Event | None = None
+        self._sum_scratch: torch.Tensor | None = None
+        self._tags: OrderedDict = OrderedDict()  # tag -> (layer, page indices)
+        self._next_tag = 1
         self._reset_state()
 
     # ---- state ------------------------------------------------------------
@@ -714,6 +758,7 @@ class PagedKVCache:
     def _place_spilled(self, layer: int, place) -> None:
         """Stream a layer's spilled pages through staging slots, calling
         ``place(page, slot_index_tensor, stage_pool)`` for each landed page."""
+        self.check_integrity(wait=False)
         spilled = [p for p in self._pages[layer] if not p.resident]
         if not spilled:
             return
@@ -791,14 +836,25 @@ class PagedKVCache:
         """Bytes of one byte plane of each pool tensor for one page (B slots)."""
         return [self._batch * pool.tensor_slot_bytes(t) // 2 for t in range(len(pool.tensors))]
 
+    def _nsum(self, pool: DevicePagePool) -> int:
+        """Checksum words per page (one per slot of each pool tensor), or 0 when
+        spills are not verified (verification needs the slot codec kernels)."""
+        if not self.verify_spills or not all(ops.slot_codec_supported(t) for t in pool.tensors):
+            return 0
+        return self._batch * len(pool.tensors)
+
+    def _record_bytes(self, pool: DevicePagePool) -> int:
+        return record_page_bytes(self._plane_parts(pool), self._nsum(pool))
+
     def _spill_plan(self, layer: int, pages: list[_Page]):
         """One host block for the layer's pages; returns its chunk work items."""
         pool = self._pool(layer)
         parts = self._plane_parts(pool)
-        page_bytes = 2 * sum(parts)
+        nsum = self._nsum(pool)
+        page_bytes = record_page_bytes(parts, nsum)
         n = len(pages)
         per_chunk = max(1, self._ring.nbytes // page_bytes)
-        sb = _SpillBlock(self.arena.alloc(n * page_bytes), n, parts, per_chunk)
+        sb = _SpillBlock(self.arena.alloc(n * page_bytes), n, parts, per_chunk, nsum)
         sb.pages = list(pages)
         self._spill_blocks.append(sb)
         for j, p in enumerate(pages):
@@ -824,10 +880,15 @@ class PagedKVCache:
                 m = len(cp)
                 slot_t = self._dev_i32([s for p in cp for s in p.slots])
                 idx, buf = self._acquire(main, m * sb.page_bytes)
+                sums = None
+                if sb.nsum:
+                    sums = sums_view(buf, sb.parts, m, sb.nsum)
+                    sums.zero_()
                 for t, tensor in enumerate(pool.tensors):
                     lo, hi = _planes(buf, sb.parts, m, t)
                     if ops.slot_codec_supported(tensor):
-                        ops.byteplane_split_slots(tensor, slot_t, lo, hi)
+                        ops.byteplane_split_slots(tensor, slot_t, lo, hi,
+                                                  sums=None if sums is None else sums[t])
                     else:
                         ops.byteplane_split(tensor.index_select(0, slot_t.long()).contiguous(),
                                             lo, hi)
@@ -875,8 +936,9 @@ class PagedKVCache:
             hi = frames if frames is not None else [sb.part(T + t, p.host_j).numpy()
                                                      for t in range(T)]
             path = page_file.page_path(self.spill_dir, p.layer, p.index)
+            sums = sb.sums(p.host_j).tolist() if sb.nsum else None
             page_file.write(path, p.layer, p.index, self._tensor_meta(p.layer), lo, hi,
-                            [frames is not None] * T)
+                            [frames is not None] * T, sums=sums)
             p.path = path
 
     def _evict_host(self) -> None:
@@ -900,21 +962,32 @@ class PagedKVCache:
         self.arena.free(sb.block)
         self._spill_blocks.remove(sb)
 
-    def _file_planes(self, p: _Page) -> list[torch.Tensor]:
-        """Planes of a page that has no host copy, read from its page file into
-        pinned buffers (low planes, then high planes)."""
+    def _file_data(self, p: _Page):
+        """Planes (low planes, then high planes) and checksums ([T, B] int32 or
+        None) of a page that has no host copy, read from its page file into
+        pinned buffers."""
         parts = self._plane_parts(self._pool(p.layer))
         bufs = [torch.empty(n, dtype=torch.uint8, pin_memory=self.arena.pin)
                 for n in parts + parts]
         T = len(parts)
-        page_file.read(p.path, [b.numpy() for b in bufs[:T]], [b.numpy() for b in bufs[T:]])
-        return bufs
+        try:
+            head = page_file.read(p.path, [b.numpy() for b in bufs[:T]],
+                                  [b.numpy() for b in bufs[T:]])
+        except (OSError, ValueError, RuntimeError) as exc:
+            raise KVIntegrityError(f"layer {p.layer} page {p.index}: {exc}") from exc
+        sums = head.get("sums")
+        if sums is not None:
+            sums = torch.tensor(sums, dtype=torch.int32)
+            if self.arena.pin:
+                sums = sums.pin_memory()
+        return bufs, sums
 
-    def _host_planes(self, p: _Page) -> list[torch.Tensor]:
-        """Pinned host tensors of a spilled page's planes: low planes of every
-        pool tensor, then high planes (decompressed when compressed)."""
+    def _host_data(self, p: _Page):
+        """Pinned host tensors of a spilled page's planes (low planes of every
+        pool tensor, then high planes, decompressed when compressed) and its
+        checksums ([T, B] int32, or None when it has none)."""
         if p.host is None:
-            return self._file_planes(p)
+            return self._file_data(p)
         sb = p.host
         T = len(sb.parts)
         planes = [sb.part(w, p.host_j) for w in range(2 * T)]
@@ -922,14 +995,19 @@ class PagedKVCache:
         if frames is not None:
             for t, frame in enumerate(frames):
                 out = torch.empty(sb.parts[t], dtype=torch.uint8, pin_memory=self.arena.pin)
-                _zstd.decompress_into(frame, out.numpy())
+                try:
+                    _zstd.decompress_into(frame, out.numpy())
+                except RuntimeError as exc:
+                    raise KVIntegrityError(
+                        f"layer {p.layer} page {p.index}: high plane {t}: {exc}") from exc
                 planes[T + t] = out
-        return planes
+        return planes, (sb.sums(p.host_j) if sb.nsum else None)
 
     def _upload_planes(self, pages: list[_Page], staging: torch.Tensor,
-                       parts: list[int]) -> None:
+                       parts: list[int], nsum: int = 0) -> None:
         """H2D the planes of ``pages`` into staging, laid out as a host record
-        (low planes of every tensor, then high planes, page-major inside each).
+        (low planes of every tensor, then high planes, page-major inside each,
+        then the checksums when ``nsum`` > 0).
 
         A chunk that is exactly one uncompressed host record, in order, moves
         in a single copy; anything else is assembled page by page.
@@ -937,29 +1015,102 @@ class PagedKVCache:
         n = len(pages)
         p0 = pages[0]
         sb = p0.host
-        if (sb is not None and p0.host_j % sb.chunk == 0 and n == sb.record_pages(p0.host_j // sb.chunk)
+        if (sb is not None and sb.nsum == nsum and p0.host_j % sb.chunk == 0
+                and n == sb.record_pages(p0.host_j // sb.chunk)
                 and all(p.host is sb and p.host_j == p0.host_j + j
                         and sb.compressed[p.host_j] is None for j, p in enumerate(pages))):
             staging.copy_(sb.record(p0.host_j // sb.chunk), non_blocking=True)
             return
         T = len(parts)
+        dst = sums_view(staging, parts, n, nsum) if nsum else None
         for j, p in enumerate(pages):
-            for w, plane in enumerate(self._host_planes(p)):
+            planes, sums = self._host_data(p)
+            for w, plane in enumerate(planes):
                 off = part_offset(parts, n, w) + j * parts[w % T]
                 staging[off:off + parts[w % T]].copy_(plane, non_blocking=True)
+            if dst is not None:
+                if sums is None:
+                    raise KVIntegrityError(f"layer {p.layer} page {p.index}: no checksums "
+                                           "were stored with the spilled page")
+                B = nsum // T
+                for t in range(T):
+                    dst[t, j * B:(j + 1) * B].copy_(sums[t], non_blocking=True)
 
     def _merge_into(self, pool: DevicePagePool, staging: torch.Tensor, n: int,
-                    parts: list[int], slots: list[int], cache: bool = False) -> None:
+                    parts: list[int], slots: list[int], cache: bool = False,
+                    tag: int = 0) -> None:
+        """Byte-plane merge of an n-page staged record into pool slots; with
+        checksums, the merged words are summed and compared with the record's
+        sums, mismatches counted into the status under ``tag``."""
         slot_t = self._dev_i32(slots, cache=cache)
+        nsum = self._nsum(pool) if tag else 0
+        got = None
+        if nsum:
+            if self._sum_scratch is None or self._sum_scratch.numel() < nsum * n:
+                self._sum_scratch = torch.empty(max(nsum * n, 4096), dtype=torch.int32,
+                                                device=self.device)
+            got = self._sum_scratch[:nsum * n].view(len(pool.tensors), -1)
+            got.zero_()
         for t, tensor in enumerate(pool.tensors):
             lo, hi = _planes(staging, parts, n, t)
             if ops.slot_codec_supported(tensor):
-                ops.byteplane_merge_slots(lo, hi, tensor, slot_t)
+                ops.byteplane_merge_slots(lo, hi, tensor, slot_t,
+                                          sums=None if got is None else got[t])
             else:
                 staged = torch.empty((len(slots),) + tuple(tensor.shape[1:]), dtype=tensor.dtype,
                                      device=self.device)
                 ops.byteplane_merge(lo, hi, staged)
                 tensor.index_copy_(0, slot_t.long(), staged)
+
+        if got is not None:
+            if self._status is None:
+                self._status = torch.zeros(2, dtype=torch.int32, device=self.device)
+            ops.page_sums_verify(sums_view(staging, parts, n, nsum), got, tag, self._status)
+
+    # ---- spill integrity -------------------------------------------------------
+
+    def _tag(self, layer: int, pages: list[_Page]) -> int:
+        """A non-zero tag naming a verified chunk in the status (the last 4096
+        are remembered for the error message)."""
+        tag = self._next_tag
+        self._next_tag = tag % 0x7FFFFFFE + 1
+        self._tags[tag] = (layer, [p.index for p in pages])
+        if len(self._tags) > 4096:
+            self._tags.popitem(last=False)
+        return tag
+
+    def _publish_status(self) -> None:
+        """Queue a copy of the device status to host memory after the merges."""
+        if self._status is None:
+            return
+        if self._status_host is None:
+            self._status_host = torch.zeros(2, dtype=torch.int32, pin_memory=self.arena.pin)
+        self._status_host.copy_(self._status, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._status_ev = ev
+
+    def check_integrity(self, wait: bool = True) -> None:
+        """Raise KVIntegrityError if a spilled page came back changed.
+
+        Every merge of spilled bytes is checked on the device against the
+        checksums the split made.  ``reload()`` and ``load()`` call this and
+        wait; attention and gathers poll it without waiting at their next call,
+        so a mismatch found during one of them is raised by a later call (or
+        here).  The count is cleared when it is raised."""
+        ev = self._status_ev
+        if ev is None or (not wait and not ev.query()):
+            return
+        ev.synchronize()
+        self._status_ev = None
+        bad, tag = (int(v) for v in self._status_host.tolist())
+        if bad:
+            self._status.zero_()
+            where = self._tags.get(tag)
+            first = (f"layer {where[0]}, pages {where[1]}" if where is not None
+                     else "an earlier reload")
+            raise KVIntegrityError(f"{bad} spilled page slot(s) failed their checksum on "
+                                   f"reload (first in {first})")
 
     @staticmethod
     def _chunk_sig(pages: list[_Page]) -> tuple:
@@ -1006,18 +1157,32 @@ class PagedKVCache:
         spilled = [p for p in self._pages[layer] if not p.resident]
         if not spilled:
             return
-        parts = self._plane_parts(self._stage_pool(layer))
-        per_chunk = max(1, self._ring.nbytes // (2 * sum(parts)))
+        stage = self._stage_pool(layer)
+        parts = self._plane_parts(stage)
+        nsum = self._nsum(stage)
+        rec = record_page_bytes(parts, nsum)
+        per_chunk = max(1, self._ring.nbytes // rec)
         cp = spilled[:per_chunk]
         copy = self._stream()
         for sb in {id(p.host): p.host for p in cp if p.host is not None}.values():
             copy.wait_event(sb.ready)
-        idx, buf = self._acquire(copy, 2 * len(cp) * sum(parts))
-        with torch.cuda.stream(copy):
-            self._upload_planes(cp, buf, parts)
+        idx, buf = self._acquire(copy, len(cp) * rec)
+        self._guarded_upload(copy, idx, buf, cp, parts, nsum)
         ev = torch.cuda.Event()
         ev.record(copy)
         self._prefetched[layer] = (self._chunk_sig(cp), (idx, buf, ev))
+
+    def _guarded_upload(self, copy: torch.cuda.Stream, idx: int, buf: torch.Tensor,
+                        pages: list[_Page], parts: list[int], nsum: int) -> None:
+        """_upload_planes on the side stream; if it raises (a page that cannot
+        be read back), the staging buffer is given back before the error
+        propagates, after whatever copies were already queued into it."""
+        try:
+            with torch.cuda.stream(copy):
+                self._upload_planes(pages, buf, parts, nsum)
+        except BaseException:
+            self._ring.release(idx, copy)
+            raise
 
     def _stream_in(self, layer: int, pages: list[_Page], target: DevicePagePool, consume,
                    transient: bool) -> None:
@@ -1045,9 +1210,12 @@ class PagedKVCache:
         t0 = time.perf_counter()
         chunks = []
         n_pages = 0
+        verified = False
         for layer, pages, target, consume, transient in jobs:
             parts = self._plane_parts(target)
-            per_chunk = max(1, self._ring.nbytes // (2 * sum(parts)))
+            nsum = self._nsum(target)
+            verified |= nsum > 0
+            per_chunk = max(1, self._ring.nbytes // record_page_bytes(parts, nsum))
             if transient:
                 target.ensure_capacity(nbuf * per_chunk * B)
             for sb in {id(p.host): p.host for p in pages if p.host is not None}.values():
@@ -1055,23 +1223,28 @@ class PagedKVCache:
             for c0 in range(0, len(pages), per_chunk):
                 cp = pages[c0:c0 + per_chunk]
                 ahead = self._take_prefetch(layer, cp) if transient and c0 == 0 else None
-                chunks.append((cp, target, consume, transient, parts, per_chunk, ahead))
+                chunks.append((layer, cp, target, consume, transient, parts, nsum, per_chunk,
+                               ahead))
             n_pages += len(pages)
         for w0 in range(0, len(chunks), nbuf):
             window = chunks[w0:w0 + nbuf]
             landed = []
-            for cp, target, consume, transient, parts, per_chunk, ahead in window:
+            for layer, cp, target, consume, transient, parts, nsum, per_chunk, ahead in window:
                 if ahead is not None:
                     landed.append(ahead)
                     continue
-                idx, buf = self._acquire(copy, 2 * len(cp) * sum(parts))
-                with torch.cuda.stream(copy):
-                    self._upload_planes(cp, buf, parts)
+                idx, buf = self._acquire(copy, len(cp) * record_page_bytes(parts, nsum))
+                try:
+                    self._guarded_upload(copy, idx, buf, cp, parts, nsum)
+                except KVIntegrityError:
+                    for held, _, _ in landed:  # this window's other buffers
+                        self._ring.release(held, copy)
+                    raise
                 ev = torch.cuda.Event()
                 ev.record(copy)
                 landed.append((idx, buf, ev))
-            for (cp, target, consume, transient, parts, per_chunk, _), (idx, buf, ev) in zip(
-                    window, landed):
+            for (layer, cp, target, consume, transient, parts, nsum, per_chunk, _), \
+                    (idx, buf, ev) in zip(window, landed):
                 main.wait_event(ev)
                 m = len(cp)
                 if transient:
@@ -1079,9 +1252,12 @@ class PagedKVCache:
                     slots = list(range(base, base + m * B))
                 else:
                     slots = target.allocate(B * m)
-                self._merge_into(target, buf, m, parts, slots, cache=transient)
+                self._merge_into(target, buf, m, parts, slots, cache=transient,
+                                 tag=self._tag(layer, cp) if nsum else 0)
                 self._ring.release(idx, main)
                 consume(cp, slots)
+        if verified:
+            self._publish_status()
         self.stats.reloads += n_pages
         self.stats.reload_s += time.perf_counter() - t0
 
@@ -1089,9 +1265,11 @@ class PagedKVCache:
         """Make spilled pages resident again in fresh pool slots; returns the count.
 
         Uploads run on the cache's side stream (or ``stream``), merges on the
-        current stream; nothing blocks the host except compressed pages,
-        which are decompressed on the host first.
+        current stream.  The host waits at the end for the pages' checksums
+        (KVIntegrityError when a page came back changed); compressed pages are
+        also decompressed on the host first.
         """
+        self.check_integrity(wait=False)
         if pages is None:
             pages = [p for layer in self._pages for p in layer if not p.resident]
         pages = [self._pages[p[0]][p[1]] if isinstance(p, tuple) else p for p in pages]
@@ -1121,6 +1299,7 @@ class PagedKVCache:
             self._set_table_cols(layer, {p.index: p.slots for p in lp})
             for p in lp:
                 self._drop_host(p)
+        self.check_integrity()
         return len(pages)
 
     def _drop_host(self, p: _Page) -> None:
@@ -1156,6 +1335,7 @@ class PagedKVCache:
             out.extend(self._slot_contents(stage, self._dev_i32(slots).long()))
 
         self._stream_in(p.layer, [p], stage, grab, transient=True)
+        self.check_integrity()
         return tuple(out)
 
     # ---- fused decode attention --------------------------------------------
@@ -1289,6 +1469,7 @@ class PagedKVCache:
         S = self._len[layer]
         pool = self._pool(layer)
         spilled = [p for p in self._pages[layer] if not p.resident]
+        self.check_integrity(wait=False)
         if not spilled:
             ctx = torch.full((B,), S, dtype=torch.int32, device=self.device)
             out = run(pool, self._tables[layer], ctx, False)

@@ -274,38 +274,68 @@ def byteplane_merge(lo: torch.Tensor, hi: torch.Tensor, out: torch.Tensor, *,
 
 
 def byteplane_split_slots(pool: torch.Tensor, slots: torch.Tensor, lo: torch.Tensor,
-                          hi: torch.Tensor, *, stream: torch.cuda.Stream | None = None) -> None:
-    """Gather pool[slots[i]] and split it into plane chunk i (slot_bytes/2 bytes each)."""
+                          hi: torch.Tensor, *, sums: torch.Tensor | None = None,
+                          stream: torch.cuda.Stream | None = None) -> None:
+    """Gather pool[slots[i]] and split it into plane chunk i (slot_bytes/2 bytes each).
+
+    ``sums`` (int32 [n], zeroed by the caller): each listed slot's checksum is
+    added in (see voom_byteplane_split_slots)."""
     _u16_view(pool)
-    _require_device(pool, slots, lo, hi)
+    _require_device(pool, slots, lo, hi, sums)
     _require(slots.dtype == torch.int32 and slots.dim() == 1, "slots must be 1-D int32")
     num_slots = pool.shape[0]
     slot_bytes = pool[0].numel() * 2
     n = slots.numel()
     _require(lo.numel() >= n * slot_bytes // 2 and hi.numel() >= n * slot_bytes // 2,
              "plane buffers too small")
+    _check_sums(sums, n)
     _lib.call("voom_byteplane_split_slots", _ptr(pool), _ptr(slots), n, slot_bytes, num_slots,
-              _ptr(lo), _ptr(hi), _stream(stream))
+              _ptr(lo), _ptr(hi), _ptr(sums), _stream(stream))
 
 
 def byteplane_merge_slots(lo: torch.Tensor, hi: torch.Tensor, pool: torch.Tensor,
-                          slots: torch.Tensor, *, stream: torch.cuda.Stream | None = None) -> None:
-    """Merge plane chunk i back into pool[slots[i]] (scatter, bit-exact)."""
+                          slots: torch.Tensor, *, sums: torch.Tensor | None = None,
+                          stream: torch.cuda.Stream | None = None) -> None:
+    """Merge plane chunk i back into pool[slots[i]] (scatter, bit-exact); with
+    ``sums`` the checksum of each slot's merged words is added into sums[i]."""
     _u16_view(pool)
-    _require_device(pool, slots, lo, hi)
+    _require_device(pool, slots, lo, hi, sums)
     _require(slots.dtype == torch.int32 and slots.dim() == 1, "slots must be 1-D int32")
     num_slots = pool.shape[0]
     slot_bytes = pool[0].numel() * 2
     n = slots.numel()
     _require(lo.numel() >= n * slot_bytes // 2 and hi.numel() >= n * slot_bytes // 2,
              "plane buffers too small")
+    _check_sums(sums, n)
     _lib.call("voom_byteplane_merge_slots", _ptr(lo), _ptr(hi), _ptr(pool), _ptr(slots), n,
-              slot_bytes, num_slots, _stream(stream))
+              slot_bytes, num_slots, _ptr(sums), _stream(stream))
+
+
+def _check_sums(sums: torch.Tensor | None, n: int) -> None:
+    if sums is not None:
+        _require(sums.dtype == torch.int32 and sums.numel() >= n,
+                 "sums must be int32 with one entry per listed slot")
+
+
+def page_sums_verify(expected: torch.Tensor, got: torch.Tensor, tag: int,
+                     status: torch.Tensor, *, stream: torch.cuda.Stream | None = None) -> None:
+    """Count the checksums in ``got`` that differ from ``expected`` into
+    status[0] and, for the first mismatch, store ``tag`` in status[1]."""
+    _require_device(expected, got, status)
+    _require(expected.dtype == got.dtype == status.dtype == torch.int32,
+             "checksums and status must be int32")
+    _require(expected.numel() == got.numel() and status.numel() >= 2, "checksum sizes differ")
+    _require(tag != 0, "tag must be non-zero")
+    _lib.call("voom_page_sums_verify", _ptr(expected), _ptr(got), expected.numel(), int(tag),
+              _ptr(status), _stream(stream))
 
 
 def slot_codec_supported(pool: torch.Tensor) -> bool:
     """True when one pool slot is a whole number of 64-byte lines (slot kernels)."""
-    return (pool[0].numel() * 2) % 64 == 0
+    slot_elems = 1
+    for d in pool.shape[1:]:
+        slot_elems *= int(d)
+    return (slot_elems * 2) % 64 == 0
 
 
 def mla_workspace_bytes(batch: int, num_heads: int, num_ranges: int = 0) -> int:

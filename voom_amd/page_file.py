@@ -7,13 +7,15 @@ byte plane.  A page file holds every tensor of one page of one layer (K and
 V^T blocks, or the latent rows) in the device page layout, B slots after each
 other:
 
-    {"format": "voom-kv-page", "version": 2, "layer": L, "page": P,
+    {"format": "voom-kv-page", "version": 3, "layer": L, "page": P,
      "tensors": [{"name": "k", "dtype": "BF16", "shape": [B, NKV, PT, D],
                   "lo": n, "hi": n, "hi_z": m | null},
-                 {"name": "v", "dtype": "BF16", "shape": [B, NKV, PT/VB, D, VB], ...}]}
+                 {"name": "v", "dtype": "BF16", "shape": [B, NKV, PT/VB, D, VB], ...}],
+     "sums": [[c_0, ..., c_{B-1}] per tensor] | null}
 
-Version 2 stores V as V^T blocks of VB = min(PT, 32) tokens (version 1 held
-one [D, PT] V^T per page).
+Version 2 stored V as V^T blocks of VB = min(PT, 32) tokens (version 1 held
+one [D, PT] V^T per page); version 3 adds ``sums``, the per-slot checksums the
+spill kernel made (int32 values), which the reload verifies on the device.
 
 ``hi_z`` is the compressed length of the high plane, or null when it is
 stored raw (``hi`` bytes).  Writing goes through a temporary name and an
@@ -32,7 +34,7 @@ import numpy as np
 from . import zstd as _zstd
 
 FORMAT = "voom-kv-page"
-VERSION = 2
+VERSION = 3
 
 
 def page_path(spill_dir: Path, layer: int, page: int) -> Path:
@@ -41,11 +43,13 @@ def page_path(spill_dir: Path, layer: int, page: int) -> Path:
 
 
 def write(path: Path, layer: int, page: int, tensors: list[dict],
-          lo_planes: list, hi_planes: list, hi_compressed: list[bool]) -> int:
+          lo_planes: list, hi_planes: list, hi_compressed: list[bool],
+          sums: list | None = None) -> int:
     """Write one page file; returns its size in bytes.
 
     ``tensors``: [{"name", "dtype", "shape"}] per tensor; ``lo_planes`` /
-    ``hi_planes``: bytes-like planes (a zstd frame where ``hi_compressed``).
+    ``hi_planes``: bytes-like planes (a zstd frame where ``hi_compressed``);
+    ``sums``: per tensor, the page's per-slot checksums (or None).
     """
     entries = []
     for meta, lo, hi, z in zip(tensors, lo_planes, hi_planes, hi_compressed):
@@ -56,8 +60,12 @@ def write(path: Path, layer: int, page: int, tensors: list[dict],
                         "hi": lo_n, "hi_z": hi_n if z else None})
         if not z and hi_n != lo_n:
             raise ValueError("raw byte planes of one tensor must be the same size")
+    if sums is not None:
+        sums = [[int(c) for c in row] for row in sums]
+        if len(sums) != len(entries):
+            raise ValueError("one checksum row per tensor")
     head = json.dumps({"format": FORMAT, "version": VERSION, "layer": int(layer),
-                       "page": int(page), "tensors": entries}).encode()
+                       "page": int(page), "tensors": entries, "sums": sums}).encode()
     tmp = path.with_name(path.name + ".tmp")
     with open(tmp, "wb") as f:
         f.write(struct.pack("<Q", len(head)))
@@ -77,7 +85,13 @@ def read(path: Path, lo_out: list, hi_out: list) -> dict:
         if len(raw) != 8:
             raise ValueError(f"{path}: truncated header length")
         (n,) = struct.unpack("<Q", raw)
-        head = json.loads(f.read(n))
+        text = f.read(n)
+        if len(text) != n:
+            raise ValueError(f"{path}: truncated header")
+        try:
+            head = json.loads(text)
+        except ValueError as exc:
+            raise ValueError(f"{path}: malformed header: {exc}") from exc
         if head.get("format") != FORMAT or head.get("version") != VERSION:
             raise ValueError(f"{path}: not a {FORMAT} v{VERSION} file")
         ents = head["tensors"]
@@ -90,8 +104,16 @@ def read(path: Path, lo_out: list, hi_out: list) -> dict:
                 _readinto(f, hi, path)
             else:
                 frame = np.frombuffer(f.read(e["hi_z"]), dtype=np.uint8)
-                _zstd.decompress_into(frame, hi)
+                if frame.nbytes != e["hi_z"]:
+                    raise ValueError(f"{path}: truncated zstd frame ({frame.nbytes} of "
+                                     f"{e['hi_z']} bytes)")
+                try:
+                    _zstd.decompress_into(frame, hi)
+                except RuntimeError as exc:
+                    raise ValueError(f"{path}: {exc}") from exc
             _readinto(f, lo, path)
+        if f.read(1):
+            raise ValueError(f"{path}: trailing bytes after the planes")
     return head
 
 
