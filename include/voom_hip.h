@@ -78,6 +78,23 @@ int voom_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                           int page_tokens, int max_pages, int num_slots, float scale,
                           int num_splits, hipStream_t stream);
 
+/* voom_paged_gqa_decode without a workspace: the split partials live in a
+ * file-scope device array of voom_paged_gqa_noalloc_max_bytes() bytes (16 MiB)
+ * held by each device for the life of the process, so the call allocates
+ * nothing.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * voom_paged_gqa_decode minus the workspace; a request whose partials exceed
+ * the array fails with VOOM_EINVAL.  The stream must belong to the current
+ * device.  Calls that overlap on one device share the array and race. */
+size_t voom_paged_gqa_noalloc_max_bytes(void);
+int voom_paged_gqa_decode_noalloc(const void* q, const void* k_pool, const void* v_pool,
+                                  const int32_t* block_table, const int32_t* ctx_lens,
+                                  void* out, float* lse_out, int batch, int num_q_heads,
+                                  int num_kv_heads, int head_dim, int page_tokens,
+                                  int max_pages, int num_slots, float scale, int num_splits,
+                                  hipStream_t stream);
+
 /* The two halves of voom_paged_gqa_decode, for callers that time or schedule
  * them separately (same arguments, same workspace, same num_splits):
  *   voom_paged_gqa_partials  streams the pages once and leaves one partial

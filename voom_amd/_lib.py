@@ -30,6 +30,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_paged_gqa_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_size_t,
                                       c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                       c_float, c_int, _P]),
+    "voom_paged_gqa_noalloc_max_bytes": (c_size_t, []),
+    "voom_paged_gqa_decode_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int,
+                                              c_int, c_int, c_int, c_int, c_float, c_int, _P]),
     "voom_paged_gqa_partials": (c_int, [_P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int, c_int,
                                         c_int, c_int, c_int, c_int, c_float, c_int, _P]),
     "voom_paged_gqa_combine": (c_int, [_P, _P, _P, _P, c_size_t, c_int, c_int, c_int, c_int,
