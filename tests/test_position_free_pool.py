@@ -74,3 +74,156 @@ def test_invariants_raise_like_the_reference():
         cache.gather_unrotated(0)
     with pytest.raises(ValueError):
         pool.allocate(-1)
+
+
+# ---- the reference's position-free cache tests (tests/test_kv_cache.py:222-335) ----
+
+from voom_amd.position_free import ReusedRange, ToolPICPlan  # noqa: E402
+
+
+def values_of(layer: int, width: int, dim: int = 32):
+    keys = (torch.arange(width * dim, dtype=torch.float32).reshape(1, 1, width, dim)
+            + layer * 10_000)
+    return keys, keys + 1000
+
+
+def f32_pool(layers, nkv, dim, **kw):
+    return PositionFreePagePool(layers, nkv, dim, device="cpu", dtype=torch.float32, **kw)
+
+
+def test_pic_plan_shares_pages_and_releases_by_reference():
+    pool = f32_pool(2, 1, 32, min_capacity=8)
+    source = PositionFreeKVCache(pool)
+    for layer in range(2):
+        source.update_unrotated(layer, *values_of(layer, 4))
+    assert source.is_complete and pool.live_pages == 4
+    plan = ToolPICPlan(reused=(ReusedRange(0, 1, 0, "tool_capsule"),
+                               ReusedRange(2, 4, 1, "tool_capsule")),
+                       selected_positions=(1, 4), exact_prefix_tokens=0,
+                       capsule_tokens_reused=3, capsule_tokens_repaired=0)
+    dest = PositionFreeKVCache.from_pic_plan(source, plan, 5)
+    # four source pages plus two new selected pages
+    assert pool.live_pages == 6
+    assert dest.page_ids[0] == source.page_ids[0]
+    assert dest.page_ids[2:4] == source.page_ids[1:3]
+    for page_id in (dest.page_ids[0], *dest.page_ids[2:4]):
+        assert pool.reference_count(page_id) == 2
+    assert not dest.is_complete
+    for layer in range(2):
+        keys, vals = values_of(layer + 10, 2)
+        dest.write_selected(layer, (1, 4), keys, vals)
+    assert dest.is_complete
+    source.release()
+    assert pool.live_pages == 5
+    assert all(pool.reference_count(p) == 1 for p in dest.page_ids)
+    gathered, _ = dest.gather_unrotated(1)
+    assert float(gathered[0, 0, 0, 0]) == 10_000
+    assert float(gathered[0, 0, 2, 0]) == 10_032
+    assert float(gathered[0, 0, 1, 0]) == 110_000  # the selected page's own write
+    dest.release()
+    assert pool.live_pages == 0 and pool.free_pages == 6
+
+
+def test_trim_recycles_only_unreferenced_tail_pages():
+    pool = f32_pool(1, 1, 32, min_capacity=4)
+    source = PositionFreeKVCache(pool)
+    source.update_unrotated(0, *values_of(0, 4))
+    shared = source.page_ids[:2]
+    pool.retain(shared)
+    source.trim(2)
+    assert pool.live_pages == 2 and source.offset == 2
+    assert all(pool.reference_count(p) == 2 for p in shared)
+    source.release()
+    assert all(pool.reference_count(p) == 1 for p in shared)
+    pool.release(shared)
+    assert pool.live_pages == 0
+
+
+def test_live_counter_tracks_reference_transitions():
+    pool = f32_pool(1, 1, 32, min_capacity=8)
+    cache = PositionFreeKVCache(pool)
+    cache.update_unrotated(0, *values_of(0, 5))
+    assert pool.live_pages == 5 == int((pool._refs[:pool._high] > 0).sum())
+    shared = cache.page_ids[1:4]
+    pool.retain(shared)
+    assert pool.live_pages == 5
+    pool.release(shared)
+    assert pool.live_pages == 5
+    cache.trim(2)
+    assert pool.live_pages == 2
+    cache.release()
+    assert pool.live_pages == 0
+    pool.close()
+    assert pool.live_pages == 0
+
+
+def test_failed_plan_restores_the_pool():
+    pool = f32_pool(1, 1, 32, min_capacity=8)
+    source = PositionFreeKVCache(pool)
+    source.update_unrotated(0, *values_of(0, 2))
+    bad = ToolPICPlan(reused=(), selected_positions=(0, 0), exact_prefix_tokens=0,
+                      capsule_tokens_reused=0, capsule_tokens_repaired=2)
+    with pytest.raises(ValueError, match="invalid PIC selected position"):
+        PositionFreeKVCache.from_pic_plan(source, bad, 2)
+    assert pool.live_pages == 2 and pool.free_pages == 2
+    overlap = ToolPICPlan(reused=(ReusedRange(0, 2, 0, "x"),), selected_positions=(1,),
+                          exact_prefix_tokens=0, capsule_tokens_reused=2,
+                          capsule_tokens_repaired=1)
+    with pytest.raises(ValueError, match="overlapping PIC destination"):
+        PositionFreeKVCache.from_pic_plan(source, overlap, 2)
+    gap = ToolPICPlan(reused=(), selected_positions=(0,), exact_prefix_tokens=0,
+                      capsule_tokens_reused=0, capsule_tokens_repaired=1)
+    with pytest.raises(ValueError, match="uncovered positions"):
+        PositionFreeKVCache.from_pic_plan(source, gap, 3)
+    past = ToolPICPlan(reused=(ReusedRange(1, 3, 1, "x"),), selected_positions=(0,),
+                       exact_prefix_tokens=0, capsule_tokens_reused=2,
+                       capsule_tokens_repaired=1)
+    with pytest.raises(ValueError, match="invalid PIC reused position layout"):
+        PositionFreeKVCache.from_pic_plan(source, past, 3)
+    assert pool.live_pages == 2 and all(pool.reference_count(p) == 1 for p in source.page_ids)
+
+
+def test_write_selected_and_trim_errors():
+    pool = f32_pool(1, 1, 32)
+    source = PositionFreeKVCache(pool)
+    source.update_unrotated(0, *values_of(0, 3))
+    plan = ToolPICPlan(reused=(ReusedRange(0, 2, 0, "x"),), selected_positions=(2,),
+                       exact_prefix_tokens=0, capsule_tokens_reused=2, capsule_tokens_repaired=1)
+    dest = PositionFreeKVCache.from_pic_plan(source, plan, 3)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        dest.write_selected(0, (2,), *values_of(0, 2))
+    with pytest.raises(ValueError, match="outside destination"):
+        dest.write_selected(0, (7,), *values_of(0, 1))
+    dest.write_selected(0, (2,), *values_of(0, 1))
+    with pytest.raises(ValueError, match="already completed"):
+        dest.write_selected(0, (2,), *values_of(0, 1))
+    with pytest.raises(ValueError, match="cannot grow"):
+        dest.trim(4)
+    with pytest.raises(ValueError, match="integer"):
+        dest.trim(1.0)
+    incomplete = PositionFreeKVCache(f32_pool(2, 1, 32))
+    incomplete.update_unrotated(0, *values_of(0, 1))
+    with pytest.raises(ValueError, match="source position-free cache is incomplete"):
+        PositionFreeKVCache.from_pic_plan(incomplete, plan, 3)
+
+
+def test_release_is_atomic_and_reserve_growth_prevents_regrowth():
+    pool = f32_pool(1, 1, 32, min_capacity=4)
+    cache = PositionFreeKVCache(pool)
+    cache.update_unrotated(0, *values_of(0, 3))
+    ids = cache.page_ids
+    with pytest.raises(RuntimeError, match="released twice"):
+        pool.release([ids[0], ids[1], ids[1]])  # ids[1] has one reference
+    assert all(pool.reference_count(p) == 1 for p in ids)  # nothing changed
+    cache.reserve_growth(40)
+    cap = pool.capacity
+    assert cap >= 43
+    for _ in range(8):
+        cache.update_unrotated(0, *values_of(0, 5))
+    assert pool.capacity == cap and cache.offset == 43
+    assert cache.block_table().tolist() == list(cache.page_ids)
+    assert cache.key_positions().tolist() == list(range(43))
+    cache.trim(10)
+    assert cache.block_table().tolist() == list(cache.page_ids)[:10]
+    cache.update_unrotated(0, *values_of(0, 2))
+    assert cache.block_table().tolist() == list(cache.page_ids)
