@@ -113,16 +113,24 @@ def test_attention_reload_reports_at_the_next_call():
     kv.release()
 
 
-def test_truncated_zstd_frame_is_refused():
-    print("[integrity] truncated zstd frame", flush=True)
+def test_damaged_zstd_frame_in_a_page_file_is_refused(tmp_path):
+    print("[integrity] damaged zstd frame in a page file", flush=True)
+    import struct
+
     gen = torch.Generator(device="cuda").manual_seed(54)
-    kv, _ = make_cache(gen, compress_spill=True)
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, spill_dir=tmp_path, page_positions=64,
+                      resident_pages=1, compress_spill=True, host_max_bytes=1)
+    kv.append(0, randn_bf16((2, 2, 400, 128), gen), randn_bf16((2, 2, 400, 128), gen))
     kv.spill([(0, 0), (0, 1)])
     p = kv._pages[0][1]
-    frames = p.host.compressed[p.host_j]
-    frames[0] = frames[0][:-4]
-    with pytest.raises(KVIntegrityError, match="page 1"):
+    assert p.host is None and p.path is not None  # on disk only, high planes compressed
+    raw = bytearray(p.path.read_bytes())
+    (hlen,) = struct.unpack("<Q", raw[:8])
+    raw[8 + hlen + 40] ^= 0xFF  # inside the first tensor's zstd frame
+    p.path.write_bytes(bytes(raw))
+    with pytest.raises(KVIntegrityError, match="layer 0"):
         kv.reload()
+    assert kv.stats.spill_bytes_compressed > 0
     kv.release()
 
 

@@ -37,8 +37,11 @@ Where the reference differs by platform:
 
 from __future__ import annotations
 
+import os
+import threading
 import time
 from collections import OrderedDict
+from concurrent.futures import Future, ThreadPoolExecutor
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -95,8 +98,8 @@ class _SpillBlock:
     ``ready`` is recorded after the last D2H copy.
     """
 
-    __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "live", "compressed", "pages",
-                 "nsum")
+    __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "rec_ready", "live", "pages",
+                 "nsum", "jobs")
 
     def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int,
                  nsum: int = 0):
@@ -106,10 +109,17 @@ class _SpillBlock:
         self.parts = list(parts)
         self.chunk = chunk
         self.nsum = nsum  # checksum words per page (T * B), 0 = none
-        self.ready: torch.cuda.Event | None = None
+        self.ready: torch.cuda.Event | None = None  # after the block's last D2H copy
+        self.rec_ready: dict[int, torch.cuda.Event] = {}  # after each record's copy
         self.live = n_pages
-        # per page: zstd frames of the high planes (one per tensor) when compressed
-        self.compressed: list[list[np.ndarray] | None] = [None] * n_pages
+        # host work queued on the spill (compression, page files), per page group
+        self.jobs: list[Future] = []
+
+    def wait_jobs(self) -> None:
+        """Wait for the block's queued host work and re-raise its first error."""
+        jobs, self.jobs = self.jobs, []
+        for job in jobs:
+            job.result()
 
     @property
     def page_bytes(self) -> int:
@@ -171,7 +181,7 @@ def _planes(buf: torch.Tensor, parts: list[int], m: int, t: int):
 class _Page:
     """One closed page of one layer: a pool slot per sequence, or a host copy."""
 
-    __slots__ = ("cache", "layer", "index", "slots", "host", "host_j", "nbytes", "path",
+    __slots__ = ("cache", "layer", "index", "slots", "host", "host_j", "nbytes", "_path",
                  "_compressed")
 
     def __init__(self, cache: "PagedKVCache", layer: int, index: int, slots: list[int],
@@ -183,12 +193,20 @@ class _Page:
         self.host: _SpillBlock | None = None
         self.host_j = 0
         self.nbytes = nbytes
-        self.path: Path | None = None
+        self._path: Path | None = None
         self._compressed = False
 
     @property
     def resident(self) -> bool:
         return self.slots is not None
+
+    @property
+    def path(self) -> Path | None:
+        """The page file of a spilled page (spill_dir), once it is written: a
+        file still being written in the background is waited for."""
+        if self.host is not None and self.host.jobs:
+            self.host.wait_jobs()
+        return self._path
 
     def load(self):
         """The page's contents, bit-exact: (K, V) as [B, NKV, page_positions, D],
@@ -314,7 +332,12 @@ class PagedKVCache:
         self.initial_slots = initial_slots
         self.arena = arena if arena is not None else HostArena()
         self._own_arena = arena is None
-        self.stats = KVStats()
+        self._stats = KVStats()
+        self._stats_lock = threading.Lock()
+        # host work of spills (zstd of the high planes, page files) runs on
+        # worker threads: the caller never waits for a D2H copy to land
+        self._workers: ThreadPoolExecutor | None = None
+        self._zstd_scratch = threading.local()
         self._copy_stream: torch.cuda.Stream | None = None
         self._ring = _StagingRing(self.device)
         self._i32_cache: OrderedDict = OrderedDict()
@@ -356,6 +379,18 @@ class PagedKVCache:
         self._tables_host: list[np.ndarray | None] = [None] * L
         # ("kv", B, NKV, D) or ("latent", B, latent_dim), fixed by the first write
         self._geom: tuple | None = None
+
+    @property
+    def stats(self) -> KVStats:
+        """Spill and reload counters (KVStats); compression counters include
+        every spill so far (queued host work is waited for)."""
+        self._wait_host_work()
+        return self._stats
+
+    def _wait_host_work(self) -> None:
+        for sb in list(getattr(self, "_spill_blocks", ())):
+            if sb.jobs:
+                sb.wait_jobs()
 
     def _set_geometry(self, geom: tuple, dtype: torch.dtype) -> None:
         if self._geom is None:
@@ -773,6 +808,7 @@ class PagedKVCache:
 
     def release(self) -> None:
         """Free device slots and host copies; offset and nbytes return to 0."""
+        self._wait_host_work()
         if self._own_arena:
             self.arena.close()
         else:
@@ -782,7 +818,7 @@ class PagedKVCache:
                     if p.host is not None and id(p.host) not in seen:
                         seen.add(id(p.host))
                         self.arena.free(p.host.block)
-        paths = {p.path for pages in self._pages for p in pages if p.path is not None}
+        paths = {p._path for pages in self._pages for p in pages if p._path is not None}
         self._reset_state()
         for path in paths:
             try:
@@ -803,9 +839,9 @@ class PagedKVCache:
         ``None`` applies the budget policy.  Returns the number of pages spilled.
         """
         if pages is None:
-            before = self.stats.spills
+            before = self._stats.spills
             self._enforce_budget()
-            return self.stats.spills - before
+            return self._stats.spills - before
         pages = [self._pages[p[0]][p[1]] if isinstance(p, tuple) else p for p in pages]
         pages = [p for p in pages if p.resident]
         by_layer: dict[int, list[_Page]] = {}
@@ -823,13 +859,12 @@ class PagedKVCache:
                 p.slots = None
             self._resident_closed -= len(lp)
             self._set_table_cols(layer, {p.index: None for p in lp})
-        if self.compress_spill:
-            self._compress_spilled(pages)
+        if self.compress_spill or self.spill_dir is not None:
+            self._queue_host_work(pages)
         if self.spill_dir is not None:
-            self._write_files(pages)
             self._evict_host()
-        self.stats.spills += len(pages)
-        self.stats.spill_s += time.perf_counter() - t0
+        self._stats.spills += len(pages)
+        self._stats.spill_s += time.perf_counter() - t0
         return len(pages)
 
     def _plane_parts(self, pool: DevicePagePool) -> list[int]:
@@ -902,18 +937,87 @@ class PagedKVCache:
                 self._ring.release(idx, copy)
                 sb.ready = torch.cuda.Event()
                 sb.ready.record(copy)
+                sb.rec_ready[rec] = sb.ready
 
-    def _compress_spilled(self, pages: list[_Page]) -> None:
-        """zstd level 1 on each high plane; low planes stay raw (formats/packed.py:49-50)."""
+    # pages per background job: small enough to spread one record over the
+    # workers, large enough that a job is milliseconds of zstd
+    _HOST_JOB_PAGES = 64
+
+    def _queue_host_work(self, pages: list[_Page]) -> None:
+        """Queue the host side of a spill on worker threads: per group of pages
+        of one record, wait for that record's D2H copy, zstd level 1 each high
+        plane (low planes stay raw, formats/packed.py:49-50) and, with
+        spill_dir, write the page files.  Nothing here blocks the caller; the
+        raw planes stay in the arena, so reloads never decompress them."""
+        if self._workers is None:
+            try:
+                n = len(os.sched_getaffinity(0))
+            except AttributeError:  # pragma: no cover
+                n = os.cpu_count() or 1
+            self._workers = ThreadPoolExecutor(max_workers=max(1, min(16, n)),
+                                               thread_name_prefix="voom-spill")
+        groups: dict[tuple, list[_Page]] = {}
         for p in pages:
-            sb = p.host
-            sb.ready.synchronize()
-            T = len(sb.parts)
-            frames = [_zstd.compress(sb.part(T + t, p.host_j).numpy(), 1) for t in range(T)]
-            sb.compressed[p.host_j] = frames
-            p._compressed = True
-            self.stats.spill_bytes_raw += p.nbytes
-            self.stats.spill_bytes_compressed += sum(sb.parts) + sum(f.nbytes for f in frames)
+            groups.setdefault((id(p.host), p.host_j // p.host.chunk), []).append(p)
+        for (_, rec), group in groups.items():
+            sb = group[0].host
+            ev = sb.rec_ready[rec]
+            meta = self._tensor_meta(group[0].layer) if self.spill_dir is not None else None
+            for g0 in range(0, len(group), self._HOST_JOB_PAGES):
+                part = group[g0:g0 + self._HOST_JOB_PAGES]
+                sb.jobs.append(self._workers.submit(self._host_job, sb, ev, part, meta))
+
+    def _host_job(self, sb: _SpillBlock, landed: torch.cuda.Event, pages: list[_Page],
+                  meta) -> None:
+        """One background job of _queue_host_work (runs on a worker thread).
+
+        The record is viewed once as a numpy array and each high plane is
+        compressed straight from it into a per-thread buffer, so the thread
+        holds the GIL only for slicing and bookkeeping, not for copies."""
+        while not landed.query():  # sleeping releases the GIL
+            time.sleep(50e-6)
+        T = len(sb.parts)
+        r = pages[0].host_j // sb.chunk
+        m = sb.record_pages(r)
+        rec = sb.record(r).numpy()
+        lo_off = [part_offset(sb.parts, m, t) for t in range(T)]
+        hi_off = [part_offset(sb.parts, m, T + t) for t in range(T)]
+        scratch = None
+        if self.compress_spill:
+            local = self._zstd_scratch
+            scratch = getattr(local, "buf", None)
+            need = _zstd.compress_bound(max(sb.parts))
+            if scratch is None or scratch.nbytes < need:
+                scratch = local.buf = np.empty(need, dtype=np.uint8)
+        raw = comp = 0
+        for p in pages:
+            i = p.host_j - r * sb.chunk
+            his = [rec[hi_off[t] + i * sb.parts[t]:hi_off[t] + (i + 1) * sb.parts[t]]
+                   for t in range(T)]
+            frames = None
+            if scratch is not None:
+                frames = []
+                for t in range(T):
+                    n = _zstd.compress_into(his[t], scratch, 1)
+                    comp += n
+                    # only a page file keeps the frame
+                    frames.append(scratch[:n].copy() if meta is not None else None)
+                comp += sum(sb.parts)  # the raw low planes
+                raw += p.nbytes
+                p._compressed = True
+            if meta is not None:
+                los = [rec[lo_off[t] + i * sb.parts[t]:lo_off[t] + (i + 1) * sb.parts[t]]
+                       for t in range(T)]
+                path = page_file.page_path(self.spill_dir, p.layer, p.index)
+                sums = sb.sums(p.host_j).tolist() if sb.nsum else None
+                page_file.write(path, p.layer, p.index, meta, los,
+                                frames if frames is not None else his,
+                                [frames is not None] * T, sums=sums)
+                p._path = path
+        if raw:
+            with self._stats_lock:
+                self._stats.spill_bytes_raw += raw
+                self._stats.spill_bytes_compressed += comp
 
     def _tensor_meta(self, layer: int) -> list[dict]:
         """Name, dtype and page shape ([B, ...slot shape]) of each pool tensor."""
@@ -921,25 +1025,6 @@ class PagedKVCache:
         names = ["k", "v_t"] if self._geom[0] == "kv" else ["latent"]
         return [{"name": n, "dtype": "BF16", "shape": (self._batch,) + shp}
                 for n, shp in zip(names, pool.slot_shapes)]
-
-    def _write_files(self, pages: list[_Page]) -> None:
-        """Write each spilled page to its page file once its host copy has landed."""
-        waited = set()
-        for p in pages:
-            sb = p.host
-            if id(sb) not in waited:
-                sb.ready.synchronize()
-                waited.add(id(sb))
-            T = len(sb.parts)
-            lo = [sb.part(t, p.host_j).numpy() for t in range(T)]
-            frames = sb.compressed[p.host_j]
-            hi = frames if frames is not None else [sb.part(T + t, p.host_j).numpy()
-                                                     for t in range(T)]
-            path = page_file.page_path(self.spill_dir, p.layer, p.index)
-            sums = sb.sums(p.host_j).tolist() if sb.nsum else None
-            page_file.write(path, p.layer, p.index, self._tensor_meta(p.layer), lo, hi,
-                            [frames is not None] * T, sums=sums)
-            p.path = path
 
     def _evict_host(self) -> None:
         """Drop host copies, oldest block first, while they exceed host_max_bytes;
@@ -949,14 +1034,16 @@ class PagedKVCache:
         for sb in list(self._spill_blocks):
             if self.arena.used_bytes <= self.host_max_bytes:
                 break
+            sb.wait_jobs()
             live = [p for p in sb.pages if p.host is sb]
-            if any(p.path is None for p in live):
+            if any(p._path is None for p in live):
                 continue
             for p in live:
                 p.host = None
             self._release_block(sb)
 
     def _release_block(self, sb: _SpillBlock) -> None:
+        sb.wait_jobs()
         if sb.ready is not None:
             sb.ready.synchronize()
         self.arena.free(sb.block)
@@ -971,7 +1058,7 @@ class PagedKVCache:
                 for n in parts + parts]
         T = len(parts)
         try:
-            head = page_file.read(p.path, [b.numpy() for b in bufs[:T]],
+            head = page_file.read(p._path, [b.numpy() for b in bufs[:T]],
                                   [b.numpy() for b in bufs[T:]])
         except (OSError, ValueError, RuntimeError) as exc:
             raise KVIntegrityError(f"layer {p.layer} page {p.index}: {exc}") from exc
@@ -991,16 +1078,6 @@ class PagedKVCache:
         sb = p.host
         T = len(sb.parts)
         planes = [sb.part(w, p.host_j) for w in range(2 * T)]
-        frames = sb.compressed[p.host_j]
-        if frames is not None:
-            for t, frame in enumerate(frames):
-                out = torch.empty(sb.parts[t], dtype=torch.uint8, pin_memory=self.arena.pin)
-                try:
-                    _zstd.decompress_into(frame, out.numpy())
-                except RuntimeError as exc:
-                    raise KVIntegrityError(
-                        f"layer {p.layer} page {p.index}: high plane {t}: {exc}") from exc
-                planes[T + t] = out
         return planes, (sb.sums(p.host_j) if sb.nsum else None)
 
     def _upload_planes(self, pages: list[_Page], staging: torch.Tensor,
@@ -1018,7 +1095,7 @@ class PagedKVCache:
         if (sb is not None and sb.nsum == nsum and p0.host_j % sb.chunk == 0
                 and n == sb.record_pages(p0.host_j // sb.chunk)
                 and all(p.host is sb and p.host_j == p0.host_j + j
-                        and sb.compressed[p.host_j] is None for j, p in enumerate(pages))):
+                        for j, p in enumerate(pages))):
             staging.copy_(sb.record(p0.host_j // sb.chunk), non_blocking=True)
             return
         T = len(parts)
@@ -1114,7 +1191,7 @@ class PagedKVCache:
 
     @staticmethod
     def _chunk_sig(pages: list[_Page]) -> tuple:
-        return tuple((id(p.host), p.host_j, p.path) for p in pages)
+        return tuple((id(p.host), p.host_j, p._path) for p in pages)
 
     def _acquire(self, writer: torch.cuda.Stream, nbytes: int):
         """Next staging buffer nobody holds.  When uploads started ahead hold
@@ -1258,8 +1335,8 @@ class PagedKVCache:
                 consume(cp, slots)
         if verified:
             self._publish_status()
-        self.stats.reloads += n_pages
-        self.stats.reload_s += time.perf_counter() - t0
+        self._stats.reloads += n_pages
+        self._stats.reload_s += time.perf_counter() - t0
 
     def reload(self, pages=None, stream: torch.cuda.Stream | None = None) -> int:
         """Make spilled pages resident again in fresh pool slots; returns the count.
@@ -1305,14 +1382,16 @@ class PagedKVCache:
     def _drop_host(self, p: _Page) -> None:
         """Forget the spilled copies of a page that is resident again."""
         sb = p.host
+        if sb is not None and sb.jobs:
+            sb.wait_jobs()  # its page file may still be being written
         p.host = None
         p._compressed = False
-        if p.path is not None:
+        if p._path is not None:
             try:
-                p.path.unlink()
+                p._path.unlink()
             except FileNotFoundError:
                 pass
-            p.path = None
+            p._path = None
         if sb is None:
             return
         sb.live -= 1

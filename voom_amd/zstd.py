@@ -79,3 +79,18 @@ def decompress_into(src: np.ndarray, dst: np.ndarray) -> int:
     if n != dst.nbytes:
         raise RuntimeError(f"zstd decompress: frame holds {n} bytes, expected {dst.nbytes}")
     return n
+
+
+def compress_into(src: np.ndarray, dst: np.ndarray, level: int = 1) -> int:
+    """Compress the contiguous uint8 array ``src`` into the preallocated
+    ``dst`` (at least compress_bound(src.nbytes) bytes); returns the frame
+    length.  No Python-side copies, so worker threads spend their time inside
+    libzstd, with the GIL released."""
+    lib = _load()
+    return _check(lib.ZSTD_compress(dst.__array_interface__["data"][0], dst.nbytes,
+                                    src.__array_interface__["data"][0], src.nbytes, level),
+                  "compress")
+
+
+def compress_bound(nbytes: int) -> int:
+    return int(_load().ZSTD_compressBound(nbytes))
