@@ -337,19 +337,55 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
     kv.reload()
     torch.cuda.synchronize()
     t_reload_cold = time.perf_counter() - t0
-    kv.max_bytes = kv.nbytes() - spill_bytes
-    t0 = time.perf_counter()
-    n_spilled = kv.spill()
-    t_spill_host = time.perf_counter() - t0
-    torch.cuda.synchronize()
-    t_spill = time.perf_counter() - t0
-    assert n_spilled == L * (S // PT // 2), n_spilled
-    assert all(not kv._pages[l][i].resident for l in range(L) for i in range(S // PT // 2))
-    t0 = time.perf_counter()
-    n_reloaded = kv.reload()
-    t_reload_host = time.perf_counter() - t0
-    torch.cuda.synchronize()
-    t_reload = time.perf_counter() - t0
+    # Warm cycles: the host link's rate into the same pinned pages varies from
+    # cycle to cycle on these boxes (other work shares the host), so several
+    # cycles are timed and the median is reported (the best alongside).
+    cycles = []
+    for _ in range(5):
+        kv.max_bytes = kv.nbytes() - spill_bytes
+        t0 = time.perf_counter()
+        n_spilled = kv.spill()
+        t_spill_host = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        t_spill = time.perf_counter() - t0
+        assert n_spilled == L * (S // PT // 2), n_spilled
+        assert all(not kv._pages[l][i].resident for l in range(L) for i in range(S // PT // 2))
+        t0 = time.perf_counter()
+        n_reloaded = kv.reload()
+        t_reload_host = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        t_reload = time.perf_counter() - t0
+        cycles.append((t_spill, t_reload, t_spill_host, t_reload_host))
+    t_spill = sorted(c[0] for c in cycles)[len(cycles) // 2]
+    t_reload = sorted(c[1] for c in cycles)[len(cycles) // 2]
+    t_spill_host = sorted(c[2] for c in cycles)[len(cycles) // 2]
+    t_reload_host = sorted(c[3] for c in cycles)[len(cycles) // 2]
+    best_spill = min(c[0] for c in cycles)
+    best_reload = min(c[1] for c in cycles)
+    # The host link measured on the arena's own pages: plain copies of the
+    # same 32 record-sized blocks the spill wrote (first fit puts them where
+    # the spill's records were), in both directions.  Pinned host pages of
+    # one process do not all sustain the same DMA rate on these boxes, so
+    # this is the ceiling the spill and reload can reach with this memory.
+    rec_bytes = (S // PT // 2) * kv.page_nbytes + 4096
+    blocks = [kv.arena.alloc(rec_bytes) for _ in range(L)]
+    dev_rec = torch.empty(rec_bytes, dtype=torch.uint8, device="cuda")
+    side = torch.cuda.Stream()
+    arena_link = {}
+    for name in ("d2h", "h2d"):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.stream(side):
+            for blk in blocks:
+                if name == "d2h":
+                    blk.view.copy_(dev_rec, non_blocking=True)
+                else:
+                    dev_rec.copy_(blk.view, non_blocking=True)
+        side.synchronize()
+        arena_link[name + "_gbs"] = L * rec_bytes / (time.perf_counter() - t0) / 1e9
+    for blk in blocks:
+        kv.arena.free(blk)
+    del dev_rec
     exact = True
     for layer in range(L):
         k2, v2 = ops.gather_kv(kv._pools[layer].k, kv._pools[layer].v, kv._tables[layer], S)
@@ -364,6 +400,11 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
         "reload_gbs": spill_bytes / t_reload / 1e9,
         "spill_s": t_spill,
         "reload_s": t_reload,
+        "warm_cycles": len(cycles),
+        "spill_gbs_per_cycle": [round(spill_bytes / c[0] / 1e9, 2) for c in cycles],
+        "reload_gbs_per_cycle": [round(spill_bytes / c[1] / 1e9, 2) for c in cycles],
+        "spill_best_gbs": spill_bytes / best_spill / 1e9,
+        "reload_best_gbs": spill_bytes / best_reload / 1e9,
         "spill_cold_gbs": spill_bytes / t_spill_cold / 1e9,
         "reload_cold_gbs": spill_bytes / t_reload_cold / 1e9,
         "spill_host_return_s": t_spill_host,
@@ -374,6 +415,9 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
         "link_ceiling": link,
         "spill_frac_of_link": spill_bytes / t_spill / 1e9 / link["d2h_gbs"],
         "reload_frac_of_link": spill_bytes / t_reload / 1e9 / link["h2d_gbs"],
+        "arena_link": arena_link,
+        "spill_frac_of_arena_link": spill_bytes / t_spill / 1e9 / arena_link["d2h_gbs"],
+        "reload_frac_of_arena_link": spill_bytes / t_reload / 1e9 / arena_link["h2d_gbs"],
     }
     # the same spill with compress_spill: zstd level 1 of the high planes runs
     # on worker threads after each record's copy lands (the raw planes stay in
@@ -415,7 +459,8 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
     log(f"config 3: spill() returned after {t_spill_host * 1e3:.1f} ms of {t_spill * 1e3:.1f} ms, "
         f"reload() after {t_reload_host * 1e3:.1f} ms of {t_reload * 1e3:.1f} ms")
     log(f"config 3: spill {res['spill_gbs']:.1f} GB/s, reload {res['reload_gbs']:.1f} GB/s, "
-        f"link d2h {link['d2h_gbs']:.1f} / h2d {link['h2d_gbs']:.1f} GB/s, exact={exact}")
+        f"link d2h {link['d2h_gbs']:.1f} / h2d {link['h2d_gbs']:.1f} GB/s (on the arena's pages "
+        f"{arena_link['d2h_gbs']:.1f} / {arena_link['h2d_gbs']:.1f}), exact={exact}")
     if cpu_sample:
         from concurrent.futures import ThreadPoolExecutor
 

@@ -79,3 +79,30 @@ def test_random_schedules_agree(seed):
 
 def test_within_budget_spills_nothing():
     assert budget_victims([[Meta(10)]], 0, 10, 10) == []
+
+
+def test_vectorised_victims_match_the_reference_order():
+    """budget_victims_fast (the cache's path for pages of one size) picks the
+    same pages in the same order as the reference-order loop."""
+    import numpy as np
+
+    from voom_amd.kv_paged import budget_victims_fast
+
+    class Page:
+        def __init__(self, resident):
+            self.resident = resident
+            self.nbytes = 100
+
+    rng = np.random.default_rng(0)
+    for trial in range(300):
+        L = int(rng.integers(1, 6))
+        lengths = rng.integers(0, 12, size=L)
+        cap = int(lengths.max()) + int(rng.integers(0, 3))
+        resident = rng.random((L, max(cap, 1))) < 0.7
+        keep = int(rng.integers(0, 3))
+        pages = [[Page(bool(resident[l, i])) for i in range(lengths[l])] for l in range(L)]
+        current = int(rng.integers(0, 4000))
+        max_bytes = int(rng.integers(0, 4000))
+        want = budget_victims(pages, keep, current, max_bytes)
+        layers, idx = budget_victims_fast(resident, lengths, keep, 100, current, max_bytes)
+        assert list(zip(layers.tolist(), idx.tolist())) == want, trial

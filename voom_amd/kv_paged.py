@@ -40,7 +40,7 @@ from __future__ import annotations
 import os
 import threading
 import time
-from collections import OrderedDict
+from collections import OrderedDict, deque
 from concurrent.futures import Future, ThreadPoolExecutor
 from dataclasses import dataclass
 from pathlib import Path
@@ -181,7 +181,7 @@ def _planes(buf: torch.Tensor, parts: list[int], m: int, t: int):
 class _Page:
     """One closed page of one layer: a pool slot per sequence, or a host copy."""
 
-    __slots__ = ("cache", "layer", "index", "slots", "host", "host_j", "nbytes", "_path",
+    __slots__ = ("cache", "layer", "index", "_slots", "host", "host_j", "nbytes", "_path",
                  "_compressed")
 
     def __init__(self, cache: "PagedKVCache", layer: int, index: int, slots: list[int],
@@ -189,7 +189,7 @@ class _Page:
         self.cache = cache
         self.layer = layer
         self.index = index
-        self.slots: list[int] | None = slots
+        self.slots = slots
         self.host: _SpillBlock | None = None
         self.host_j = 0
         self.nbytes = nbytes
@@ -197,8 +197,18 @@ class _Page:
         self._compressed = False
 
     @property
+    def slots(self) -> list[int] | None:
+        """Pool slots (one per sequence) while resident, None while spilled."""
+        return self._slots
+
+    @slots.setter
+    def slots(self, value) -> None:
+        self._slots = value
+        self.cache._mark(self.layer, self.index, value is not None)
+
+    @property
     def resident(self) -> bool:
-        return self.slots is not None
+        return self._slots is not None
 
     @property
     def path(self) -> Path | None:
@@ -276,6 +286,67 @@ class _StagingRing:
         self.held.discard(idx)
 
 
+class _PinnedUploads:
+    """Small host-to-device index uploads through one persistent pinned buffer.
+
+    Allocating pinned memory per upload (``pin_memory()``) can stall the host
+    for milliseconds; the buffer here is carved round-robin instead, and a
+    region is rewritten only after the copy that last read it has completed.
+    """
+
+    def __init__(self, device: torch.device, pin: bool, words: int = 1 << 20):
+        self.device = device
+        self.pin = pin
+        self.buf = torch.empty(words, dtype=torch.int32, pin_memory=pin)
+        self.np = self.buf.numpy()
+        self.pos = 0
+        # regions whose copies may still be reading the buffer, oldest first;
+        # regions are handed out in address order, so the ones a new region
+        # overlaps are always at the front
+        self.inflight: deque = deque()
+
+    def upload(self, arr: np.ndarray) -> torch.Tensor:
+        n = arr.size
+        if n > self.buf.numel() // 2:  # rare: a dedicated buffer
+            host = torch.from_numpy(arr)
+            return (host.pin_memory() if self.pin else host).to(self.device, non_blocking=True)
+        if self.pos + n > self.buf.numel():
+            self.pos = 0
+        lo, hi = self.pos, self.pos + n
+        q = self.inflight
+        while q and (q[0][0] < hi and q[0][1] > lo or q[0][2].query()):
+            q[0][2].synchronize()
+            q.popleft()
+        self.np[lo:hi] = arr.reshape(-1)
+        dev = torch.empty(arr.shape, dtype=torch.int32, device=self.device)
+        dev.view(-1).copy_(self.buf[lo:hi], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.inflight.append((lo, hi, ev))
+        self.pos = hi
+        return dev
+
+
+def budget_victims_fast(resident: np.ndarray, lengths, resident_pages: int, page_nbytes: int,
+                        current_bytes: int, max_bytes: int) -> tuple[np.ndarray, np.ndarray]:
+    """``budget_victims`` for pages of one size, on a resident mask.
+
+    ``resident`` [L, cap] bool (page i of layer l is resident), ``lengths``
+    the closed-page count per layer.  Returns (layers, page indices) of the
+    victims in the reference's order (oldest page index first, round-robin
+    over layers, never the newest ``resident_pages`` of a layer), as many as
+    bring ``current_bytes`` within ``max_bytes``.
+    """
+    if current_bytes <= max_bytes or resident.size == 0:
+        return np.zeros(0, np.int64), np.zeros(0, np.int64)
+    need = -(-(current_bytes - max_bytes) // page_nbytes)
+    L, cap = resident.shape
+    limit = np.asarray(lengths, dtype=np.int64) - resident_pages
+    eligible = resident & (np.arange(cap)[None, :] < limit[:, None])
+    flat = np.flatnonzero(eligible.T.reshape(-1))[:need]  # page index major, layer minor
+    return flat % L, flat // L
+
+
 def budget_victims(pages: list[list], resident_pages: int, current_bytes: int,
                    max_bytes: int) -> list[tuple[int, int]]:
     """Pages to spill so resident bytes fall to ``max_bytes``.
@@ -341,6 +412,7 @@ class PagedKVCache:
         self._copy_stream: torch.cuda.Stream | None = None
         self._ring = _StagingRing(self.device)
         self._i32_cache: OrderedDict = OrderedDict()
+        self._uploads: _PinnedUploads | None = None
         # attend(layer) starts the upload of the next layer's first spilled
         # chunk, so host-link time overlaps the compute in between
         self.prefetch = prefetch
@@ -369,6 +441,9 @@ class PagedKVCache:
         self._len = [0] * L
         self._offset = 0
         self._resident_closed = 0  # closed pages held in device slots, all layers
+        # _res[layer, i]: closed page i of the layer is resident (the budget
+        # scan reads this mask instead of the page objects)
+        self._res = np.zeros((L, 64), dtype=bool)
         self._spill_blocks: list[_SpillBlock] = []  # host blocks, oldest first
         self._pools: list[DevicePagePool | None] = [None] * L
         # one transient staging pool shared by all layers: every transient
@@ -391,6 +466,14 @@ class PagedKVCache:
         for sb in list(getattr(self, "_spill_blocks", ())):
             if sb.jobs:
                 sb.wait_jobs()
+
+    def _mark(self, layer: int, index: int, resident: bool) -> None:
+        if index >= self._res.shape[1]:
+            grown = np.zeros((self.num_layers, max(2 * self._res.shape[1], index + 1)),
+                             dtype=bool)
+            grown[:, :self._res.shape[1]] = self._res
+            self._res = grown
+        self._res[layer, index] = resident
 
     def _set_geometry(self, geom: tuple, dtype: torch.dtype) -> None:
         if self._geom is None:
@@ -458,10 +541,9 @@ class PagedKVCache:
             if hit is not None:
                 self._i32_cache.move_to_end(key)
                 return hit
-        host = torch.from_numpy(arr)
-        if self.arena.pin:
-            host = host.pin_memory()
-        dev = host.to(self.device, non_blocking=True)
+        if self._uploads is None:
+            self._uploads = _PinnedUploads(self.device, self.arena.pin)
+        dev = self._uploads.upload(arr)
         if cache:
             self._i32_cache[key] = dev
             if len(self._i32_cache) > 256:
@@ -829,9 +911,21 @@ class PagedKVCache:
     # ---- spilling -----------------------------------------------------------
 
     def _enforce_budget(self) -> None:
-        victims = budget_victims(self._pages, self.resident_pages, self.nbytes(), self.max_bytes)
-        if victims:
-            self.spill([self._pages[l][i] for l, i in victims])
+        """Spill in the reference's order until resident bytes fit max_bytes
+        (kv_paged.py:216-240; every page of a cache has the same size, so the
+        order is found on the resident mask by budget_victims_fast)."""
+        current = self.nbytes()
+        if current <= self.max_bytes:
+            return
+        layers, idx = budget_victims_fast(self._res, [len(p) for p in self._pages],
+                                          self.resident_pages, self.page_nbytes, current,
+                                          self.max_bytes)
+        if layers.size:
+            groups = {}
+            for layer in np.unique(layers).tolist():
+                pages = self._pages[layer]
+                groups[layer] = [pages[i] for i in idx[layers == layer].tolist()]
+            self._spill_groups(groups)
 
     def spill(self, pages=None) -> int:
         """Spill pages (``_Page`` objects or (layer, index) pairs) to the host arena.
@@ -842,16 +936,25 @@ class PagedKVCache:
             before = self._stats.spills
             self._enforce_budget()
             return self._stats.spills - before
-        pages = [self._pages[p[0]][p[1]] if isinstance(p, tuple) else p for p in pages]
-        pages = [p for p in pages if p.resident]
-        by_layer: dict[int, list[_Page]] = {}
+        groups: dict[int, list[_Page]] = {}
         for p in pages:
-            by_layer.setdefault(p.layer, []).append(p)
+            if isinstance(p, tuple):
+                p = self._pages[p[0]][p[1]]
+            if p.resident:
+                groups.setdefault(p.layer, []).append(p)
+        return self._spill_groups(groups)
+
+    def _spill_groups(self, by_layer: dict) -> int:
+        """Spill resident pages grouped by layer.  Each layer's chunks are
+        enqueued as soon as the layer is planned, so the first copy starts
+        while later layers are still being planned."""
         t0 = time.perf_counter()
-        work = []
+        pages = [p for lp in by_layer.values() for p in lp]
+        issue = self._spill_issuer()
         for layer, lp in by_layer.items():
-            work += self._spill_plan(layer, lp)
-        self._spill_chunks(work)
+            for item in self._spill_plan(layer, lp):
+                issue(item)
+        issue(None)
         for layer, lp in by_layer.items():
             pool = self._pool(layer)
             pool.release([s for p in lp for s in p.slots])
@@ -898,38 +1001,22 @@ class PagedKVCache:
         return [(pool, pages[c0:c0 + per_chunk], sb, c0 // per_chunk)
                 for c0 in range(0, n, per_chunk)]
 
-    def _spill_chunks(self, work) -> None:
-        """Byte-plane split (main stream, ordered after the pages' writes) into
-        staging buffers, then D2H of each staged record (side stream).
+    def _spill_issuer(self):
+        """A function taking spill work items (pool, pages, block, record) one
+        at a time (None flushes): the byte-plane split of each (main stream,
+        ordered after the pages' writes) into a staging buffer, then the D2H
+        of the staged record (side stream).
 
-        Work is processed in windows of ring size; within a window every split
+        Items are issued in windows of ring size; within a window every split
         is enqueued before any copy, so copies run back to back even when the
         two streams share a hardware queue.
         """
         main = torch.cuda.current_stream()
         copy = self._stream()
         nbuf = len(self._ring.bufs)
-        for w0 in range(0, len(work), nbuf):
-            staged = []
-            for pool, cp, sb, rec in work[w0:w0 + nbuf]:
-                m = len(cp)
-                slot_t = self._dev_i32([s for p in cp for s in p.slots])
-                idx, buf = self._acquire(main, m * sb.page_bytes)
-                sums = None
-                if sb.nsum:
-                    sums = sums_view(buf, sb.parts, m, sb.nsum)
-                    sums.zero_()
-                for t, tensor in enumerate(pool.tensors):
-                    lo, hi = _planes(buf, sb.parts, m, t)
-                    if ops.slot_codec_supported(tensor):
-                        ops.byteplane_split_slots(tensor, slot_t, lo, hi,
-                                                  sums=None if sums is None else sums[t])
-                    else:
-                        ops.byteplane_split(tensor.index_select(0, slot_t.long()).contiguous(),
-                                            lo, hi)
-                ev = torch.cuda.Event()
-                ev.record(main)
-                staged.append((idx, buf, sb, rec, ev))
+        staged = []
+
+        def flush():
             for idx, buf, sb, rec, ev in staged:
                 copy.wait_event(ev)
                 with torch.cuda.stream(copy):
@@ -938,6 +1025,35 @@ class PagedKVCache:
                 sb.ready = torch.cuda.Event()
                 sb.ready.record(copy)
                 sb.rec_ready[rec] = sb.ready
+            staged.clear()
+
+        def issue(item) -> None:
+            if item is None:
+                flush()
+                return
+            pool, cp, sb, rec = item
+            m = len(cp)
+            slot_t = self._dev_i32([s for p in cp for s in p.slots])
+            idx, buf = self._acquire(main, m * sb.page_bytes)
+            sums = None
+            if sb.nsum:
+                sums = sums_view(buf, sb.parts, m, sb.nsum)
+                sums.zero_()
+            for t, tensor in enumerate(pool.tensors):
+                lo, hi = _planes(buf, sb.parts, m, t)
+                if ops.slot_codec_supported(tensor):
+                    ops.byteplane_split_slots(tensor, slot_t, lo, hi,
+                                              sums=None if sums is None else sums[t])
+                else:
+                    ops.byteplane_split(tensor.index_select(0, slot_t.long()).contiguous(),
+                                        lo, hi)
+            ev = torch.cuda.Event()
+            ev.record(main)
+            staged.append((idx, buf, sb, rec, ev))
+            if len(staged) == nbuf:
+                flush()
+
+        return issue
 
     # pages per background job: small enough to spread one record over the
     # workers, large enough that a job is milliseconds of zstd
@@ -1285,26 +1401,11 @@ class PagedKVCache:
         copy = self._stream()
         nbuf = len(self._ring.bufs)
         t0 = time.perf_counter()
-        chunks = []
         n_pages = 0
         verified = False
-        for layer, pages, target, consume, transient in jobs:
-            parts = self._plane_parts(target)
-            nsum = self._nsum(target)
-            verified |= nsum > 0
-            per_chunk = max(1, self._ring.nbytes // record_page_bytes(parts, nsum))
-            if transient:
-                target.ensure_capacity(nbuf * per_chunk * B)
-            for sb in {id(p.host): p.host for p in pages if p.host is not None}.values():
-                copy.wait_event(sb.ready)
-            for c0 in range(0, len(pages), per_chunk):
-                cp = pages[c0:c0 + per_chunk]
-                ahead = self._take_prefetch(layer, cp) if transient and c0 == 0 else None
-                chunks.append((layer, cp, target, consume, transient, parts, nsum, per_chunk,
-                               ahead))
-            n_pages += len(pages)
-        for w0 in range(0, len(chunks), nbuf):
-            window = chunks[w0:w0 + nbuf]
+        window: list = []
+
+        def run_window():
             landed = []
             for layer, cp, target, consume, transient, parts, nsum, per_chunk, ahead in window:
                 if ahead is not None:
@@ -1333,6 +1434,29 @@ class PagedKVCache:
                                  tag=self._tag(layer, cp) if nsum else 0)
                 self._ring.release(idx, main)
                 consume(cp, slots)
+            window.clear()
+
+        # chunks are produced job by job and issued a window at a time, so the
+        # first copy starts before later jobs are even looked at
+        for layer, pages, target, consume, transient in jobs:
+            parts = self._plane_parts(target)
+            nsum = self._nsum(target)
+            verified |= nsum > 0
+            per_chunk = max(1, self._ring.nbytes // record_page_bytes(parts, nsum))
+            if transient:
+                target.ensure_capacity(nbuf * per_chunk * B)
+            for sb in {id(p.host): p.host for p in pages if p.host is not None}.values():
+                copy.wait_event(sb.ready)
+            for c0 in range(0, len(pages), per_chunk):
+                cp = pages[c0:c0 + per_chunk]
+                ahead = self._take_prefetch(layer, cp) if transient and c0 == 0 else None
+                window.append((layer, cp, target, consume, transient, parts, nsum, per_chunk,
+                               ahead))
+                if len(window) == nbuf:
+                    run_window()
+            n_pages += len(pages)
+        if window:
+            run_window()
         if verified:
             self._publish_status()
         self._stats.reloads += n_pages
@@ -1348,36 +1472,50 @@ class PagedKVCache:
         """
         self.check_integrity(wait=False)
         if pages is None:
-            pages = [p for layer in self._pages for p in layer if not p.resident]
-        pages = [self._pages[p[0]][p[1]] if isinstance(p, tuple) else p for p in pages]
-        pages = [p for p in pages if not p.resident]
-        if not pages:
-            return 0
+            # every spilled page, found layer by layer from the resident mask
+            # while the first layers' uploads are already running
+            def layer_lists():
+                for layer, lp in enumerate(self._pages):
+                    idx = np.flatnonzero(~self._res[layer, :len(lp)])
+                    if idx.size:
+                        yield layer, [lp[i] for i in idx.tolist()]
+        else:
+            by_layer: dict[int, list[_Page]] = {}
+            for p in pages:
+                if isinstance(p, tuple):
+                    p = self._pages[p[0]][p[1]]
+                if not p.resident:
+                    by_layer.setdefault(p.layer, []).append(p)
+
+            def layer_lists():
+                yield from by_layer.items()
         if stream is not None:
             self._copy_stream = stream
         B = self._batch
-        by_layer: dict[int, list[_Page]] = {}
-        for p in pages:
-            by_layer.setdefault(p.layer, []).append(p)
-        jobs = []
         done: dict[int, list[_Page]] = {}
-        for layer, lp in by_layer.items():
-            done[layer] = []
 
-            def adopt(chunk, slots, acc=done[layer]):
-                for j, p in enumerate(chunk):
-                    p.slots = slots[j * B:(j + 1) * B]
-                    acc.append(p)
-                self._resident_closed += len(chunk)
+        def jobs():
+            for layer, lp in layer_lists():
+                done[layer] = []
 
-            jobs.append((layer, lp, self._pool(layer), adopt, False))
-        self._pipeline_in(jobs)
+                def adopt(chunk, slots, acc=done[layer]):
+                    for j, p in enumerate(chunk):
+                        p.slots = slots[j * B:(j + 1) * B]
+                        acc.append(p)
+                    self._resident_closed += len(chunk)
+
+                yield layer, lp, self._pool(layer), adopt, False
+
+        self._pipeline_in(jobs())
+        n = 0
         for layer, lp in done.items():
             self._set_table_cols(layer, {p.index: p.slots for p in lp})
             for p in lp:
                 self._drop_host(p)
-        self.check_integrity()
-        return len(pages)
+            n += len(lp)
+        if n:
+            self.check_integrity()
+        return n
 
     def _drop_host(self, p: _Page) -> None:
         """Forget the spilled copies of a page that is resident again."""
