@@ -27,8 +27,19 @@ __device__ __forceinline__ float bf2f(uint16_t x) {
 }
 
 // Packs two fp32 values into one dword of two bf16 (low half = a).
+// One v_cvt_pk_bf16_f32 (round to nearest even, as f2bf).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+// a.lo + a.hi (+ c) of two packed bf16 values in fp32: one v_dot2_f32_bf16
+// against (1, 1).
+__device__ __forceinline__ float sum_bf16x2(uint32_t a, float c) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), one, c, false);
 }
 
 __device__ __forceinline__ float wave_max_across_groups(float v) {
@@ -106,9 +117,19 @@ __device__ __forceinline__ void wait_vmem_all() {
 
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
 // operations, then s_barrier.  Unlike __syncthreads() it does not drain
-// outstanding global loads, so register prefetches stay in flight across it.
+// outstanding global loads, so register prefetches and direct-to-LDS loads
+// stay in flight across it.  The wait and the barrier are builtins, which the
+// compiler's wait-count pass sees; the empty asm statements only stop the
+// compiler from moving memory accesses across the barrier.  (With the wait
+// and barrier written as inline asm, the pass no longer told the LDS buffers
+// apart after the barrier and put a vmcnt(0) before LDS accesses that no
+// pending direct-to-LDS load writes -- in the MLA kernel before the P reads,
+// i.e. a wait for the whole next tile.)
 __device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // gfx9 encoding: lgkmcnt 0, vmcnt 63, expcnt 7
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Hardware base-2 exponential (v_exp_f32).

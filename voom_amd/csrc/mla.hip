@@ -489,6 +489,463 @@ __global__ __launch_bounds__(kMlaThreads) void mla_latent_kernel(MlaArgs a) {
   }
 }
 
+// ------------------------------------------- 64-head groups, 32x32 tiles ----
+// mla_group64_kernel: the latent contraction for head groups of 64 with four
+// wavefronts (one per SIMD, so each has the SIMD's whole register file) and
+// v_mfma_f32_32x32x16_bf16, whose 32x32 output tile halves the LDS operand
+// bytes per flop of the 16x16 shape.  Per 64-token tile:
+//   scores  wave w: tokens 32(w>>1).., heads 32(w&1)..   A = latent rows (LDS),
+//           B = q (registers, all 36 k-steps)
+//   P.V     wave w: dims 128w..128w+127 x all 64 heads   A = C^T (transposed
+//           LDS reads), B = P (LDS)
+// Two barriers per tile: one after the tile has landed, one after P is
+// written.  The softmax uses one reference maximum M per head for the whole
+// token range, the maximum of the range's first tile (shared by the four
+// wavefronts), so P of a tile is formed before its maximum is known across
+// wavefronts and the accumulators are never rescaled: P = 2^(x - M) stays
+// below 2^kBig, and a tile that would exceed that -- in practice never after
+// the first -- starts the range over with the raised M.  Every wavefront
+// reads the same tile maxima from LDS, so all four take the same branches.
+constexpr int kGThreads = 256;
+constexpr int kGWaves = 4;
+constexpr int kGLoads = kLoadsPerTile / kGWaves;  // 18 direct-to-LDS loads per wave and tile
+constexpr int kGPRow = kTile + 8;                 // P row stride: 144 B, conflict-free rows
+constexpr int kGSteps = kLat / 16;                // 36 k-steps of the score MFMA
+constexpr float kBig = 64.f;
+static_assert(kLoadsPerTile % kGWaves == 0, "loads split evenly over the wavefronts");
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Chunk c of token row r is stored at chunk c ^ group_swizzle(r).  The score
+// reads (32 consecutive rows, one chunk) and the transposed reads (rows
+// 4k..4k+3, four adjacent chunks) then spread over all banks: rows r and r+4j
+// differ in bits 0-2 of the swizzle for j = 1..7, and rows r and r+2 in bit 2.
+__device__ __forceinline__ int group_swizzle(int r) {
+  return ((r >> 2) ^ (((r >> 1) & 1) << 2)) & 7;
+}
+
+template <bool SPARSE>
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void mla_group64_kernel(MlaArgs a) {
+  constexpr int HG = 64;
+  __shared__ __attribute__((aligned(16))) uint16_t tile_a[kTile * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t tile_b[kTile * kRow];
+  __shared__ __attribute__((aligned(16))) uint16_t p_lds[HG * kGPRow];
+  // per tile parity and head: the four partial maxima of the tile
+  __shared__ __attribute__((aligned(16))) float tmax_lds[2][HG][4];
+  __shared__ float lsum_lds[2][HG];
+  __shared__ uint32_t pre_off[SPARSE ? kPre : 1][kTile];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = uniform(tid >> 6);  // 0..3
+  const int th = w >> 1;            // score tokens 32 th ..
+  const int hh = w & 1;             // score heads 32 hh ..
+  const int l32 = lane & 31;
+  const int lh = lane >> 5;
+  const int NHG = a.H / HG;
+
+  const int n_tasks = a.B * a.NR;
+  int task, hg;
+  const int bid = blockIdx.x;
+  if (n_tasks % 8 == 0) {
+    // the head groups of one (sequence, range) share bid % 8: the same XCD
+    const int local = bid >> 3;
+    hg = local % NHG;
+    task = (local / NHG) * 8 + (bid & 7);
+  } else {
+    hg = bid % NHG;
+    task = bid / NHG;
+  }
+  const int b = task / a.NR;
+  const int range = task - b * a.NR;
+  int ctx = a.ctx_lens[b];
+  const int cap = SPARSE ? a.sel_stride : a.max_pages << a.pt_shift;
+  ctx = uniform(ctx < 0 ? 0 : (ctx > cap ? cap : ctx));
+  const int n_tiles = (ctx + kTile - 1) / kTile;
+  const int per = (n_tiles + a.NR - 1) / a.NR;
+  const int t_lo = range * per;
+  const int t_hi = (t_lo + per < n_tiles) ? t_lo + per : n_tiles;
+  const int head0 = hg * HG;
+  const int32_t* trow = a.table + static_cast<size_t>(b) * a.max_pages;
+
+  // B operand of the scores: lane (head 32 hh + l32, half lh) holds
+  // q[head][16 s + 8 lh .. + 8] for all 36 k-steps.
+  u32x4 qop[kGSteps];  // filled from LDS below
+
+  f32x16 acc[4][2];  // out^T: dims 128 w + 32 dt .., heads 32 ht + l32
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) acc[dt][ht] = f32x16{};
+  }
+  // Reference maxima (log2 units) of heads l32 and 32 + l32, the same in
+  // every wavefront; the normaliser of the score head (32 hh + l32) over this
+  // lane's tokens, relative to M.
+  float M[2] = {-INFINITY, -INFINITY};
+  float l_run = 0.f;
+
+  if constexpr (SPARSE) {
+    if (w == 0) {
+      int pos[kPre];
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) {
+        const int tok = (t_lo + k) * kTile + lane;
+        pos[k] = (t_lo + k < t_hi && tok < ctx)
+                     ? a.sel[static_cast<size_t>(b) * a.sel_stride + tok]
+                     : -1;
+      }
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) {
+        // a position past the table reads from slot 0 (the slot an invalid
+        // table entry falls back to); no position: a row of zeros
+        const int page = pos[k] >> a.pt_shift;
+        int slot = (pos[k] >= 0 && page < a.max_pages) ? trow[page] : 0;
+        if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
+        pre_off[k][lane] =
+            pos[k] < 0 ? 0xFFFFFFF0u
+                       : static_cast<uint32_t>(((static_cast<long long>(slot) << a.pt_shift) +
+                                                (pos[k] & ((1 << a.pt_shift) - 1))) *
+                                               (kLat * 2));
+      }
+    }
+    lds_barrier();
+  }
+
+  // LDS tile layout: nine column blocks of 8 chunks (128 bytes of a row)
+  // for all 64 rows, 8 KiB each; row r of block cb holds chunks 8 cb .. 8 cb
+  // + 7 of token row r at r * 128 bytes, chunk c at position c ^
+  // group_swizzle(r).  A direct-to-LDS load fills 1 KiB, i.e. rows 8 g ..
+  // 8 g + 7 of one block: load k of wave w covers block k >> 1, rows 8 w +
+  // 32 (k & 1) + lane / 8, so its source offset is one of two per-lane bases
+  // plus 128 (k >> 1) -- the swizzle of those rows does not depend on k.
+  const int ld_row = 8 * w + (lane >> 3);
+  const int ld_col = 16 * ((lane & 7) ^ group_swizzle(ld_row));
+  const int ld_base0 = ld_row * (kLat * 2) + ld_col;
+  const int ld_base1 = ld_base0 + 32 * (kLat * 2);
+
+  // Source of a tile's direct-to-LDS loads: a buffer descriptor and two
+  // per-lane offsets (rows 8 w + lane / 8 and 32 rows further); load k adds
+  // 128 (k >> 1) bytes.  Rows past the context, and a tile that does not
+  // exist, read as zeros: their offsets lie past the descriptor's range
+  // (0xFFFF0000 and above, which no pool or tile range reaches).
+  const int tile_shift = a.pt_shift - 6;
+  int tab_base = -(1 << 30);
+  int tab = 0;
+  auto tile_src = [&](int t, uint32_t (&off)[2]) -> __amdgpu_buffer_rsrc_t {
+    if (t >= t_hi) {
+      off[0] = off[1] = 0xFFFF0000u;
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.lat), static_cast<short>(0),
+                                               0, 0x00020000);
+    }
+    if constexpr (SPARSE) {
+      const uint32_t* po = pre_off[(t - t_lo) & (kPre - 1)];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t rb = po[ld_row + 32 * i];
+        off[i] = rb != 0xFFFFFFF0u ? rb + static_cast<uint32_t>(ld_col) : 0xFFFF0000u;
+      }
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.lat), static_cast<short>(0),
+                                               static_cast<int>(a.pool_bytes), 0x00020000);
+    }
+    const int page = t >> tile_shift;
+    const int sub = t - (page << tile_shift);
+    if (page < tab_base || page >= tab_base + 64) {
+      tab_base = page;
+      tab = tab_base + lane < a.max_pages ? trow[tab_base + lane] : 0;
+    }
+    int slot = __builtin_amdgcn_readlane(tab, page - tab_base);
+    if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
+    const uint16_t* base =
+        a.lat + ((static_cast<size_t>(slot) << a.pt_shift) + sub * kTile) * kLat;
+    int valid = ctx - t * kTile;
+    valid = valid > kTile ? kTile : valid;
+    off[0] = static_cast<uint32_t>(ld_base0);
+    off[1] = static_cast<uint32_t>(ld_base1);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), static_cast<short>(0),
+                                             valid * kLat * 2, 0x00020000);
+  };
+  auto load_tile = [&](int t, uint16_t* dst) {
+    uint32_t off[2];
+    const __amdgpu_buffer_rsrc_t r = tile_src(t, off);
+#pragma unroll
+    for (int k = 0; k < kGLoads; ++k) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + (w + kGWaves * k) * 512), 16,
+                                               static_cast<int>(off[k & 1] + 128 * (k >> 1)), 0,
+                                               0, 0);
+    }
+  };
+
+  // Per-lane parts of the LDS addresses (in bf16 elements; a block is 4096).
+  // Scores: row 32 th + l32 (its swizzle depends on l32 only), logical chunk
+  // 2 s + lh, i.e. block s >> 2, chunk 2 (s & 3) + lh within it.
+  const int sw_row = group_swizzle(l32);
+  int a_off[4];  // k-step s = 4 i + j: element offset 4096 i + a_off[j]
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a_off[j] = (32 * th + l32) * 64 + 8 * ((2 * j + lh) ^ sw_row);
+  // Transposed reads: in 16-lane group G, lane i16 addresses token row
+  // 16 ks + 8 (G >> 1) + 4 h + (i16 >> 2) at dims 128 w + 32 dt + 16 (G & 1) +
+  // 4 (i16 & 3), i.e. block 2 w + (dt >> 1), chunk 4 (dt & 1) + 2 (G & 1) +
+  // (i16 & 3) / 2; the swizzle of that row is (4 (ks & 1) + 2 (G >> 1) + h) ^
+  // 4 (i16 >> 3).
+  const int G = lane >> 4;
+  const int i16 = lane & 15;
+  // The lane-dependent part depends on ks & 1, h and dt & 1 only (eight
+  // registers); ks >> 1 adds 32 rows and dt >> 1 one block.
+  int tr_base[2][2][2];
+#pragma unroll
+  for (int k1 = 0; k1 < 2; ++k1) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int d1 = 0; d1 < 2; ++d1) {
+        const int row = 16 * k1 + 8 * (G >> 1) + 4 * h + (i16 >> 2);
+        const int sw = ((4 * k1 + 2 * (G >> 1) + h) ^ (4 * (i16 >> 3))) & 7;
+        const int chunk = 4 * d1 + 2 * (G & 1) + ((i16 & 3) >> 1);
+        tr_base[k1][h][d1] = 4096 * 2 * w + row * 64 + 8 * (chunk ^ sw) + 4 * (i16 & 1);
+      }
+    }
+  }
+  auto tr_off = [&](int ks, int h, int dt) {
+    return tr_base[ks & 1][h][dt & 1] + 2048 * (ks >> 1) + 4096 * (dt >> 1);
+  };
+
+  // Instruction-group order for the scheduler (masks of
+  // __builtin_amdgcn_sched_group_barrier).
+  constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
+
+  // One tile on LDS buffer `tile` while tile t + 1 streams into `next`;
+  // false: the range has to start over (see below).
+  const int t_first = t_lo;
+  // Reference check of tile tp: its tile maxima against M (kept in LDS by
+  // tile parity, so that the check of tile t - 1 can be made during tile t).
+  auto too_big = [&](int tp) {
+    float tm[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&tmax_lds[tp & 1][32 * k + l32][0]);
+      tm[k] = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    }
+    if (__builtin_amdgcn_ballot_w64(tm[0] > M[0] + kBig || tm[1] > M[1] + kBig) == 0) return false;
+    M[0] = fmaxf(M[0], tm[0]);
+    M[1] = fmaxf(M[1], tm[1]);
+    return true;
+  };
+
+  auto step = [&](int t, const uint16_t* tile, uint16_t* next) -> bool {
+    wait_vmem_all();
+    lds_barrier();
+    uint32_t noff[2];
+    const __amdgpu_buffer_rsrc_t nsrc = tile_src(t + 1, noff);
+
+    // ---- scores: 32 tokens x 32 heads, one accumulator chain (dependent
+    // 32x32 MFMAs issue back to back).  The latent rows of k-step s + kAhead
+    // are read while the MFMA of step s runs, and the next tile's 18 loads go
+    // out one every two k-steps: issued in one burst, they stall the wave
+    // until the memory pipeline has taken them. ----
+    f32x16 sc = f32x16{};
+    {
+      constexpr int kAhead = 5;
+      u32x4 ring[kAhead];
+#pragma unroll
+      for (int s = 0; s < kAhead; ++s) {
+        ring[s] = *reinterpret_cast<const u32x4*>(tile + 4096 * (s >> 2) + a_off[s & 3]);
+      }
+      __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead, 0);
+#pragma unroll
+      for (int s = 0; s < kGSteps; ++s) {
+        const bf16x8 av = __builtin_bit_cast(bf16x8, ring[s % kAhead]);
+        const bf16x8 qv = __builtin_bit_cast(bf16x8, qop[s]);
+        if (s + kAhead < kGSteps) {
+          const int n = s + kAhead;
+          ring[s % kAhead] = *reinterpret_cast<const u32x4*>(tile + 4096 * (n >> 2) + a_off[n & 3]);
+          __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        }
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qv, sc, 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        if ((s & 1) == 0 && (s >> 1) < kGLoads) {
+          const int k = s >> 1;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              nsrc, (lds_void*)(next + (w + kGWaves * k) * 512), 16,
+              static_cast<int>(noff[k & 1] + 128 * (k >> 1)), 0, 0, 0);
+          __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+        }
+      }
+    }
+    // The previous tile's reference check, deferred to here so that its LDS
+    // reads were hidden behind the score MFMAs; a failure drops this tile too.
+    if (t - 1 > t_first && too_big(t - 1)) return false;
+
+    // lane (head 32 hh + l32) holds tokens 32 th + 4 lh + (8 (r >> 2) + (r & 3))
+    // as raw dot products; the scale (> 0) is applied inside the exponent.
+    // Only the last tile of a sequence has rows past its end.
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = sc[r];
+    if (ctx - t * kTile < kTile) {
+      const int lim = ctx - t * kTile - (32 * th + 4 * lh);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = 8 * (r >> 2) + (r & 3) < lim ? x[r] : -INFINITY;
+    }
+    float mloc = x[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, x[r]);
+    // the maximum of this lane's 16 tokens (log2 units); the four lanes
+    // holding a head's 64 tokens (th, lh) each leave theirs
+    tmax_lds[t & 1][32 * hh + l32][2 * th + lh] = mloc * a.scale_log2e;
+
+    uint16_t* prow = p_lds + (32 * hh + l32) * kGPRow + 32 * th + 4 * lh;
+    auto write_p = [&](float m) {
+      float ps = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = fast_exp2(__builtin_fmaf(x[4 * q + i], a.scale_log2e, -m));
+        const uint32_t w0 = pack_bf16x2(e[0], e[1]);
+        const uint32_t w1 = pack_bf16x2(e[2], e[3]);
+        *reinterpret_cast<u32x2*>(prow + 8 * q) = u32x2{w0, w1};
+        ps = sum_bf16x2(w1, sum_bf16x2(w0, ps));
+      }
+      return ps;
+    };
+
+    // ---- operands of P.V: C^T by transposed reads of the tile, P from LDS
+    // once every wavefront has written it.  The C^T operand of step (ks, dt)
+    // is read two steps ahead, P one k-step ahead. ----
+    constexpr int kCAhead = 2;
+    bf16x8 pb[2][2];
+    bf16x8 cv[kCAhead + 1];
+    auto read_c = [&](int i) {  // step i = 4 ks + dt
+      const int ks = i >> 2, dt = i & 3;
+      const bf16x4 lo =
+          __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + tr_off(ks, 0, dt)));
+      const bf16x4 hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + tr_off(ks, 1, dt)));
+      cv[i % (kCAhead + 1)] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    auto read_p = [&](int ks) {
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht) {
+        pb[ks & 1][ht] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u32x4*>(p_lds + (32 * ht + l32) * kGPRow + 16 * ks +
+                                                    8 * lh));
+      }
+    };
+    if (t == t_first) {
+      // first tile of the range: the reference maximum comes from it, so the
+      // maxima are exchanged before P is formed (one more barrier)
+      lds_barrier();
+      too_big(t);
+    }
+    const float ps = write_p(hh ? M[1] : M[0]);
+    lds_barrier();
+    read_p(0);
+#pragma unroll
+    for (int i = 0; i < kCAhead; ++i) read_c(i);
+
+    // ---- out^T[dims 128 w .., heads] += C^T . P^T, 16 tokens per k-step ----
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 2 + 2 * kCAhead, 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int ks = i >> 2, dt = i & 3;
+      if (i + kCAhead < 16) {
+        read_c(i + kCAhead);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 1);
+      }
+      if (dt == 0 && ks + 1 < 4) {
+        read_p(ks + 1);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 1);
+      }
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht) {
+        acc[dt][ht] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cv[i % (kCAhead + 1)], pb[ks & 1][ht],
+                                                              acc[dt][ht], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
+      }
+    }
+    l_run += ps;
+    return true;
+  };
+
+  // A restart (a tile more than 2^kBig above the reference of the first)
+  // drops the range's sums and runs it again from its first tile with the
+  // raised reference, which no tile of the range can exceed by that much
+  // again before a still higher one: M grows by more than kBig per restart,
+  // so the loop ends.  The accumulators are only ever zeroed or fed to MFMAs,
+  // which keeps them in accumulation registers.
+  //
+  // The group's q rows (64 x 576, contiguous in memory) first go through the
+  // second tile buffer in the tile layout: one coalesced stream instead of 36
+  // row-strided loads per wavefront, and the score operands are then read
+  // with the conflict-free pattern of the latent rows (row 32 hh + l32).
+  {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.q + (static_cast<size_t>(b) * a.H + head0) * kLat),
+        static_cast<short>(0), HG * kLat * 2, 0x00020000);
+#pragma unroll
+    for (int k = 0; k < kGLoads; ++k) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile_b + (w + kGWaves * k) * 512), 16,
+                                               ((k & 1) ? ld_base1 : ld_base0) + 128 * (k >> 1),
+                                               0, 0, 0);
+    }
+    wait_vmem_all();
+    lds_barrier();
+#pragma unroll
+    for (int s = 0; s < kGSteps; ++s) {
+      qop[s] = *reinterpret_cast<const u32x4*>(tile_b + 4096 * (s >> 2) + a_off[s & 3] +
+                                               (hh - th) * 32 * 64);
+    }
+  }
+  for (;;) {
+    int t = t_lo;
+    bool ok = true;
+    if (t < t_hi) load_tile(t, tile_a);
+    while (ok && t < t_hi) {
+      ok = step(t, tile_a, tile_b);
+      if (ok && t + 1 < t_hi) ok = step(t + 1, tile_b, tile_a);
+      t += 2;
+    }
+    if (ok && t_hi - 1 > t_lo) {
+      // the last tile's check (the others were made one tile later)
+      lds_barrier();
+      ok = !too_big(t_hi - 1);
+    }
+    if (ok) break;
+    wait_vmem_all();  // loads issued before the restart
+    lds_barrier();
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht) acc[dt][ht] = f32x16{};
+    }
+    l_run = 0.f;
+  }
+
+  // ---- partial state of this (sequence, range, head group) ----
+  const size_t pbase = (static_cast<size_t>(b) * a.NR + range) * a.H + head0;
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    float* po = a.part_o + (pbase + 32 * ht + l32) * kC + 128 * w + 4 * lh;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * q) =
+            f32x4{acc[dt][ht][4 * q], acc[dt][ht][4 * q + 1], acc[dt][ht][4 * q + 2],
+                  acc[dt][ht][4 * q + 3]};
+      }
+    }
+  }
+  const float lw = l_run + __shfl_xor(l_run, 32);
+  if (lh == 0) lsum_lds[th][32 * hh + l32] = lw;
+  lds_barrier();
+  if (w == 0) {
+    a.part_ml[(pbase + lane) * 2 + 0] = lh ? M[1] : M[0];
+    a.part_ml[(pbase + lane) * 2 + 1] = lsum_lds[0][lane] + lsum_lds[1][lane];
+  }
+}
+
 // One wavefront per (sequence, head): merges the NR range partials.  Lane r
 // holds range r's (m, l); the partial rows of a batch of ranges are all loaded
 // before the first is used (one memory round trip per batch).
@@ -575,9 +1032,9 @@ int launch_mla(const MlaArgs& a, int hg, bool sparse, long long grid, uint16_t* 
   const dim3 g(static_cast<unsigned>(grid));
   if (hg == 64) {
     if (sparse) {
-      hipLaunchKernelGGL((mla_latent_kernel<64, true>), g, dim3(kMlaThreads), 0, stream, a);
+      hipLaunchKernelGGL((mla_group64_kernel<true>), g, dim3(kGThreads), 0, stream, a);
     } else {
-      hipLaunchKernelGGL((mla_latent_kernel<64, false>), g, dim3(kMlaThreads), 0, stream, a);
+      hipLaunchKernelGGL((mla_group64_kernel<false>), g, dim3(kGThreads), 0, stream, a);
     }
   } else {
     if (sparse) {
