@@ -71,8 +71,9 @@ struct MlaArgs {
   const uint16_t* __restrict__ lat;      // [slots, PT, 576]
   const int32_t* __restrict__ table;     // [B, max_pages]
   const int32_t* __restrict__ ctx_lens;  // [B] (sparse: selected counts)
-  float* __restrict__ part_o;            // [B, NR, H, 512]
-  float* __restrict__ part_ml;           // [B, NR, H, 2]
+  float* __restrict__ part_o;            // [B, NR, H, 512] fp32 sums (32-head groups)
+  void* __restrict__ part_o16;           // [B, NR, H, 512] fp16 rows (64-head groups)
+  float* __restrict__ part_ml;           // [B, NR, H, 2] (m, l); 64-head groups: [.., 4] (m, l, e, 0)
   const int32_t* __restrict__ sel;       // sparse: [B, sel_stride] positions, ascending
   int B, H, NR, max_pages, pt_shift, num_slots, sel_stride;
   uint32_t pool_bytes;                   // sparse: bytes of the latent pool (< 4 GiB)
@@ -879,7 +880,12 @@ void mla_group64_kernel(MlaArgs a) {
   // second tile buffer in the tile layout: one coalesced stream instead of 36
   // row-strided loads per wavefront, and the score operands are then read
   // with the conflict-free pattern of the latent rows (row 32 hh + l32).
+  // The first tile's loads are issued right behind q's (its table lookup
+  // first: that load's wait would also wait for q), and only q is waited for
+  // before its rows are read out, so the tile's latency overlaps that.
   {
+    uint32_t off[2];
+    const __amdgpu_buffer_rsrc_t r0 = tile_src(t_lo, off);  // empty past t_hi
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.q + (static_cast<size_t>(b) * a.H + head0) * kLat),
         static_cast<short>(0), HG * kLat * 2, 0x00020000);
@@ -889,7 +895,14 @@ void mla_group64_kernel(MlaArgs a) {
                                                ((k & 1) ? ld_base1 : ld_base0) + 128 * (k >> 1),
                                                0, 0, 0);
     }
-    wait_vmem_all();
+#pragma unroll
+    for (int k = 0; k < kGLoads; ++k) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r0, (lds_void*)(tile_a + (w + kGWaves * k) * 512),
+                                               16, static_cast<int>(off[k & 1] + 128 * (k >> 1)),
+                                               0, 0, 0);
+    }
+    static_assert(kGLoads == 18, "the wait below counts the first tile's 18 loads");
+    __builtin_amdgcn_s_waitcnt(0x4F72);  // gfx9 encoding: vmcnt 18 (q landed), lgkmcnt 15
     lds_barrier();
 #pragma unroll
     for (int s = 0; s < kGSteps; ++s) {
@@ -897,10 +910,10 @@ void mla_group64_kernel(MlaArgs a) {
                                                (hh - th) * 32 * 64);
     }
   }
-  for (;;) {
+  for (bool first_pass = true;; first_pass = false) {
     int t = t_lo;
     bool ok = true;
-    if (t < t_hi) load_tile(t, tile_a);
+    if (!first_pass) load_tile(t, tile_a);
     while (ok && t < t_hi) {
       ok = step(t, tile_a, tile_b);
       if (ok && t + 1 < t_hi) ok = step(t + 1, tile_b, tile_a);
@@ -923,34 +936,87 @@ void mla_group64_kernel(MlaArgs a) {
   }
 
   // ---- partial state of this (sequence, range, head group) ----
+  // Written as normalised rows o = acc / l in fp16, each (range, head) row
+  // scaled by 2^-e so that its largest magnitude stays below 2^15, with
+  // (m, l, e) beside it: half the bytes of fp32 sums, at 11 significant bits
+  // (the reduce multiplies 2^e back).  The rows go through LDS so that each
+  // store instruction writes 1 KiB of one row.
   const size_t pbase = (static_cast<size_t>(b) * a.NR + range) * a.H + head0;
+  const float lw = l_run + __shfl_xor(l_run, 32);
+  if (lh == 0) lsum_lds[th][32 * hh + l32] = lw;
+  wait_vmem_all();  // the last step's (empty) next-tile loads write tile_b
+  lds_barrier();
+  float inv[2], amax[2];
 #pragma unroll
   for (int ht = 0; ht < 2; ++ht) {
-    float* po = a.part_o + (pbase + 32 * ht + l32) * kC + 128 * w + 4 * lh;
+    const float l = lsum_lds[0][32 * ht + l32] + lsum_lds[1][32 * ht + l32];
+    inv[ht] = l > 0.f ? 1.f / l : 0.f;
+    float mx = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fabsf(acc[dt][ht][r]));
+    }
+    mx *= inv[ht];
+    amax[ht] = fmaxf(mx, __shfl_xor(mx, 32));
+  }
+  float* amax_lds = &tmax_lds[0][0][0];  // [4 wavefronts][64 heads]; the maxima are done with
+  if (lh == 0) {
+    amax_lds[w * HG + l32] = amax[0];
+    amax_lds[w * HG + 32 + l32] = amax[1];
+  }
+  lds_barrier();
+  constexpr int kStageRow = kC + 8;  // fp16 elements per staged row (1040 bytes)
+  _Float16* stage = reinterpret_cast<_Float16*>(tile_a);
+  int ex[2];
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    const int h = 32 * ht + l32;
+    const float rowmax = fmaxf(fmaxf(amax_lds[h], amax_lds[HG + h]),
+                               fmaxf(amax_lds[2 * HG + h], amax_lds[3 * HG + h]));
+    // e = max(0, ilogb(rowmax) - 14): rowmax 2^-e < 2^15 (finite rows only)
+    const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, rowmax) >> 23) & 0xff) - 127;
+    ex[ht] = (eb >= 15 && eb < 128) ? eb - 14 : 0;
+    const float f = inv[ht] * __builtin_bit_cast(float, static_cast<uint32_t>(127 - ex[ht]) << 23);
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * q) =
-            f32x4{acc[dt][ht][4 * q], acc[dt][ht][4 * q + 1], acc[dt][ht][4 * q + 2],
-                  acc[dt][ht][4 * q + 3]};
+        const f32x4 v = f32x4{acc[dt][ht][4 * q], acc[dt][ht][4 * q + 1], acc[dt][ht][4 * q + 2],
+                              acc[dt][ht][4 * q + 3]} * f;
+        *reinterpret_cast<f16x4*>(stage + h * kStageRow + 128 * w + 32 * dt + 8 * q + 4 * lh) =
+            __builtin_convertvector(v, f16x4);
       }
     }
   }
-  const float lw = l_run + __shfl_xor(l_run, 32);
-  if (lh == 0) lsum_lds[th][32 * hh + l32] = lw;
   lds_barrier();
+  // wavefront w stores heads 16 w .. 16 w + 15, one 1 KiB row per instruction
+  _Float16* po = static_cast<_Float16*>(a.part_o16) + pbase * kC;
+#pragma unroll
+  for (int i = 0; i < HG / kGWaves; ++i) {
+    const int h = (HG / kGWaves) * w + i;
+    *reinterpret_cast<u32x4*>(po + static_cast<size_t>(h) * kC + 8 * lane) =
+        *reinterpret_cast<const u32x4*>(stage + h * kStageRow + 8 * lane);
+  }
   if (w == 0) {
-    a.part_ml[(pbase + lane) * 2 + 0] = lh ? M[1] : M[0];
-    a.part_ml[(pbase + lane) * 2 + 1] = lsum_lds[0][lane] + lsum_lds[1][lane];
+    const int e = lh ? ex[1] : ex[0];
+    // lane = head: heads l32 and 32 + l32 sit in lanes l32 and l32 + 32
+    reinterpret_cast<f32x4*>(a.part_ml)[pbase + lane] =
+        f32x4{lh ? M[1] : M[0],
+              lsum_lds[0][lane] + lsum_lds[1][lane], static_cast<float>(e), 0.f};
   }
 }
 
 // One wavefront per (sequence, head): merges the NR range partials.  Lane r
 // holds range r's (m, l); the partial rows of a batch of ranges are all loaded
 // before the first is used (one memory round trip per batch).
+// F16 = false: rows are fp32 sums relative to 2^m, stats (m, l).
+// F16 = true: rows are fp16 o 2^-e with o = sum / l, stats (m, l, e, 0); the
+// row's weight is then 2^(m - M) l 2^e.
+template <bool F16>
 __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
-    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    const void* __restrict__ part_o, const float* __restrict__ part_ml,
     uint16_t* __restrict__ out, float* __restrict__ lse_out, int B, int H, int NR) {
   constexpr int DPL = kC / 64;  // 8 dims per lane
   constexpr int kBatch = 8;
@@ -959,7 +1025,6 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
   if (task >= B * H) return;
   const int b = task / H;
   const int h = task - b * H;
-  const float2* ml2 = reinterpret_cast<const float2*>(part_ml);
   float M = -INFINITY;
   float L = 0.f;
   f32x4 acc[DPL / 4];
@@ -967,35 +1032,58 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
   for (int c = 0; c < DPL / 4; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int r0 = 0; r0 < NR; r0 += 64) {
     const int r = r0 + lane;
-    const float2 ml = r < NR ? ml2[(static_cast<size_t>(b) * NR + r) * H + h]
-                             : make_float2(-INFINITY, 0.f);
+    const size_t ri = (static_cast<size_t>(b) * NR + r) * H + h;
+    float m = -INFINITY, l = 0.f, e = 0.f;
+    if (r < NR) {
+      if constexpr (F16) {
+        const f32x4 v = reinterpret_cast<const f32x4*>(part_ml)[ri];
+        m = v[0];
+        l = v[1];
+        e = v[2];
+      } else {
+        const float2 v = reinterpret_cast<const float2*>(part_ml)[ri];
+        m = v.x;
+        l = v.y;
+      }
+    }
     // cross-lane work by DPP moves and v_readlane (no LDS crossbar trips)
-    const float Mc = wave_max_uniform(ml.x);
+    const float Mc = wave_max_uniform(m);
     const float Mn = fmaxf(M, Mc);
     if (Mn == -INFINITY) continue;  // no tokens in any range so far
     const float rescale = fast_exp2(M - Mn);
-    const float wl = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - Mn);
-    const float Lc = wave_sum_uniform(ml.y * wl);
+    const float wl = m == -INFINITY ? 0.f : fast_exp2(m - Mn);
+    const float Lc = wave_sum_uniform(l * wl);
     L = L * rescale + Lc;
     M = Mn;
 #pragma unroll
     for (int c = 0; c < DPL / 4; ++c) acc[c] *= rescale;
+    // weight of a row: fp32 sums 2^(m - M); fp16 rows 2^(m - M) l 2^e
+    const float wrow = F16 ? wl * l * fast_exp2(e) : wl;
     const int cnt = NR - r0 < 64 ? NR - r0 : 64;
     for (int k0 = 0; k0 < cnt; k0 += kBatch) {
       f32x4 v[kBatch][DPL / 4];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int k = k0 + u < cnt ? k0 + u : cnt - 1;
-        const f32x4* po = reinterpret_cast<const f32x4*>(
-            part_o + ((static_cast<size_t>(b) * NR + r0 + k) * H + h) * kC + lane * DPL);
+        const size_t row = ((static_cast<size_t>(b) * NR + r0 + k) * H + h) * kC + lane * DPL;
+        if constexpr (F16) {
+          typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+          const f16x8 x = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(part_o) + row);
+          v[u][0] = f32x4{static_cast<float>(x[0]), static_cast<float>(x[1]),
+                          static_cast<float>(x[2]), static_cast<float>(x[3])};
+          v[u][1] = f32x4{static_cast<float>(x[4]), static_cast<float>(x[5]),
+                          static_cast<float>(x[6]), static_cast<float>(x[7])};
+        } else {
+          const f32x4* po = reinterpret_cast<const f32x4*>(static_cast<const float*>(part_o) + row);
 #pragma unroll
-        for (int c = 0; c < DPL / 4; ++c) v[u][c] = po[c];
+          for (int c = 0; c < DPL / 4; ++c) v[u][c] = po[c];
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const float wk = k0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                            __builtin_bit_cast(int, wl), k0 + u))
+                                            __builtin_bit_cast(int, wrow), k0 + u))
                                       : 0.f;
         // a range without tokens has weight 0 and an all-zero row
 #pragma unroll
@@ -1046,8 +1134,13 @@ int launch_mla(const MlaArgs& a, int hg, bool sparse, long long grid, uint16_t* 
   int rc = VOOM_LAUNCH_CHECK("mla: latent kernel launch");
   if (rc) return rc;
   const unsigned red_grid = static_cast<unsigned>((a.B * a.H + 3) / 4);
-  hipLaunchKernelGGL(mla_reduce_kernel, dim3(red_grid), dim3(kThreads), 0, stream, a.part_o,
-                     a.part_ml, out, lse_out, a.B, a.H, a.NR);
+  if (hg == 64) {
+    hipLaunchKernelGGL(mla_reduce_kernel<true>, dim3(red_grid), dim3(kThreads), 0, stream,
+                       static_cast<const void*>(a.part_o16), a.part_ml, out, lse_out, a.B, a.H, a.NR);
+  } else {
+    hipLaunchKernelGGL(mla_reduce_kernel<false>, dim3(red_grid), dim3(kThreads), 0, stream,
+                       static_cast<const void*>(a.part_o), a.part_ml, out, lse_out, a.B, a.H, a.NR);
+  }
   return VOOM_LAUNCH_CHECK("mla: reduce kernel launch");
 }
 
@@ -1184,19 +1277,37 @@ __global__ __launch_bounds__(kThreads) void head_gemv_kernel(
 
 using namespace voom;
 
+namespace voom {
+namespace {
+// Workspace of n = batch x ranges x heads partial rows: the rows (fp32 sums
+// for 32-head groups, fp16 for 64-head groups), 256-byte aligned, then the
+// per-row statistics ((m, l), or (m, l, e, 0) with the fp16 rows).
+size_t partial_rows_bytes(size_t n, int H) {
+  const size_t row = heads_per_group(H) == 64 ? kC * 2 : kC * sizeof(float);
+  return (n * row + 255) & ~size_t(255);
+}
+size_t partial_bytes(size_t n, int H) {
+  return partial_rows_bytes(n, H) + n * (heads_per_group(H) == 64 ? 4 : 2) * sizeof(float);
+}
+void set_partials(MlaArgs& a, void* workspace, size_t n) {
+  a.part_o = static_cast<float*>(workspace);
+  a.part_o16 = workspace;
+  a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + partial_rows_bytes(n, a.H));
+}
+}  // namespace
+}  // namespace voom
+
 extern "C" size_t voom_mla_sparse_workspace_bytes(int batch, int num_heads, int sel_stride,
                                                   int num_ranges) {
   if (batch <= 0 || num_heads <= 0 || sel_stride <= 0) return 0;
   if (num_ranges <= 0) num_ranges = sparse_ranges(batch, num_heads, sel_stride);
-  const size_t n = static_cast<size_t>(batch) * num_ranges * num_heads;
-  return ((n * kC * sizeof(float) + 255) & ~size_t(255)) + n * 2 * sizeof(float);
+  return partial_bytes(static_cast<size_t>(batch) * num_ranges * num_heads, num_heads);
 }
 
 extern "C" size_t voom_mla_workspace_bytes(int batch, int num_heads, int num_ranges) {
   if (batch <= 0 || num_heads <= 0) return 0;
   if (num_ranges <= 0) num_ranges = default_ranges(batch, num_heads);
-  const size_t n = static_cast<size_t>(batch) * num_ranges * num_heads;
-  return ((n * kC * sizeof(float) + 255) & ~size_t(255)) + n * 2 * sizeof(float);
+  return partial_bytes(static_cast<size_t>(batch) * num_ranges * num_heads, num_heads);
 }
 
 extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
@@ -1217,6 +1328,8 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
                "mla_absorbed_decode: page_tokens %d must be a power of two in [64, 4096]",
                page_tokens);
   VOOM_REQUIRE(max_pages > 0 && num_slots > 0, "mla_absorbed_decode: empty table or pool");
+  VOOM_REQUIRE(scale > 0.f && scale < INFINITY, "mla_absorbed_decode: scale %g must be positive",
+               static_cast<double>(scale));
   VOOM_REQUIRE(static_cast<long long>(max_pages) * page_tokens < (1LL << 30),
                "mla_absorbed_decode: table capacity too large");
   if (num_ranges <= 0) num_ranges = default_ranges(batch, num_heads);
@@ -1237,11 +1350,9 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
   a.lat = static_cast<const uint16_t*>(lat_pool);
   a.table = block_table;
   a.ctx_lens = ctx_lens;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                       ((n * kC * sizeof(float) + 255) & ~size_t(255)));
   a.B = batch;
   a.H = num_heads;
+  set_partials(a, workspace, n);
   a.NR = num_ranges;
   a.max_pages = max_pages;
   a.pt_shift = ilog2(page_tokens);
@@ -1271,6 +1382,8 @@ extern "C" int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool,
                "%s: page_tokens %d must be a power of two in [64, 4096]", who, page_tokens);
   VOOM_REQUIRE(max_pages > 0 && num_slots > 0 && sel_stride > 0, "%s: empty table, pool or selection",
                who);
+  VOOM_REQUIRE(scale > 0.f && scale < INFINITY, "%s: scale %g must be positive", who,
+               static_cast<double>(scale));
   const unsigned long long pool =
       static_cast<unsigned long long>(num_slots) * page_tokens * kLat * 2;
   VOOM_REQUIRE(pool < 0xFFFF0000ull,
@@ -1296,12 +1409,10 @@ extern "C" int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool,
   a.lat = static_cast<const uint16_t*>(lat_pool);
   a.table = block_table;
   a.ctx_lens = sel_lens;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                       ((n * kC * sizeof(float) + 255) & ~size_t(255)));
   a.sel = sel;
   a.B = batch;
   a.H = num_heads;
+  set_partials(a, workspace, n);
   a.NR = num_ranges;
   a.max_pages = max_pages;
   a.pt_shift = ilog2(page_tokens);
