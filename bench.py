@@ -682,14 +682,39 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
     flops = inp.latent_flops()
     # absorption GEMMs (q_nope . W_UK, weighted_c . W_UV) on their own, replayed
     # from a graph like the contraction (eager launches from Python would
-    # time the host)
-    def absorb():
-        ops.mla_absorb_query(inp.q_nope, inp.q_rope, w_uk)
-        ops.mla_project_out(out, w_uv_t)
+    # time the host).  Eight weight sets (8 x 33.6 MB) rotate so that the
+    # 256 MB Infinity Cache cannot serve them.
+    # The weights are packed once, as a deployment would at load time.
+    gw = torch.Generator(device="cuda").manual_seed(77)
+    w_sets = [(w_uk, w_uv_t)] + [
+        ((torch.randn(w_uk.shape, generator=gw, device="cuda") * 0.02).to(torch.bfloat16),
+         (torch.randn(w_uv_t.shape, generator=gw, device="cuda") * 0.02).to(torch.bfloat16))
+        for _ in range(7)]
+    w_sets = [(ops.pack_head_weights(a), ops.pack_head_weights(b)) for a, b in w_sets]
 
-    absorb()
+    def absorb(i):
+        wk, wv = w_sets[i % 8]
+        ops.mla_absorb_query(inp.q_nope, inp.q_rope, wk)
+        ops.mla_project_out(out, wv)
+
+    for i in range(8):
+        absorb(i)
     torch.cuda.synchronize()
-    t_gemm = graph_seconds([absorb], max(steps, 4))
+    t_gemm = graph_seconds([lambda i=i: absorb(i) for i in range(8)], max(1, steps // 8))
+
+    # the whole decode step of config 5: q absorption (with q_rope, one
+    # launch), latent kernel, merge of its partials fused with weighted_c .
+    # W_UV; rotating latent and weight sets
+    def full(i):
+        s_ = sets[i % 4]
+        wk, wv = w_sets[i % 8]
+        return ops.mla_absorbed_decode(s_.q_nope, s_.q_rope, s_.lat_pool, s_.block_table,
+                                       s_.ctx_lens, wk, wv, scale=s_.scale)
+
+    for i in range(8):
+        full(i)
+    torch.cuda.synchronize()
+    t_full = graph_seconds([lambda i=i: full(i) for i in range(8)], max(1, steps // 8))
     res = {
         "workload": "config 5: absorbed MLA decode, B=8, H=128, ctx 16384, latent 512+64 bf16 "
                     "in 64-token pages, 4 rotating input sets",
@@ -701,13 +726,18 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
         "bytes_per_call": nbytes,
         "flops_per_call": flops,
         "absorption_gemms_us": t_gemm * 1e6,
+        "absorption_gemms_note": "q_nope . W_UK with q_rope (one launch) + weighted_c . W_UV "
+                                 "(head_gemv), packed weights, 8 rotating weight sets",
+        "decode_step_us": t_full * 1e6,
+        "decode_step_note": "absorb_query + latent kernel + merge fused with the W_UV "
+                            "projection (3 launches), rotating inputs and weights",
         "traffic": profiled_traffic("mla_config5"),
         "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, calibrated; "
                           "profiles/mla_config5.md (latent kernel + reduce)",
     }
     log(f"config 5: latent kernel {t * 1e6:.1f} us, {res['hbm_gbs']:.0f} GB/s "
         f"({100 * res['hbm_frac']:.1f}% HBM), {res['mfma_tflops']:.0f} TFLOP/s; "
-        f"absorption GEMMs {t_gemm * 1e6:.1f} us")
+        f"absorption GEMMs {t_gemm * 1e6:.1f} us; whole decode step {t_full * 1e6:.1f} us")
     if cpu_sample:
         from oracle import mla as omla
 

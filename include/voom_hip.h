@@ -137,12 +137,31 @@ int voom_fold_attn_state(float* o_acc, float* lse_acc, const void* o_b, const fl
 /* voom_mla_head_gemv: y[b, h, n] = bf16(sum_k x[b, h, k] w[h, k, n]), fp32
  * sums, for the few query rows of a decode step -- the absorption products
  * q_nope . W_UK (runtime/glm.py:129-132) and weighted_c . W_UV
- * (runtime/glm.py:200-202) that hipBLASLt runs as batched GEMMs with M =
- * batch.  x [batch, num_heads, x_stride] (first k used), w [num_heads, k, n]
- * (16-byte aligned), y [batch, num_heads, y_stride] (first n written);
- * batch 1..16, k <= 512, n in 8, 16, ..., 512 with n / 8 dividing 64. */
-int voom_mla_head_gemv(const void* x, const void* w, void* y, int batch, int num_heads, int k,
-                       int n, int x_stride, int y_stride, hipStream_t stream);
+ * (runtime/glm.py:200-202) that the reference runs as batched products with
+ * M = batch.  x [batch, num_heads, x_stride] (first k used), w_packed from
+ * voom_mla_pack_head_weights for the same (num_heads, k, n), y [batch,
+ * num_heads, y_stride] (first n written); batch 1..16, any k, n >= 1. */
+int voom_mla_head_gemv(const void* x, const void* w_packed, void* y, int batch, int num_heads,
+                       int k, int n, int x_stride, int y_stride, hipStream_t stream);
+
+/* voom_mla_absorb_query: q_lat [batch, num_heads, c_dim + rope_dim] =
+ * [q_nope . W_UK | q_rope] in one launch (runtime/glm.py:129-132): q_nope
+ * [batch, num_heads, dn], q_rope [batch, num_heads, rope_dim], w_uk_packed
+ * = W_UK [num_heads, dn, c_dim] packed by voom_mla_pack_head_weights. */
+int voom_mla_absorb_query(const void* q_nope, const void* q_rope, const void* w_uk_packed,
+                          void* q_lat, int batch, int num_heads, int dn, int c_dim, int rope_dim,
+                          hipStream_t stream);
+
+/* Bytes of the packed form of per-head weights w [num_heads, k, n] bf16
+ * (k and n padded to multiples of 32 and 16). */
+size_t voom_mla_head_weights_bytes(int num_heads, int k, int n);
+
+/* Pack w [num_heads, k, n] bf16 into w_packed (voom_mla_head_weights_bytes,
+ * 16-byte aligned) in the operand order of voom_mla_head_gemv's matrix
+ * instructions; done once per weight matrix (the reference keeps W_UK and
+ * W_UV as slices of kv_b_proj, runtime/glm.py:124-125). */
+int voom_mla_pack_head_weights(const void* w, void* w_packed, int num_heads, int k, int n,
+                               hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Absorbed-MLA paged decode: the latent contraction.
@@ -168,6 +187,21 @@ int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
                              int batch, int num_heads, int latent_dim, int c_dim,
                              int page_tokens, int max_pages, int num_slots, float scale,
                              int num_ranges, hipStream_t stream);
+
+/* voom_mla_absorbed_decode_project: voom_mla_absorbed_decode followed by the
+ * output projection y [batch, num_heads, dv] = weighted_c . W_UV
+ * (runtime/glm.py:200-202), the merge of the range partials and the
+ * projection in one launch; num_heads a multiple of 64, batch <= 16, dv <=
+ * 128, w_uv_packed = W_UV^T [num_heads, c_dim, dv] packed by
+ * voom_mla_pack_head_weights.  wc_out [batch, num_heads, c_dim] (weighted_c,
+ * bf16) and lse_out are optional (null). */
+int voom_mla_absorbed_decode_project(const void* q_lat, const void* lat_pool,
+                                     const int32_t* block_table, const int32_t* ctx_lens,
+                                     const void* w_uv_packed, int dv, void* y, void* wc_out,
+                                     float* lse_out, void* workspace, size_t ws_bytes, int batch,
+                                     int num_heads, int latent_dim, int c_dim, int page_tokens,
+                                     int max_pages, int num_slots, float scale, int num_ranges,
+                                     hipStream_t stream);
 
 /* The same contraction over a selection of each sequence's positions: the
  * DSA gather of the top-k latent rows feeding absorbed MLA

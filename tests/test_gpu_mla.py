@@ -83,6 +83,39 @@ def test_full_pipeline_matches_absorbed_and_expanded_oracles():
         np.testing.assert_allclose(got, ref_exp[0, :, 0], atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("heads,ctx", [(64, [500, 130, 64]), (128, [1000, 1])])
+def test_fused_merge_and_projection(heads, ctx):
+    """64-head groups: the merge of the range partials and weighted_c . W_UV in
+    one launch give the bits of the two-launch path and match the oracles."""
+    print(f"[mla] fused merge + projection H={heads} ctx={ctx}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=len(ctx), heads=heads, ctx_lens=ctx)
+    w_uk, w_uv_t = ops.split_kv_b(inp.kv_b, heads, inp.dn, inp.dv)
+    q_lat = ops.mla_absorb_query(inp.q_nope, inp.q_rope, ops.pack_head_weights(w_uk))
+    y, wc, lse = ops.mla_latent_decode_project(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                                               w_uv_t, scale=inp.scale, return_weighted_c=True,
+                                               return_lse=True)
+    wc2, lse2 = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                                      scale=inp.scale, return_lse=True)
+    y2 = ops.mla_project_out(wc2, w_uv_t)
+    out = ops.mla_absorbed_decode(inp.q_nope, inp.q_rope, inp.lat_pool, inp.block_table,
+                                  inp.ctx_lens, w_uk, w_uv_t, scale=inp.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(wc.view(torch.int16), wc2.view(torch.int16))
+    assert torch.equal(lse, lse2)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), y.view(torch.int16))
+    kv_b = inp.kv_b.float().cpu().numpy()
+    for b in range(len(ctx)):
+        lat = synthetic.mla_logical_latent(inp, b)
+        qn = inp.q_nope[b:b + 1, :, None].float().cpu().numpy()
+        qr = inp.q_rope[b:b + 1, :, None].float().cpu().numpy()
+        S = lat.shape[0]
+        ref_bf, _ = omla.absorbed(qn, qr, lat[None], kv_b, inp.dn, inp.dv, offset=S - 1,
+                                  bf16=True)
+        np.testing.assert_allclose(y[b].float().cpu().numpy(), ref_bf[0, :, 0], atol=ATOL,
+                                   rtol=RTOL)
+
+
 def test_paging_invariance_is_bitwise():
     print("[mla] paging invariance", flush=True)
     inp = synthetic.mla_decode_inputs(batch=2, heads=32, ctx_lens=[700, 333], slack_pages=7)
@@ -106,7 +139,8 @@ def test_config5_full_size_two_sequences():
 
 
 @pytest.mark.parametrize("B,H,K,N", [(8, 128, 128, 512), (8, 128, 512, 128), (3, 5, 40, 64),
-                                     (16, 4, 512, 512), (1, 2, 1, 8), (9, 3, 100, 256)])
+                                     (16, 4, 512, 512), (1, 2, 1, 8), (9, 3, 100, 256),
+                                     (2, 3, 64, 24), (5, 7, 1000, 40)])
 def test_head_gemv_is_the_fp32_per_head_product_rounded(B, H, K, N):
     print(f"[mla] head_gemv B={B} H={H} K={K} N={N}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(B * 1000 + H + K + N)
@@ -132,7 +166,14 @@ def test_head_gemv_writes_into_a_wider_row_and_rejects_bad_shapes():
     torch.cuda.synchronize()
     assert torch.equal(out[..., :32].view(torch.int16), ref.view(torch.int16))
     assert bool((out[..., 32:] == 7.0).all())
+    # weights packed once give the same bits as weights packed per call
+    packed = ops.pack_head_weights(w)
+    again = ops.head_gemv(x, packed)
+    torch.cuda.synchronize()
+    assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
     with pytest.raises(ValueError):
         ops.head_gemv(torch.zeros((17, 3, 64), dtype=torch.bfloat16, device="cuda"), w)
     with pytest.raises(ValueError):
-        ops.head_gemv(x, torch.zeros((3, 64, 24), dtype=torch.bfloat16, device="cuda"))
+        ops.head_gemv(x, torch.zeros((3, 48, 32), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError):
+        ops.head_gemv(x[:, :2], packed)

@@ -42,6 +42,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_mla_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "voom_mla_absorbed_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int,
                                          c_int, c_int, c_int, c_int, c_int, c_float, c_int, _P]),
+    "voom_mla_absorbed_decode_project": (c_int, [_P, _P, _P, _P, _P, c_int, _P, _P, _P, _P, c_size_t,
+                                                 c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                                 c_float, c_int, _P]),
     "voom_mla_sparse_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "voom_mla_sparse_decode": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_size_t, c_int, c_int,
                                        c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
@@ -58,6 +61,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                      c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                      _P]),
     "voom_mla_head_gemv": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, _P]),
+    "voom_mla_head_weights_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "voom_mla_pack_head_weights": (c_int, [_P, _P, c_int, c_int, c_int, _P]),
+    "voom_mla_absorb_query": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P]),
     "voom_lm_head_argmax": (c_int, [_P, _P, _P, c_float, _P, c_int, c_int, _P, c_size_t, _P, _P,
                                     _P]),
     "voom_add_rms_norm_gemv": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int, c_int,

@@ -47,6 +47,8 @@ constexpr int kRow = kChunksPerRow * 8;        // LDS row stride in bf16 element
 constexpr int kTileChunks = kTile * kChunksPerRow;  // 4608 = 72 x 64
 constexpr int kLoadsPerTile = kTileChunks / 64;     // 72 wave-wide 16-byte loads
 constexpr int kQSteps = kLat / 32;  // 18 k-steps of the score MFMA
+constexpr int kHgTile = 16;  // per-head products: output columns per 16x16x32 MFMA tile
+constexpr int kHgStep = 32;  // per-head products: k per MFMA
 constexpr int kPRow = kTile + 16;   // P row stride (160 B = 10 chunks): the 16 head rows
                                     // of a 32-lane read phase fall on distinct banks
 
@@ -1008,28 +1010,25 @@ void mla_group64_kernel(MlaArgs a) {
   }
 }
 
-// One wavefront per (sequence, head): merges the NR range partials.  Lane r
-// holds range r's (m, l); the partial rows of a batch of ranges are all loaded
-// before the first is used (one memory round trip per batch).
+// Merge of the NR range partials of (sequence b, head h) by one wavefront:
+// lane r holds range r's statistics; the partial rows of a batch of ranges
+// are all loaded before the first is used (one memory round trip per batch).
 // F16 = false: rows are fp32 sums relative to 2^m, stats (m, l).
 // F16 = true: rows are fp16 o 2^-e with o = sum / l, stats (m, l, e, 0); the
-// row's weight is then 2^(m - M) l 2^e.
+// row's weight is then 2^(m - M) l 2^e.  Lane `lane` ends with dims
+// 8 lane .. 8 lane + 7 of sum_r weight_r row_r in acc, and M, L such that the
+// merged row is acc / L with log-sum-exp M + log2 L (log2 units).
+constexpr int kDPL = kC / 64;  // 8 dims per lane
 template <bool F16>
-__global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
-    const void* __restrict__ part_o, const float* __restrict__ part_ml,
-    uint16_t* __restrict__ out, float* __restrict__ lse_out, int B, int H, int NR) {
-  constexpr int DPL = kC / 64;  // 8 dims per lane
+__device__ __forceinline__ void merge_ranges(const void* __restrict__ part_o,
+                                             const float* __restrict__ part_ml, int b, int h,
+                                             int H, int NR, int lane, f32x4 (&acc)[kDPL / 4],
+                                             float& M, float& L) {
   constexpr int kBatch = 8;
-  const int lane = threadIdx.x & 63;
-  const int task = blockIdx.x * (kThreads / 64) + uniform(threadIdx.x >> 6);
-  if (task >= B * H) return;
-  const int b = task / H;
-  const int h = task - b * H;
-  float M = -INFINITY;
-  float L = 0.f;
-  f32x4 acc[DPL / 4];
+  M = -INFINITY;
+  L = 0.f;
 #pragma unroll
-  for (int c = 0; c < DPL / 4; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < kDPL / 4; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int r0 = 0; r0 < NR; r0 += 64) {
     const int r = r0 + lane;
     const size_t ri = (static_cast<size_t>(b) * NR + r) * H + h;
@@ -1056,16 +1055,16 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
     L = L * rescale + Lc;
     M = Mn;
 #pragma unroll
-    for (int c = 0; c < DPL / 4; ++c) acc[c] *= rescale;
+    for (int c = 0; c < kDPL / 4; ++c) acc[c] *= rescale;
     // weight of a row: fp32 sums 2^(m - M); fp16 rows 2^(m - M) l 2^e
     const float wrow = F16 ? wl * l * fast_exp2(e) : wl;
     const int cnt = NR - r0 < 64 ? NR - r0 : 64;
     for (int k0 = 0; k0 < cnt; k0 += kBatch) {
-      f32x4 v[kBatch][DPL / 4];
+      f32x4 v[kBatch][kDPL / 4];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int k = k0 + u < cnt ? k0 + u : cnt - 1;
-        const size_t row = ((static_cast<size_t>(b) * NR + r0 + k) * H + h) * kC + lane * DPL;
+        const size_t row = ((static_cast<size_t>(b) * NR + r0 + k) * H + h) * kC + lane * kDPL;
         if constexpr (F16) {
           typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
           const f16x8 x = *reinterpret_cast<const f16x8*>(static_cast<const _Float16*>(part_o) + row);
@@ -1076,7 +1075,7 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
         } else {
           const f32x4* po = reinterpret_cast<const f32x4*>(static_cast<const float*>(part_o) + row);
 #pragma unroll
-          for (int c = 0; c < DPL / 4; ++c) v[u][c] = po[c];
+          for (int c = 0; c < kDPL / 4; ++c) v[u][c] = po[c];
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1087,21 +1086,161 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
                                       : 0.f;
         // a range without tokens has weight 0 and an all-zero row
 #pragma unroll
-        for (int c = 0; c < DPL / 4; ++c) acc[c] += v[u][c] * wk;
+        for (int c = 0; c < kDPL / 4; ++c) acc[c] += v[u][c] * wk;
       }
     }
   }
+}
+
+// The merged row as bf16 (dims 8 lane .. + 7, one 16-byte word per lane).
+__device__ __forceinline__ u32x4 merged_row_bf16(const f32x4 (&acc)[kDPL / 4], float L) {
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  uint32_t pk[DPL / 2];
+  return u32x4{pack_bf16x2(acc[0][0] * inv, acc[0][1] * inv),
+               pack_bf16x2(acc[0][2] * inv, acc[0][3] * inv),
+               pack_bf16x2(acc[1][0] * inv, acc[1][1] * inv),
+               pack_bf16x2(acc[1][2] * inv, acc[1][3] * inv)};
+}
+
+__device__ __forceinline__ float merged_lse(float M, float L) {
+  return L > 0.f ? (M + __log2f(L)) * 0.6931471805599453f : -INFINITY;
+}
+
+// One wavefront per (sequence, head): merges the range partials into
+// weighted_c [B, H, 512] bf16 (and the log-sum-exp).
+template <bool F16>
+__global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
+    const void* __restrict__ part_o, const float* __restrict__ part_ml,
+    uint16_t* __restrict__ out, float* __restrict__ lse_out, int B, int H, int NR) {
+  const int lane = threadIdx.x & 63;
+  const int task = blockIdx.x * (kThreads / 64) + uniform(threadIdx.x >> 6);
+  if (task >= B * H) return;
+  const int b = task / H;
+  const int h = task - b * H;
+  f32x4 acc[kDPL / 4];
+  float M, L;
+  merge_ranges<F16>(part_o, part_ml, b, h, H, NR, lane, acc, M, L);
+  *reinterpret_cast<u32x4*>(out + static_cast<size_t>(task) * kC + lane * kDPL) =
+      merged_row_bf16(acc, L);
+  if (lse_out != nullptr && lane == 0) lse_out[task] = merged_lse(M, L);
+}
+
+// Merge and output projection fused, one workgroup per head (64-head-group
+// partials): weighted_c [b, h, :] for every sequence b, rounded to bf16 as the
+// reference rounds it (runtime/glm.py:162-164), then y [b, h, :dv] =
+// weighted_c . W_UV (runtime/glm.py:200-202) on v_mfma_f32_16x16x32_bf16 with
+// the sequences as the M = 16 dimension.  W_UV[h] (packed as for
+// voom_mla_head_gemv, dv <= 128: at most 128 KiB) streams into LDS from the
+// first instruction on, beside the partial rows the merge reads, so one
+// launch replaces the merge and the projection's weight stream.  Eight
+// wavefronts: wavefront w merges sequences w, w + 8, then projects column
+// tiles w, w + 8.
+constexpr int kRpMaxTiles = 8;                 // dv <= 128
+constexpr int kRpSteps = kC / kHgStep;         // 16 k-steps over the 512 latent dims
+constexpr int kRpThreads = 512;                // 8 wavefronts: one per sequence, one per tile
+__global__ __launch_bounds__(kRpThreads) void mla_reduce_project_kernel(
+    const void* __restrict__ part_o16, const float* __restrict__ part_ml,
+    const uint16_t* __restrict__ w_uv, uint16_t* __restrict__ y, uint16_t* __restrict__ wc_out,
+    float* __restrict__ lse_out, int B, int H, int NR, int DV, int NT, int splits) {
+  __shared__ __attribute__((aligned(16))) uint16_t wl[kRpMaxTiles * kRpSteps * 512];
+  __shared__ __attribute__((aligned(16))) uint16_t wcs[16][kC + 8];
+  // workgroups h + H part (same XCD for every part of a head when H % 8 == 0,
+  // so the parts' reads of the head's partial rows meet in one L2) split the
+  // head's column tiles; each merges all rows, part 0 writes weighted_c / lse
+  const int h = blockIdx.x % H;
+  const int part = blockIdx.x / H;
+  const int tpp = (NT + splits - 1) / splits;  // column tiles per part
+  const int nt_lo = part * tpp;
+  const int nt_hi = nt_lo + tpp < NT ? nt_lo + tpp : NT;
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  constexpr int kWaves = kRpThreads / kWave;
+  // The merge's loads go out first (statistics and, for up to kRpRanges
+  // ranges, every partial row), then the weight stream: the merge waits only
+  // for its own loads, which the wait counter drains in issue order.
+  constexpr int kRpRanges = 16;
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  const int bw = w < B ? w : 0;  // wavefronts past B merge row 0 and keep nothing
+  const bool small = NR <= kRpRanges;
+  f32x4 st = f32x4{-INFINITY, 0.f, 0.f, 0.f};
+  f16x8 rows[kRpRanges];
+  if (small) {
+    if (lane < NR) st = reinterpret_cast<const f32x4*>(part_ml)[(static_cast<size_t>(bw) * NR + lane) * H + h];
 #pragma unroll
-  for (int c = 0; c < DPL / 4; ++c) {
-    pk[2 * c] = pack_bf16x2(acc[c][0] * inv, acc[c][1] * inv);
-    pk[2 * c + 1] = pack_bf16x2(acc[c][2] * inv, acc[c][3] * inv);
+    for (int r = 0; r < kRpRanges; ++r) {
+      const int rr = r < NR ? r : NR - 1;
+      rows[r] = *reinterpret_cast<const f16x8*>(
+          static_cast<const _Float16*>(part_o16) +
+          ((static_cast<size_t>(bw) * NR + rr) * H + h) * kC + lane * kDPL);
+    }
   }
-  *reinterpret_cast<u32x4*>(out + static_cast<size_t>(task) * kC + lane * DPL) =
-      u32x4{pk[0], pk[1], pk[2], pk[3]};
-  if (lse_out != nullptr && lane == 0) {
-    lse_out[task] = L > 0.f ? (M + __log2f(L)) * 0.6931471805599453f : -INFINITY;
+  {
+    // this part's tiles: blocks nt_lo * 16 .. nt_hi * 16 (1 KiB each) of the head
+    const int blocks = (nt_hi - nt_lo) * kRpSteps;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(w_uv + (static_cast<size_t>(h) * NT + nt_lo) * kRpSteps * 512),
+        static_cast<short>(0), blocks * 1024, 0x00020000);
+    for (int i = w; i < blocks; i += kWaves) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(wl + i * 512), 16, i * 1024 + lane * 16,
+                                               0, 0, 0);
+    }
+  }
+  for (int b = w; b < B; b += kWaves) {
+    f32x4 acc[kDPL / 4];
+    float M, L;
+    if (small && b == w) {
+      // all ranges at once: weights 2^(m - M) l 2^e, lane r holding range r
+      const float m = st[0], l = st[1], e = st[2];
+      M = wave_max_uniform(m);
+      const float wl_ = m == -INFINITY ? 0.f : fast_exp2(m - M);
+      L = wave_sum_uniform(l * wl_);
+      const float wrow = wl_ * l * fast_exp2(e);
+      acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int r = 0; r < kRpRanges; ++r) {
+          const float wk = r < NR ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                        __builtin_bit_cast(int, wrow), r))
+                                  : 0.f;
+          acc[0] += f32x4{static_cast<float>(rows[r][0]), static_cast<float>(rows[r][1]),
+                          static_cast<float>(rows[r][2]), static_cast<float>(rows[r][3])} * wk;
+          acc[1] += f32x4{static_cast<float>(rows[r][4]), static_cast<float>(rows[r][5]),
+                          static_cast<float>(rows[r][6]), static_cast<float>(rows[r][7])} * wk;
+        }
+      }
+    } else {
+      merge_ranges<true>(part_o16, part_ml, b, h, H, NR, lane, acc, M, L);
+    }
+    const u32x4 row = merged_row_bf16(acc, L);
+    *reinterpret_cast<u32x4*>(&wcs[b][lane * kDPL]) = row;
+    const size_t task = static_cast<size_t>(b) * H + h;
+    if (part == 0 && wc_out != nullptr) {
+      *reinterpret_cast<u32x4*>(wc_out + task * kC + lane * kDPL) = row;
+    }
+    if (part == 0 && lse_out != nullptr && lane == 0) lse_out[task] = merged_lse(M, L);
+  }
+  wait_vmem_all();  // this wave's weight loads; the barrier makes it everyone's
+  lds_barrier();
+  const int bq = lane & 15;
+  const int kq = 8 * (lane >> 4);
+  for (int nt = nt_lo + w; nt < nt_hi; nt += kWaves) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kRpSteps; ++s) {
+      const u32x4 av = bq < B ? *reinterpret_cast<const u32x4*>(&wcs[bq][kHgStep * s + kq])
+                              : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 bv =
+          *reinterpret_cast<const u32x4*>(wl + ((nt - nt_lo) * kRpSteps + s) * 512 + lane * 8);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                    __builtin_bit_cast(bf16x8, bv), acc, 0, 0, 0);
+    }
+    const int n = kHgTile * nt + (lane & 15);
+    if (n < DV) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * (lane >> 4) + r;
+        if (row < B) y[(static_cast<size_t>(row) * H + h) * DV + n] = f2bf(acc[r]);
+      }
+    }
   }
 }
 
@@ -1144,6 +1283,24 @@ int launch_mla(const MlaArgs& a, int hg, bool sparse, long long grid, uint16_t* 
   return VOOM_LAUNCH_CHECK("mla: reduce kernel launch");
 }
 
+// Latent kernel (64-head groups) and the fused merge + output projection.
+int launch_mla_project(const MlaArgs& a, long long grid, const void* w_uv_packed, int dv,
+                       void* y, uint16_t* wc_out, float* lse_out, hipStream_t stream) {
+  hipLaunchKernelGGL((mla_group64_kernel<false>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kGThreads), 0, stream, a);
+  int rc = VOOM_LAUNCH_CHECK("mla: latent kernel launch");
+  if (rc) return rc;
+  const int nt = (dv + kHgTile - 1) / kHgTile;
+  // two parts per head when there are at least two column tiles: twice the
+  // workgroups for the weight stream
+  const int splits = nt >= 2 ? 2 : 1;
+  hipLaunchKernelGGL(mla_reduce_project_kernel, dim3(static_cast<unsigned>(a.H * splits)),
+                     dim3(kRpThreads), 0, stream, static_cast<const void*>(a.part_o16), a.part_ml,
+                     static_cast<const uint16_t*>(w_uv_packed), static_cast<uint16_t*>(y), wc_out,
+                     lse_out, a.B, a.H, a.NR, dv, nt, splits);
+  return VOOM_LAUNCH_CHECK("mla: merge + projection kernel launch");
+}
+
 // Ranges for a selection of at most sel_stride positions: one per two 64-row
 // tiles (a selection is short, and every range costs a partial row per head
 // that the reduce reads back) unless the dense default is lower, and never so
@@ -1163,113 +1320,166 @@ int sparse_ranges(int B, int H, int sel_stride) {
 
 // ------------------------------------------------------ per-head products ----
 // y[b, h, n] = sum_k x[b, h, k] w[h, k, n] for the few query rows of a decode
-// step (B <= 16): q_nope . W_UK and weighted_c . W_UV^T of absorbed MLA.  A
-// batched GEMM with M = B spends most of its time on empty tile rows; this is
-// a weight stream.  One workgroup per (head, column part): x[:, h, :] goes to
-// LDS as fp32, then lane (kk, nl) of each wavefront walks k = 4 KR i + KR
-// wave + kk, loads w[h, k, c0 + 8 nl .. + 7] 16 rows at a time (non-temporal:
-// each weight byte is read once) and accumulates all B rows against them.
-// The partial sums of the (wavefront, kk) groups meet in LDS in a fixed
-// order, so the result does not depend on scheduling.
-constexpr int kHgMaxK = 512;
-constexpr int kHgMaxN = 512;
+// step (B <= 16): q_nope . W_UK and weighted_c . W_UV^T of absorbed MLA.  The
+// work is a weight stream (2 x 16.8 MB at config 5 against 1 MB of rows), and
+// fp32 FMAs over it would cost as much VALU time as the stream takes, so the
+// products run on v_mfma_f32_16x16x32_bf16 with the batch as the (padded)
+// M = 16 dimension: A = x rows, B = a 32 x 16 block of w.
+//
+// Weights are packed once (voom_mla_pack_head_weights) in MFMA operand order:
+// for head h, column tile nt (16 columns) and k-step s (32 rows) a 1 KiB
+// block in which lane l holds w[32 s + 8 (l / 16) + e][16 nt + l % 16],
+// e = 0..7 -- every weight load is one contiguous 1 KiB per wavefront.  K and
+// N are zero-padded to multiples of 32 and 16.
+constexpr int kHgChunk = 16;    // k-steps whose weight loads are issued together
 
-template <int BM>
+// Packs w [H, K, N] (bf16) into [H, Np / 16, Kp / 32, 64, 8].
+__global__ __launch_bounds__(kThreads) void pack_head_weights_kernel(
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ wp, int H, int K, int N, int NT,
+    int KS) {
+  const long long total = static_cast<long long>(H) * NT * KS * 64;
+  const long long p = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (p >= total) return;
+  const int l = static_cast<int>(p & 63);
+  long long r = p >> 6;
+  const int s = static_cast<int>(r % KS);
+  r /= KS;
+  const int nt = static_cast<int>(r % NT);
+  const int h = static_cast<int>(r / NT);
+  const int n = kHgTile * nt + (l & 15);
+  const int k0 = kHgStep * s + 8 * (l >> 4);
+  uint32_t v[4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const int ka = k0 + e, kb = k0 + e + 1;
+    const uint32_t lo = (ka < K && n < N) ? w[(static_cast<size_t>(h) * K + ka) * N + n] : 0u;
+    const uint32_t hi = (kb < K && n < N) ? w[(static_cast<size_t>(h) * K + kb) * N + n] : 0u;
+    v[e >> 1] = lo | (hi << 16);
+  }
+  *reinterpret_cast<u32x4*>(wp + p * 8) = u32x4{v[0], v[1], v[2], v[3]};
+}
+
+// Each wavefront takes TPW adjacent 16-column tiles of one head and walks K in
+// chunks of KC k-steps; the TPW x KC = 16 weight loads of a chunk (16 KiB per
+// wavefront) are all issued before its first MFMA, and the x operands of a
+// k-step serve all TPW tiles.  Four wavefronts per workgroup, no LDS and no
+// barriers.  Lane l's x operand is row b = l % 16 (zero for b >= B) at k =
+// 32 s + 8 (l / 16) .. + 7; a 16 x 16 result has lane l holding column l % 16
+// of rows 4 (l / 16) .. + 3.  tail (optional): tail[b, h, 0 .. tail_cols) is
+// copied to y[b, h, N ..] by the first wavefront of each head (q_rope beside
+// q_nope . W_UK in q_lat).
+template <int KC, int TPW>
 __global__ __launch_bounds__(kThreads) void head_gemv_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
-    int B, int H, int K, int N, int NW, int x_stride, int y_stride) {
-  // x rows while the weights stream, then the wavefronts' partial sums
-  __shared__ float lds[(kThreads / kWave) * BM * kHgMaxN];
-  static_assert(kHgMaxK <= (kThreads / kWave) * kHgMaxN, "x rows fit the reduction space");
-  float (*xs)[BM] = reinterpret_cast<float (*)[BM]>(lds);
-  const int h = blockIdx.x;
-  const int c0 = blockIdx.y * NW;  // this workgroup's columns c0 .. c0 + NW - 1
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wv = tid / kWave;
-  // adjacent threads read adjacent k of one row (coalesced).  Every load is
-  // unconditional (dead slots reread row 0, column 0) and all are issued
-  // before the first store: a conditional load is waited for on its own.
-  constexpr int kStage = kHgMaxK * BM / kThreads;
-  uint16_t xr[kStage];
-#pragma unroll
-  for (int j = 0; j < kStage; ++j) {
-    const int i = tid + j * kThreads;
-    const int b = i / K;
-    const int k = i - b * K;
-    const bool live = i < K * BM && b < B;
-    xr[j] = x[(static_cast<size_t>(live ? b : 0) * H + h) * x_stride + (live ? k : 0)];
-  }
-#pragma unroll
-  for (int j = 0; j < kStage; ++j) {
-    const int i = tid + j * kThreads;
-    if (i < K * BM) {
-      const int b = i / K;
-      const int k = i - b * K;
-      xs[k][b] = b < B ? bf2f(xr[j]) : 0.f;
-    }
-  }
-  __syncthreads();
-  const int NL = NW / 8;      // lanes across the workgroup's part of one weight row
-  const int KR = kWave / NL;  // weight rows per wavefront load
-  const int kk = lane / NL;
-  const int n0 = 8 * (lane - kk * NL);
-  float acc[BM][8];
-#pragma unroll
-  for (int b = 0; b < BM; ++b) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[b][e] = 0.f;
-  }
-  const uint16_t* wh = w + static_cast<size_t>(h) * K * N + c0 + n0;
-  const int step = (kThreads / kWave) * KR;
-  constexpr int kInFlight = 16;  // weight loads issued before the first use
-  for (int kb = wv * KR + kk; kb < K; kb += kInFlight * step) {
-    u32x4 q[kInFlight];
-#pragma unroll
-    for (int i = 0; i < kInFlight; ++i) {
-      const int k = kb + i * step;
-      q[i] = k < K ? __builtin_nontemporal_load(
-                         reinterpret_cast<const u32x4*>(wh + static_cast<size_t>(k) * N))
-                   : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < kInFlight; ++i) {
-      const int k = kb + i * step;
-      if (k >= K) break;
-      float wf[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        wf[2 * e] = bf2f(static_cast<uint16_t>(q[i][e] & 0xffffu));
-        wf[2 * e + 1] = bf2f(static_cast<uint16_t>(q[i][e] >> 16));
-      }
-#pragma unroll
-      for (int b = 0; b < BM; ++b) {
-        const float xb = xs[k][b];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[b][e] = __builtin_fmaf(xb, wf[e], acc[b][e]);
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wp, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ tail, int B, int H, int K, int N, int NT, int KS, int x_stride,
+    int y_stride, int x_vec, int tail_cols, int tail_stride) {
+  static_assert(KC * TPW == kHgChunk, "16 weight loads per chunk");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * (kThreads / kWave) + uniform(threadIdx.x / kWave);
+  const int h = blockIdx.y;
+  if (tail != nullptr && wave == 0) {
+    for (int c = lane; c < tail_cols; c += kWave) {
+      for (int bb = 0; bb < B; ++bb) {
+        y[(static_cast<size_t>(bb) * H + h) * y_stride + N + c] =
+            tail[(static_cast<size_t>(bb) * H + h) * tail_stride + c];
       }
     }
   }
-  // every (wavefront, kk) group leaves its partial sums in LDS -- 4 KR groups
-  // of [BM][NW], exactly the buffer (KR NW = 512) -- and each output sums
-  // them in group order
-  __syncthreads();  // every wavefront is done with the x rows
-  const int groups = (kThreads / kWave) * KR;
-  float* red = lds;
-  const int grp = wv * KR + kk;
+  const int nt0 = wave * TPW;
+  if (nt0 >= NT) return;
+  const int b = lane & 15;
+  const int kq = 8 * (lane >> 4);
+  const uint16_t* xr = x + (static_cast<size_t>(b < B ? b : 0) * H + h) * x_stride;
+  f32x4 acc[TPW];
 #pragma unroll
-  for (int b = 0; b < BM; ++b) {
+  for (int j = 0; j < TPW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < KS; s0 += KC) {
+    u32x4 wq[TPW][KC];
+    u32x4 xq[KC];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[(grp * BM + b) * NW + n0 + e] = acc[b][e];
+    for (int j = 0; j < TPW; ++j) {
+      // tiles past NT and k-steps past KS reread a valid block, unused
+      const int nt = nt0 + j < NT ? nt0 + j : NT - 1;
+      const u32x4* wt = reinterpret_cast<const u32x4*>(wp) +
+                        (static_cast<size_t>(h) * NT + nt) * KS * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < KC; ++i) {
+        const int s = s0 + i < KS ? s0 + i : KS - 1;
+        wq[j][i] = __builtin_nontemporal_load(wt + static_cast<size_t>(s) * 64);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      const int k = kHgStep * (s0 + i) + kq;
+      if (x_vec) {
+        // rows 16-byte aligned with K % 8 == 0: whole 8-element pieces
+        xq[i] = (b < B && k < K) ? *reinterpret_cast<const u32x4*>(xr + k)
+                                 : u32x4{0u, 0u, 0u, 0u};
+      } else {
+        uint32_t v[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const uint32_t lo = (b < B && k + e < K) ? xr[k + e] : 0u;
+          const uint32_t hi = (b < B && k + e + 1 < K) ? xr[k + e + 1] : 0u;
+          v[e >> 1] = lo | (hi << 16);
+        }
+        xq[i] = u32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      if (s0 + i < KS) {
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xq[i]),
+                                                           __builtin_bit_cast(bf16x8, wq[j][i]),
+                                                           acc[j], 0, 0, 0);
+        }
+      }
+    }
   }
-  __syncthreads();
-  for (int i = tid; i < B * NW; i += kThreads) {
-    const int b = i / NW;
-    const int n = i - b * NW;
-    float v = red[b * NW + n];
-    for (int g = 1; g < groups; ++g) v += red[(g * BM + b) * NW + n];
-    y[(static_cast<size_t>(b) * H + h) * y_stride + c0 + n] = f2bf(v);
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int n = kHgTile * (nt0 + j) + (lane & 15);
+    if (nt0 + j < NT && n < N) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * (lane >> 4) + r;
+        if (row < B) y[(static_cast<size_t>(row) * H + h) * y_stride + n] = f2bf(acc[j][r]);
+      }
+    }
   }
+}
+
+int launch_head_gemv(const void* x, const void* w_packed, void* y, const void* tail, int batch,
+                     int num_heads, int k, int n, int x_stride, int y_stride, int tail_cols,
+                     int tail_stride, hipStream_t stream) {
+  const int nt = (n + kHgTile - 1) / kHgTile;
+  const int ks = (k + kHgStep - 1) / kHgStep;
+  const int x_vec = (k % 8 == 0 && x_stride % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  // short K: several tiles per wavefront share each x operand
+  const int tpw = ks <= 4 ? 4 : (ks <= 8 ? 2 : 1);
+  const int waves = (nt + tpw - 1) / tpw;
+  const dim3 grid(static_cast<unsigned>((waves + kThreads / kWave - 1) / (kThreads / kWave)),
+                  static_cast<unsigned>(num_heads));
+  const auto* xv = static_cast<const uint16_t*>(x);
+  const auto* wv = static_cast<const uint16_t*>(w_packed);
+  auto* yv = static_cast<uint16_t*>(y);
+  const auto* tv = static_cast<const uint16_t*>(tail);
+  if (tpw == 4) {
+    hipLaunchKernelGGL((head_gemv_kernel<4, 4>), grid, dim3(kThreads), 0, stream, xv, wv, yv, tv,
+                       batch, num_heads, k, n, nt, ks, x_stride, y_stride, x_vec, tail_cols,
+                       tail_stride);
+  } else if (tpw == 2) {
+    hipLaunchKernelGGL((head_gemv_kernel<8, 2>), grid, dim3(kThreads), 0, stream, xv, wv, yv, tv,
+                       batch, num_heads, k, n, nt, ks, x_stride, y_stride, x_vec, tail_cols,
+                       tail_stride);
+  } else {
+    hipLaunchKernelGGL((head_gemv_kernel<16, 1>), grid, dim3(kThreads), 0, stream, xv, wv, yv, tv,
+                       batch, num_heads, k, n, nt, ks, x_stride, y_stride, x_vec, tail_cols,
+                       tail_stride);
+  }
+  return VOOM_LAUNCH_CHECK("mla_head_gemv: kernel launch");
 }
 
 }  // namespace
@@ -1310,49 +1520,44 @@ extern "C" size_t voom_mla_workspace_bytes(int batch, int num_heads, int num_ran
   return partial_bytes(static_cast<size_t>(batch) * num_ranges * num_heads, num_heads);
 }
 
-extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
-                                        const int32_t* block_table, const int32_t* ctx_lens,
-                                        void* out_c, float* lse_out, void* workspace,
-                                        size_t ws_bytes, int batch, int num_heads,
-                                        int latent_dim, int c_dim, int page_tokens, int max_pages,
-                                        int num_slots, float scale, int num_ranges,
-                                        hipStream_t stream) {
-  VOOM_REQUIRE(q_lat && lat_pool && block_table && ctx_lens && out_c && workspace,
-               "mla_absorbed_decode: null pointer argument");
-  VOOM_REQUIRE(latent_dim == kLat && c_dim == kC,
-               "mla_absorbed_decode: latent %d / c_dim %d unsupported (576 / 512)", latent_dim,
-               c_dim);
+namespace voom {
+namespace {
+// Checks of the dense latent decode's arguments; fills `a` and the grid.
+int prepare_dense(const char* who, const void* q_lat, const void* lat_pool,
+                  const int32_t* block_table, const int32_t* ctx_lens, void* workspace,
+                  size_t ws_bytes, int batch, int num_heads, int latent_dim, int c_dim,
+                  int page_tokens, int max_pages, int num_slots, float scale, int num_ranges,
+                  MlaArgs& a, long long& grid) {
+  VOOM_REQUIRE(q_lat && lat_pool && block_table && ctx_lens && workspace,
+               "%s: null pointer argument", who);
+  VOOM_REQUIRE(latent_dim == kLat && c_dim == kC, "%s: latent %d / c_dim %d unsupported (576 / 512)",
+               who, latent_dim, c_dim);
   VOOM_REQUIRE(batch > 0 && num_heads > 0 && num_heads % 32 == 0,
-               "mla_absorbed_decode: num_heads %d must be a positive multiple of 32", num_heads);
+               "%s: num_heads %d must be a positive multiple of 32", who, num_heads);
   VOOM_REQUIRE(is_pow2(page_tokens) && page_tokens >= kTile && page_tokens <= 4096,
-               "mla_absorbed_decode: page_tokens %d must be a power of two in [64, 4096]",
-               page_tokens);
-  VOOM_REQUIRE(max_pages > 0 && num_slots > 0, "mla_absorbed_decode: empty table or pool");
-  VOOM_REQUIRE(scale > 0.f && scale < INFINITY, "mla_absorbed_decode: scale %g must be positive",
+               "%s: page_tokens %d must be a power of two in [64, 4096]", who, page_tokens);
+  VOOM_REQUIRE(max_pages > 0 && num_slots > 0, "%s: empty table or pool", who);
+  VOOM_REQUIRE(scale > 0.f && scale < INFINITY, "%s: scale %g must be positive", who,
                static_cast<double>(scale));
   VOOM_REQUIRE(static_cast<long long>(max_pages) * page_tokens < (1LL << 30),
-               "mla_absorbed_decode: table capacity too large");
+               "%s: table capacity too large", who);
   if (num_ranges <= 0) num_ranges = default_ranges(batch, num_heads);
   const size_t need = voom_mla_workspace_bytes(batch, num_heads, num_ranges);
-  VOOM_REQUIRE(ws_bytes >= need, "mla_absorbed_decode: workspace %zu bytes < required %zu",
-               ws_bytes, need);
+  VOOM_REQUIRE(ws_bytes >= need, "%s: workspace %zu bytes < required %zu", who, ws_bytes, need);
   VOOM_REQUIRE(reinterpret_cast<uintptr_t>(q_lat) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(lat_pool) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
-               "mla_absorbed_decode: q, pool and workspace must be 16-byte aligned");
+               "%s: q, pool and workspace must be 16-byte aligned", who);
   const int hg = heads_per_group(num_heads);
-  const long long grid = static_cast<long long>(batch) * num_ranges * (num_heads / hg);
-  VOOM_REQUIRE(grid < (1LL << 31), "mla_absorbed_decode: grid too large");
-
-  const size_t n = static_cast<size_t>(batch) * num_ranges * num_heads;
-  MlaArgs a;
+  grid = static_cast<long long>(batch) * num_ranges * (num_heads / hg);
+  VOOM_REQUIRE(grid < (1LL << 31), "%s: grid too large", who);
   a.q = static_cast<const uint16_t*>(q_lat);
   a.lat = static_cast<const uint16_t*>(lat_pool);
   a.table = block_table;
   a.ctx_lens = ctx_lens;
   a.B = batch;
   a.H = num_heads;
-  set_partials(a, workspace, n);
+  set_partials(a, workspace, static_cast<size_t>(batch) * num_ranges * num_heads);
   a.NR = num_ranges;
   a.max_pages = max_pages;
   a.pt_shift = ilog2(page_tokens);
@@ -1361,7 +1566,51 @@ extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
   a.sel = nullptr;
   a.sel_stride = 0;
   a.pool_bytes = 0;
-  return launch_mla(a, hg, false, grid, static_cast<uint16_t*>(out_c), lse_out, stream);
+  return VOOM_OK;
+}
+}  // namespace
+}  // namespace voom
+
+extern "C" int voom_mla_absorbed_decode(const void* q_lat, const void* lat_pool,
+                                        const int32_t* block_table, const int32_t* ctx_lens,
+                                        void* out_c, float* lse_out, void* workspace,
+                                        size_t ws_bytes, int batch, int num_heads,
+                                        int latent_dim, int c_dim, int page_tokens, int max_pages,
+                                        int num_slots, float scale, int num_ranges,
+                                        hipStream_t stream) {
+  const char* who = "mla_absorbed_decode";
+  VOOM_REQUIRE(out_c != nullptr, "%s: null pointer argument", who);
+  MlaArgs a;
+  long long grid = 0;
+  const int rc = prepare_dense(who, q_lat, lat_pool, block_table, ctx_lens, workspace, ws_bytes,
+                               batch, num_heads, latent_dim, c_dim, page_tokens, max_pages,
+                               num_slots, scale, num_ranges, a, grid);
+  if (rc) return rc;
+  return launch_mla(a, heads_per_group(num_heads), false, grid, static_cast<uint16_t*>(out_c),
+                    lse_out, stream);
+}
+
+extern "C" int voom_mla_absorbed_decode_project(
+    const void* q_lat, const void* lat_pool, const int32_t* block_table, const int32_t* ctx_lens,
+    const void* w_uv_packed, int dv, void* y, void* wc_out, float* lse_out, void* workspace,
+    size_t ws_bytes, int batch, int num_heads, int latent_dim, int c_dim, int page_tokens,
+    int max_pages, int num_slots, float scale, int num_ranges, hipStream_t stream) {
+  const char* who = "mla_absorbed_decode_project";
+  VOOM_REQUIRE(w_uv_packed && y, "%s: null pointer argument", who);
+  VOOM_REQUIRE(num_heads % 64 == 0, "%s: num_heads %d must be a multiple of 64", who, num_heads);
+  VOOM_REQUIRE(batch <= 16, "%s: batch %d must be at most 16", who, batch);
+  VOOM_REQUIRE(dv >= 1 && dv <= kRpMaxTiles * kHgTile, "%s: dv %d must be 1..%d", who, dv,
+               kRpMaxTiles * kHgTile);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w_uv_packed) % 16 == 0,
+               "%s: w_uv_packed must be 16-byte aligned", who);
+  MlaArgs a;
+  long long grid = 0;
+  const int rc = prepare_dense(who, q_lat, lat_pool, block_table, ctx_lens, workspace, ws_bytes,
+                               batch, num_heads, latent_dim, c_dim, page_tokens, max_pages,
+                               num_slots, scale, num_ranges, a, grid);
+  if (rc) return rc;
+  return launch_mla_project(a, grid, w_uv_packed, dv, y, static_cast<uint16_t*>(wc_out), lse_out,
+                            stream);
 }
 
 extern "C" int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool,
@@ -1423,32 +1672,53 @@ extern "C" int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool,
   return launch_mla(a, hg, true, grid, static_cast<uint16_t*>(out_c), lse_out, stream);
 }
 
-extern "C" int voom_mla_head_gemv(const void* x, const void* w, void* y, int batch,
+extern "C" size_t voom_mla_head_weights_bytes(int num_heads, int k, int n) {
+  if (num_heads <= 0 || k <= 0 || n <= 0) return 0;
+  const size_t nt = (n + kHgTile - 1) / kHgTile;
+  const size_t ks = (k + kHgStep - 1) / kHgStep;
+  return static_cast<size_t>(num_heads) * nt * ks * 64 * 8 * 2;
+}
+
+extern "C" int voom_mla_pack_head_weights(const void* w, void* w_packed, int num_heads, int k,
+                                          int n, hipStream_t stream) {
+  const char* who = "mla_pack_head_weights";
+  VOOM_REQUIRE(w && w_packed, "%s: null pointer argument", who);
+  VOOM_REQUIRE(num_heads >= 1 && k >= 1 && n >= 1, "%s: empty weights", who);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w_packed) % 16 == 0, "%s: w_packed must be 16-byte aligned",
+               who);
+  const int nt = (n + kHgTile - 1) / kHgTile;
+  const int ks = (k + kHgStep - 1) / kHgStep;
+  const long long total = static_cast<long long>(num_heads) * nt * ks * 64;
+  VOOM_REQUIRE(total / kThreads < (1LL << 31), "%s: weights too large", who);
+  hipLaunchKernelGGL(pack_head_weights_kernel, dim3(static_cast<unsigned>((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, static_cast<const uint16_t*>(w),
+                     static_cast<uint16_t*>(w_packed), num_heads, k, n, nt, ks);
+  return VOOM_LAUNCH_CHECK("mla_pack_head_weights: kernel launch");
+}
+
+extern "C" int voom_mla_head_gemv(const void* x, const void* w_packed, void* y, int batch,
                                   int num_heads, int k, int n, int x_stride, int y_stride,
                                   hipStream_t stream) {
   const char* who = "mla_head_gemv";
-  VOOM_REQUIRE(x && w && y, "%s: null pointer argument", who);
+  VOOM_REQUIRE(x && w_packed && y, "%s: null pointer argument", who);
   VOOM_REQUIRE(batch >= 1 && batch <= 16 && num_heads >= 1, "%s: batch must be 1..16", who);
-  VOOM_REQUIRE(k >= 1 && k <= kHgMaxK, "%s: k %d must be 1..%d", who, k, kHgMaxK);
-  VOOM_REQUIRE(n % 8 == 0 && n >= 8 && n <= kHgMaxN && kWave % (n / 8) == 0,
-               "%s: n %d must be 8, 16, ..., 512 (n / 8 dividing 64)", who, n);
+  VOOM_REQUIRE(k >= 1 && n >= 1, "%s: k %d and n %d must be positive", who, k, n);
   VOOM_REQUIRE(x_stride >= k && y_stride >= n, "%s: row strides below k / n", who);
-  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w) % 16 == 0, "%s: w must be 16-byte aligned", who);
-  const auto* xv = static_cast<const uint16_t*>(x);
-  const auto* wv = static_cast<const uint16_t*>(w);
-  auto* yv = static_cast<uint16_t*>(y);
-  // split the columns until the grid covers the CUs (each part keeps n / 8
-  // dividing 64 and at least 8 lanes per weight row)
-  int ns = 1;
-  while (static_cast<long long>(num_heads) * ns < 256 && (n / ns) % 16 == 0 && n / ns >= 64) ns *= 2;
-  const int nw = n / ns;
-  const dim3 grid(static_cast<unsigned>(num_heads), static_cast<unsigned>(ns));
-  if (batch <= 8) {
-    hipLaunchKernelGGL(head_gemv_kernel<8>, grid, dim3(kThreads), 0, stream, xv, wv, yv, batch,
-                       num_heads, k, n, nw, x_stride, y_stride);
-  } else {
-    hipLaunchKernelGGL(head_gemv_kernel<16>, grid, dim3(kThreads), 0, stream, xv, wv, yv, batch,
-                       num_heads, k, n, nw, x_stride, y_stride);
-  }
-  return VOOM_LAUNCH_CHECK("mla_head_gemv: kernel launch");
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w_packed) % 16 == 0,
+               "%s: w_packed must be 16-byte aligned", who);
+  return launch_head_gemv(x, w_packed, y, nullptr, batch, num_heads, k, n, x_stride, y_stride, 0,
+                          0, stream);
+}
+
+extern "C" int voom_mla_absorb_query(const void* q_nope, const void* q_rope, const void* w_uk_packed,
+                                     void* q_lat, int batch, int num_heads, int dn, int c_dim,
+                                     int rope_dim, hipStream_t stream) {
+  const char* who = "mla_absorb_query";
+  VOOM_REQUIRE(q_nope && q_rope && w_uk_packed && q_lat, "%s: null pointer argument", who);
+  VOOM_REQUIRE(batch >= 1 && batch <= 16 && num_heads >= 1, "%s: batch must be 1..16", who);
+  VOOM_REQUIRE(dn >= 1 && c_dim >= 1 && rope_dim >= 0, "%s: empty dimensions", who);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(w_uk_packed) % 16 == 0,
+               "%s: w_uk_packed must be 16-byte aligned", who);
+  return launch_head_gemv(q_nope, w_uk_packed, q_lat, rope_dim > 0 ? q_rope : nullptr, batch,
+                          num_heads, dn, c_dim, dn, c_dim + rope_dim, rope_dim, rope_dim, stream);
 }

@@ -1616,12 +1616,13 @@ class PagedKVCache:
         return out.reshape(B, L, NQ, D).permute(0, 2, 1, 3)
 
     def attend_mla(self, layer: int, q_nope: torch.Tensor, q_rope: torch.Tensor,
-                   w_uk: torch.Tensor, w_uv_t: torch.Tensor, scale: float,
+                   w_uk, w_uv_t, scale: float,
                    return_weighted_c: bool = False, selection=None):
         """Absorbed-MLA decode over the layer's latent pages (runtime/glm.py:78-202).
 
         q_nope [B, H, dn], q_rope [B, H, 64] bf16 (one query token); W_UK
-        [H, dn, 512] and W_UV^T [H, 512, dv] as from ops.split_kv_b; ``scale``
+        [H, dn, 512] and W_UV^T [H, 512, dv] as from ops.split_kv_b (tensors,
+        or ops.HeadWeights packed once, which saves a packing pass per call); ``scale``
         is the reference's (dn + dr) ** -0.5.  q_lat = [q_nope . W_UK | q_rope]
         is contracted with the paged latent in the HIP kernel (resident pages
         first, spilled pages chunk by chunk as they land, LSE-merged), and

@@ -628,60 +628,153 @@ def split_kv_b(kv_b: torch.Tensor, num_heads: int, dn: int, dv: int):
     return w[:, :dn, :].contiguous(), w[:, dn:, :].transpose(1, 2).contiguous()
 
 
-def mla_absorb_query(q_nope: torch.Tensor, q_rope: torch.Tensor, w_uk: torch.Tensor):
+class HeadWeights:
+    """Per-head weights w [H, K, N] packed once for ``head_gemv``
+    (``voom_mla_pack_head_weights``): the operand order of its matrix
+    instructions, so that every weight load is a contiguous 1 KiB."""
+
+    __slots__ = ("packed", "heads", "k", "n")
+
+    def __init__(self, w: torch.Tensor, *, stream: torch.cuda.Stream | None = None):
+        dev = _require_device(w)
+        _require(w.dtype == torch.bfloat16 and w.dim() == 3, "w must be bf16 [H, K, N]")
+        w = w.contiguous()
+        self.heads, self.k, self.n = (int(v) for v in w.shape)
+        nbytes = int(_lib.lib().voom_mla_head_weights_bytes(self.heads, self.k, self.n))
+        self.packed = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev)
+        _lib.call("voom_mla_pack_head_weights", _ptr(w), _ptr(self.packed), self.heads, self.k,
+                  self.n, _stream(stream))
+
+    @property
+    def shape(self):
+        return (self.heads, self.k, self.n)
+
+
+def pack_head_weights(w, *, stream: torch.cuda.Stream | None = None) -> HeadWeights:
+    """``w`` as HeadWeights (packed once; a HeadWeights is returned as is)."""
+    return w if isinstance(w, HeadWeights) else HeadWeights(w, stream=stream)
+
+
+def mla_absorb_query(q_nope: torch.Tensor, q_rope: torch.Tensor, w_uk):
     """q_lat = [q_nope . W_UK | q_rope] [B, H, 576] (runtime/glm.py:129-132).
 
-    q_nope [B, H, dn], q_rope [B, H, 64] bf16, W_UK [H, dn, 512]; the
-    per-head product runs as one weight stream (``head_gemv``).
+    q_nope [B, H, dn], q_rope [B, H, 64] bf16, W_UK [H, dn, 512] (a tensor,
+    packed on each call, or HeadWeights packed once); the per-head product
+    runs as one weight stream (``head_gemv``).
     """
+    q_nope = q_nope.contiguous()
+    q_rope = q_rope.contiguous()
+    dev = _require_device(q_nope, q_rope)
+    _require(q_nope.dtype == q_rope.dtype == torch.bfloat16 and q_nope.dim() == q_rope.dim() == 3,
+             "bf16 q_nope [B, H, dn] and q_rope [B, H, dr]")
     B, H, dn = q_nope.shape
-    C = w_uk.shape[-1]
-    q_lat = torch.empty((B, H, C + q_rope.shape[-1]), dtype=q_nope.dtype, device=q_nope.device)
-    head_gemv(q_nope, w_uk, out=q_lat)      # writes q_lat[..., :C]
-    q_lat[..., C:].copy_(q_rope)
+    _require(tuple(q_rope.shape[:2]) == (B, H) and 1 <= B <= 16, "q_rope [B, H, dr], B <= 16")
+    w_uk = pack_head_weights(w_uk)
+    _require(w_uk.packed.device == dev and w_uk.heads == H and w_uk.k == dn,
+             "W_UK must be [H, dn, C] for q_nope [B, H, dn]")
+    C, dr = w_uk.n, q_rope.shape[-1]
+    q_lat = torch.empty((B, H, C + dr), dtype=q_nope.dtype, device=dev)
+    _lib.call("voom_mla_absorb_query", _ptr(q_nope), _ptr(q_rope), _ptr(w_uk.packed), _ptr(q_lat),
+              B, H, dn, C, dr, _stream(None))
     return q_lat
 
 
-def mla_project_out(wc: torch.Tensor, w_uv_t: torch.Tensor) -> torch.Tensor:
+def mla_project_out(wc: torch.Tensor, w_uv_t) -> torch.Tensor:
     """weighted_c [B, H, 512] . W_UV -> [B, H, dv] (runtime/glm.py:200-202)."""
     return head_gemv(wc, w_uv_t)
 
 
-def head_gemv(x: torch.Tensor, w: torch.Tensor, *, out: torch.Tensor | None = None,
+def head_gemv(x: torch.Tensor, w, *, out: torch.Tensor | None = None,
               stream: torch.cuda.Stream | None = None) -> torch.Tensor:
     """y [B, H, N] = x [B, H, K] . w [H, K, N] per head (fp32 sums, bf16 out)
     for decode-sized B (<= 16): the absorbed-MLA products as one weight
-    stream (``voom_mla_head_gemv``).  ``out`` may be wider than N in its last
-    dimension (only the first N columns are written)."""
+    stream on matrix instructions (``voom_mla_head_gemv``).  ``w`` is a
+    HeadWeights (pack_head_weights, once) or a bf16 tensor [H, K, N], packed
+    on the spot.  ``out`` may be wider than N in its last dimension (only the
+    first N columns are written)."""
     x = x.contiguous()
-    dev = _require_device(x, w)
-    _require(x.dtype == w.dtype == torch.bfloat16 and x.dim() == 3 and w.dim() == 3,
-             "bf16 x [B, H, K] and w [H, K, N]")
+    dev = _require_device(x)
+    _require(x.dtype == torch.bfloat16 and x.dim() == 3, "bf16 x [B, H, K]")
     B, H, K = x.shape
-    _require(w.shape[0] == H and w.shape[1] == K, "w must be [H, K, N] for x [B, H, K]")
-    N = w.shape[2]
+    _require(1 <= B <= 16, "head_gemv: batch must be 1..16")
+    if not isinstance(w, HeadWeights):
+        _require(isinstance(w, torch.Tensor) and w.dtype == torch.bfloat16 and w.dim() == 3,
+                 "w must be HeadWeights or bf16 [H, K, N]")
+        _require(w.shape[0] == H and w.shape[1] == K, "w must be [H, K, N] for x [B, H, K]")
+        w = HeadWeights(w, stream=stream)
+    _require(w.packed.device == dev, "w and x must be on the same device")
+    _require(w.heads == H and w.k == K, "w must be [H, K, N] for x [B, H, K]")
+    N = w.n
     if out is None:
         out = torch.empty((B, H, N), dtype=x.dtype, device=dev)
     _require(out.dtype == x.dtype and out.device == dev and out.dim() == 3 and
              tuple(out.shape[:2]) == (B, H) and out.shape[2] >= N and out.is_contiguous(),
              "out [B, H, >= N] contiguous bf16")
-    _lib.call("voom_mla_head_gemv", _ptr(x), _ptr(w), _ptr(out), B, H, K, N, K,
+    _lib.call("voom_mla_head_gemv", _ptr(x), _ptr(w.packed), _ptr(out), B, H, K, N, K,
               out.shape[2], _stream(stream))
     return out
 
 
+def mla_latent_decode_project(q_lat: torch.Tensor, lat_pool: torch.Tensor,
+                              block_table: torch.Tensor, ctx_lens: torch.Tensor, w_uv_t, *,
+                              scale: float, num_ranges: int = 0, return_weighted_c: bool = False,
+                              return_lse: bool = False, ws: torch.Tensor | None = None,
+                              stream: torch.cuda.Stream | None = None):
+    """Latent contraction and output projection: y [B, H, dv] = weighted_c .
+    W_UV (runtime/glm.py:133-164, 200-202) with the merge of the range
+    partials and the projection in one launch (``voom_mla_absorbed_decode_project``;
+    H a multiple of 64, B <= 16, dv <= 128).  ``w_uv_t`` is W_UV^T [H, 512,
+    dv] or its HeadWeights.  Returns y, then weighted_c [B, H, 512] and the
+    log-sum-exp [B, H] when asked for."""
+    dev = _require_device(q_lat, lat_pool, block_table, ctx_lens)
+    _require(q_lat.dim() == 3 and lat_pool.dim() == 3, "q_lat [B,H,576], lat_pool [slots,PT,576]")
+    B, H, LD = q_lat.shape
+    slots, PT, LD2 = lat_pool.shape
+    _require(LD == LD2 == 576, "latent width must be 576 (512 + 64)")
+    _require(q_lat.dtype == lat_pool.dtype == torch.bfloat16, "q_lat and lat_pool must be bf16")
+    _require(block_table.dtype == torch.int32 and ctx_lens.dtype == torch.int32,
+             "block_table and ctx_lens must be int32")
+    _require(block_table.dim() == 2 and block_table.shape[0] == B and tuple(ctx_lens.shape) == (B,),
+             "block_table [B, max_pages], ctx_lens [B]")
+    w_uv = pack_head_weights(w_uv_t, stream=stream)
+    _require(w_uv.packed.device == dev and w_uv.heads == H and w_uv.k == 512,
+             "W_UV^T must be [H, 512, dv]")
+    need = mla_workspace_bytes(B, H, num_ranges)
+    if ws is None:
+        ws = workspace(dev, need, tag=2)
+    _require(ws.numel() * ws.element_size() >= need, "workspace too small")
+    y = torch.empty((B, H, w_uv.n), dtype=torch.bfloat16, device=dev)
+    wc = torch.empty((B, H, 512), dtype=torch.bfloat16, device=dev) if return_weighted_c else None
+    lse = torch.empty((B, H), dtype=torch.float32, device=dev) if return_lse else None
+    _lib.call("voom_mla_absorbed_decode_project", _ptr(q_lat), _ptr(lat_pool), _ptr(block_table),
+              _ptr(ctx_lens), _ptr(w_uv.packed), w_uv.n, _ptr(y), _ptr(wc), _ptr(lse), _ptr(ws),
+              need, B, H, LD, 512, PT, block_table.shape[1], slots, float(scale), int(num_ranges),
+              _stream(stream))
+    res = (y,) + ((wc,) if return_weighted_c else ()) + ((lse,) if return_lse else ())
+    return res if len(res) > 1 else y
+
+
 def mla_absorbed_decode(q_nope: torch.Tensor, q_rope: torch.Tensor, lat_pool: torch.Tensor,
-                        block_table: torch.Tensor, ctx_lens: torch.Tensor, w_uk: torch.Tensor,
-                        w_uv_t: torch.Tensor, *, scale: float, num_ranges: int = 0,
-                        return_weighted_c: bool = False):
+                        block_table: torch.Tensor, ctx_lens: torch.Tensor, w_uk, w_uv_t, *,
+                        scale: float, num_ranges: int = 0, return_weighted_c: bool = False):
     """Absorbed MLA decode of one query token: runtime/glm.py:78-202.
 
     q_nope [B, H, dn], q_rope [B, H, 64] bf16; W_UK [H, dn, 512] and W_UV^T
-    [H, 512, dv] from split_kv_b.  q_nope . W_UK and weighted_c . W_UV run
-    in the per-head weight-stream kernel (``head_gemv``); the latent
-    contraction runs in the HIP latent kernel.  Returns the per-head output [B, H, dv] bf16 (before o_proj).
+    [H, 512, dv] from split_kv_b (tensors, or HeadWeights packed once).
+    q_lat = [q_nope . W_UK | q_rope] comes from one launch
+    (``voom_mla_absorb_query``); the latent contraction runs in the HIP latent
+    kernel, and with 64-head groups (H a multiple of 64, B <= 16, dv <= 128)
+    the merge of its partials and weighted_c . W_UV share one launch.
+    Returns the per-head output [B, H, dv] bf16 (before o_proj).
     """
     q_lat = mla_absorb_query(q_nope, q_rope, w_uk)
+    B, H = q_lat.shape[:2]
+    dv = w_uv_t.shape[-1]
+    if H % 64 == 0 and B <= 16 and dv <= 128:
+        res = mla_latent_decode_project(q_lat, lat_pool, block_table, ctx_lens, w_uv_t,
+                                        scale=scale, num_ranges=num_ranges,
+                                        return_weighted_c=return_weighted_c)
+        return res
     wc = mla_latent_decode(q_lat, lat_pool, block_table, ctx_lens, scale=scale,
                            num_ranges=num_ranges)
     out = mla_project_out(wc, w_uv_t)
