@@ -41,7 +41,7 @@ extern "C" {
 const char* voom_last_error(void);
 
 /* ABI version, bumped on any signature or layout change (2: checksums in the
- * slot codec). */
+ * slot codec; 3: spill-record calls). */
 int voom_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -429,6 +429,48 @@ int voom_byteplane_merge_slots(const void* lo, const void* hi, void* pool,
  * status words are sticky until the caller clears them. */
 int voom_page_sums_verify(const uint32_t* expected, const uint32_t* got, int n, int tag,
                           int32_t* status, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Spill records: pool slots <-> one record in pinned host memory, moved by
+ * the codec kernel itself (no staging buffer, no copy engine).
+ *
+ * Replaces the page move of the reference's spill (runtime/kv_paged.py:77-96,
+ * planes as formats/packed.py:49-50) and reload (runtime/kv_paged.py:98-113).
+ *
+ * A record of R slots over T pool tensors (T <= 4; tensor t's slots are
+ * slot_bytes[t] bytes, a multiple of 64, h_t = slot_bytes[t] / 2) is laid out
+ * as the low planes of every tensor (tensor t: R * h_t bytes, record slot r at
+ * r * h_t), then the high planes in the same arrangement, then, with
+ * checksums, int32 [T][R] (the checksum of voom_byteplane_split_slots).
+ * Listed slot i (pool slot slots[i] of every tensor) is record slot first + i;
+ * first + n_slots <= rec_slots.  `slots` is an int32 array of n_slots
+ * entries in device or pinned host memory (read by the kernel, so a host list
+ * needs no upload; it must stay unchanged until the call has run); entries
+ * outside [0, num_slots[t]) are skipped.
+ *
+ * `record` is pinned host memory (hipHostMalloc) or device memory; the call
+ * looks the record and the slot list up and refuses pageable or too-short
+ * memory.  Host
+ * records are written and read with system-scope accesses, so the host sees
+ * a spilled record once the stream has passed the call, and a reload reads
+ * what the host last wrote.  Both calls run on `stream`, which must be
+ * ordered after the writes of the slots they read.
+ * ------------------------------------------------------------------------- */
+/* Sets the record kernels up on the current device, so that the first spill
+ * does not pay their one-time launch setup (optional; idempotent). */
+int voom_record_prepare(void);
+/* Splits listed slots into the record; with_sums stores their checksums. */
+int voom_spill_record(const void* const* pools, const size_t* slot_bytes, const int* num_slots,
+                      int n_tensors, const int32_t* slots, int n_slots, void* record,
+                      int rec_slots, int first, int with_sums, hipStream_t stream);
+/* Merges record slots back into listed pool slots.  tag != 0: the checksum
+ * of every merged slot is compared with the record's; each mismatch adds 1
+ * to status[0] and the first stores tag in status[1] if it is still 0
+ * (device int32[2], as voom_page_sums_verify). */
+int voom_reload_record(const void* record, int rec_slots, int first, void* const* pools,
+                       const size_t* slot_bytes, const int* num_slots, int n_tensors,
+                       const int32_t* slots, int n_slots, int tag, int32_t* status,
+                       hipStream_t stream);
 
 #ifdef __cplusplus
 }

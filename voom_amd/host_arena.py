@@ -30,8 +30,15 @@ class HostBlock:
     view: torch.Tensor  # uint8 pinned view of exactly nbytes
 
 
+# Slab size: 256 MiB of page planes plus 1 MiB for what rides along with them
+# (checksum words, 256-byte record alignment), so that blocks of a power-of-two
+# plane size (64 MiB = one config-3 layer's spilled half) pack four to a slab
+# instead of three.
+SLAB_BYTES = (256 + 1) << 20
+
+
 class HostArena:
-    def __init__(self, slab_bytes: int = 256 << 20, pin: bool | None = None):
+    def __init__(self, slab_bytes: int = SLAB_BYTES, pin: bool | None = None):
         self.slab_bytes = int(slab_bytes)
         # Page-locked whenever a device exists (asynchronous copies need it);
         # plain host memory otherwise, which keeps the allocator testable.

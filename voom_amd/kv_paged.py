@@ -94,12 +94,15 @@ class _SpillBlock:
     ``m * parts[t]`` long, page i of the record at ``i * parts[t]`` inside its
     part, then (when ``nsum`` > 0) the pages' checksums as int32 [T, m * B],
     page i's B slots at ``i * B`` of each tensor's row.  A record therefore
-    moves in one copy each way, exactly as it sits in a staging buffer.
-    ``ready`` is recorded after the last D2H copy.
+    moves in one copy each way, exactly as it sits in a staging buffer, and
+    is the unit of voom_spill_record / voom_reload_record.  Records start
+    ``rec_stride`` bytes apart (a multiple of 256).  ``ready`` is recorded
+    after the block's last record is written, ``last_use`` after the last
+    kernel that reads the block.
     """
 
     __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "rec_ready", "live", "pages",
-                 "nsum", "jobs")
+                 "nsum", "jobs", "last_use")
 
     def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int,
                  nsum: int = 0):
@@ -109,8 +112,9 @@ class _SpillBlock:
         self.parts = list(parts)
         self.chunk = chunk
         self.nsum = nsum  # checksum words per page (T * B), 0 = none
-        self.ready: torch.cuda.Event | None = None  # after the block's last D2H copy
-        self.rec_ready: dict[int, torch.cuda.Event] = {}  # after each record's copy
+        self.ready: torch.cuda.Event | None = None  # after the block's last record landed
+        self.rec_ready: dict[int, torch.cuda.Event] = {}  # after each record landed
+        self.last_use: torch.cuda.Event | None = None  # after the last direct reload from it
         self.live = n_pages
         # host work queued on the spill (compression, page files), per page group
         self.jobs: list[Future] = []
@@ -128,15 +132,19 @@ class _SpillBlock:
     def record_pages(self, r: int) -> int:
         return min(self.chunk, self.n_pages - r * self.chunk)
 
+    @property
+    def rec_stride(self) -> int:
+        return record_stride(self.chunk, self.page_bytes)
+
     def record(self, r: int) -> torch.Tensor:
-        off = r * self.chunk * self.page_bytes
+        off = r * self.rec_stride
         return self.block.view[off:off + self.record_pages(r) * self.page_bytes]
 
     def part(self, which: int, j: int) -> torch.Tensor:
         """Plane ``which`` (low planes 0..T-1, then high planes) of page j."""
         r, i = divmod(j, self.chunk)
         m = self.record_pages(r)
-        off = r * self.chunk * self.page_bytes + part_offset(self.parts, m, which) + \
+        off = r * self.rec_stride + part_offset(self.parts, m, which) + \
             i * self.parts[which % len(self.parts)]
         return self.block.view[off:off + self.parts[which % len(self.parts)]]
 
@@ -154,6 +162,21 @@ def record_page_bytes(parts: list[int], nsum: int) -> int:
     """Bytes one page takes in a record: both planes of every tensor plus its
     ``nsum`` int32 checksums."""
     return 2 * sum(parts) + 4 * nsum
+
+
+def record_stride(chunk: int, page_bytes: int) -> int:
+    """Distance between the starts of consecutive records of a spill block:
+    one full record rounded up to 256 bytes, so every record is aligned for
+    the record kernels' 16-byte accesses."""
+    return -(-chunk * page_bytes // 256) * 256
+
+
+def block_bytes(n_pages: int, chunk: int, page_bytes: int) -> int:
+    """Host bytes of a spill block of ``n_pages`` pages in records of ``chunk``."""
+    full, last = divmod(n_pages, chunk)
+    if last == 0:
+        full, last = full - 1, chunk
+    return full * record_stride(chunk, page_bytes) + last * page_bytes
 
 
 def sums_view(buf: torch.Tensor, parts: list[int], m: int, nsum: int) -> torch.Tensor:
@@ -287,11 +310,14 @@ class _StagingRing:
 
 
 class _PinnedUploads:
-    """Small host-to-device index uploads through one persistent pinned buffer.
+    """Small host-to-device index lists through one persistent pinned buffer.
 
-    Allocating pinned memory per upload (``pin_memory()``) can stall the host
+    Allocating pinned memory per list (``pin_memory()``) can stall the host
     for milliseconds; the buffer here is carved round-robin instead, and a
-    region is rewritten only after the copy that last read it has completed.
+    region is rewritten only after the work that last read it has completed.
+    ``upload`` copies a list to the device; ``stage`` leaves it in the pinned
+    buffer for a kernel that reads host memory itself, and ``settle`` names
+    the event after which the staged regions may be reused.
     """
 
     def __init__(self, device: torch.device, pin: bool, words: int = 1 << 20):
@@ -300,31 +326,62 @@ class _PinnedUploads:
         self.buf = torch.empty(words, dtype=torch.int32, pin_memory=pin)
         self.np = self.buf.numpy()
         self.pos = 0
-        # regions whose copies may still be reading the buffer, oldest first;
-        # regions are handed out in address order, so the ones a new region
-        # overlaps are always at the front
+        # regions whose readers may still be running, oldest first: [lo, hi,
+        # event or None while staged and not yet settled]; regions are handed
+        # out in address order, so the ones a new region overlaps are always
+        # at the front
         self.inflight: deque = deque()
+        self._own: list = []  # (event or None, dedicated buffer) of oversized lists
+
+    def _region(self, arr: np.ndarray) -> tuple[int, int]:
+        n = arr.size
+        if self.pos + n > self.buf.numel():
+            self.pos = 0
+        lo, hi = self.pos, self.pos + n
+        q = self.inflight
+        while q and (q[0][0] < hi and q[0][1] > lo or (q[0][2] is not None and q[0][2].query())):
+            if q[0][2] is None:
+                raise RuntimeError("pinned list ring: a staged region was never settled")
+            q[0][2].synchronize()
+            q.popleft()
+        self.np[lo:hi] = arr.reshape(-1)
+        self.pos = hi
+        return lo, hi
 
     def upload(self, arr: np.ndarray) -> torch.Tensor:
         n = arr.size
         if n > self.buf.numel() // 2:  # rare: a dedicated buffer
             host = torch.from_numpy(arr)
             return (host.pin_memory() if self.pin else host).to(self.device, non_blocking=True)
-        if self.pos + n > self.buf.numel():
-            self.pos = 0
-        lo, hi = self.pos, self.pos + n
-        q = self.inflight
-        while q and (q[0][0] < hi and q[0][1] > lo or q[0][2].query()):
-            q[0][2].synchronize()
-            q.popleft()
-        self.np[lo:hi] = arr.reshape(-1)
+        lo, hi = self._region(arr)
         dev = torch.empty(arr.shape, dtype=torch.int32, device=self.device)
         dev.view(-1).copy_(self.buf[lo:hi], non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
-        self.inflight.append((lo, hi, ev))
-        self.pos = hi
+        self.inflight.append([lo, hi, ev])
         return dev
+
+    def stage(self, arr: np.ndarray) -> torch.Tensor:
+        """The int32 list in pinned host memory, for a kernel to read; the
+        region stays reserved until the event given to the next ``settle``."""
+        if arr.size > self.buf.numel() // 2:
+            own = torch.from_numpy(np.ascontiguousarray(arr, dtype=np.int32).reshape(-1))
+            own = own.pin_memory() if self.pin else own
+            self._own.append([None, own])
+            return own
+        lo, hi = self._region(arr)
+        self.inflight.append([lo, hi, None])
+        return self.buf[lo:hi]
+
+    def settle(self, ev: torch.cuda.Event) -> None:
+        """Every staged region is free once ``ev`` has passed."""
+        for region in self.inflight:
+            if region[2] is None:
+                region[2] = ev
+        for entry in self._own:
+            if entry[0] is None:
+                entry[0] = ev
+        self._own = [e for e in self._own if not e[0].query()]
 
 
 def budget_victims_fast(resident: np.ndarray, lengths, resident_pages: int, page_nbytes: int,
@@ -427,6 +484,11 @@ class PagedKVCache:
         self._status_host: torch.Tensor | None = None
         self._status_ev: torch.cuda.Event | None = None
         self._sum_scratch: torch.Tensor | None = None
+        # spill records move between pool slots and the pinned arena through
+        # the record kernels (the split writes host memory, the merge reads
+        # it); False takes the staging ring and copy-engine path instead
+        self.direct_host = True
+        self._pending_frees: list = []  # (event, host block) freed once the event passed
         self._tags: OrderedDict = OrderedDict()  # tag -> (layer, page indices)
         self._next_tag = 1
         self._reset_state()
@@ -480,6 +542,8 @@ class PagedKVCache:
             if dtype != torch.bfloat16:
                 raise ValueError("PagedKVCache stores bfloat16 pages")
             self._geom = geom
+            if self.direct_host and self.arena.pin:
+                ops.record_prepare()  # the first spill then pays no kernel setup
         elif self._geom != geom:
             raise ValueError(f"cache geometry changed: {self._geom} -> {geom}")
 
@@ -549,6 +613,14 @@ class PagedKVCache:
             if len(self._i32_cache) > 256:
                 self._i32_cache.popitem(last=False)
         return dev
+
+    def _host_i32(self, values) -> torch.Tensor:
+        """Int32 list staged in pinned host memory for a kernel that reads it
+        there (no upload); call ``_uploads.settle`` with an event recorded
+        after that kernel."""
+        if self._uploads is None:
+            self._uploads = _PinnedUploads(self.device, self.arena.pin)
+        return self._uploads.stage(np.ascontiguousarray(values, dtype=np.int32))
 
     def _token_nbytes(self) -> int:
         """Bytes one token adds to a layer across the batch (K+V, or one latent row)."""
@@ -891,6 +963,12 @@ class PagedKVCache:
     def release(self) -> None:
         """Free device slots and host copies; offset and nbytes return to 0."""
         self._wait_host_work()
+        # no kernel may still touch the host copies once they are given back
+        for sb in self._spill_blocks:
+            for ev in (sb.ready, sb.last_use):
+                if ev is not None:
+                    ev.synchronize()
+        self._reap_frees(wait=True)
         if self._own_arena:
             self.arena.close()
         else:
@@ -921,11 +999,12 @@ class PagedKVCache:
                                           self.resident_pages, self.page_nbytes, current,
                                           self.max_bytes)
         if layers.size:
-            groups = {}
-            for layer in np.unique(layers).tolist():
-                pages = self._pages[layer]
-                groups[layer] = [pages[i] for i in idx[layers == layer].tolist()]
-            self._spill_groups(groups)
+            def groups():  # layer by layer, so the first layer spills while the rest are listed
+                for layer in np.unique(layers).tolist():
+                    pages = self._pages[layer]
+                    yield layer, [pages[i] for i in idx[layers == layer].tolist()]
+
+            self._spill_groups(groups())
 
     def spill(self, pages=None) -> int:
         """Spill pages (``_Page`` objects or (layer, index) pairs) to the host arena.
@@ -942,20 +1021,26 @@ class PagedKVCache:
                 p = self._pages[p[0]][p[1]]
             if p.resident:
                 groups.setdefault(p.layer, []).append(p)
-        return self._spill_groups(groups)
+        return self._spill_groups(groups.items())
 
-    def _spill_groups(self, by_layer: dict) -> int:
-        """Spill resident pages grouped by layer.  Each layer's chunks are
-        enqueued as soon as the layer is planned, so the first copy starts
-        while later layers are still being planned."""
+    def _spill_groups(self, by_layer) -> int:
+        """Spill resident pages given as (layer, pages) pairs.  Each layer's
+        records are enqueued as soon as the layer is planned, so the first
+        transfer starts while later layers are still being listed and planned."""
         t0 = time.perf_counter()
-        pages = [p for lp in by_layer.values() for p in lp]
         issue = self._spill_issuer()
-        for layer, lp in by_layer.items():
+        done = []
+        for layer, lp in by_layer:
+            direct = self._direct_ok(self._pool(layer))
             for item in self._spill_plan(layer, lp):
-                issue(item)
+                if direct:
+                    self._spill_record(item)
+                else:
+                    issue(item)
+            done.append((layer, lp))
         issue(None)
-        for layer, lp in by_layer.items():
+        pages = [p for _, lp in done for p in lp]
+        for layer, lp in done:
             pool = self._pool(layer)
             pool.release([s for p in lp for s in p.slots])
             for p in lp:
@@ -992,7 +1077,9 @@ class PagedKVCache:
         page_bytes = record_page_bytes(parts, nsum)
         n = len(pages)
         per_chunk = max(1, self._ring.nbytes // page_bytes)
-        sb = _SpillBlock(self.arena.alloc(n * page_bytes), n, parts, per_chunk, nsum)
+        self._reap_frees(wait=True)
+        sb = _SpillBlock(self.arena.alloc(block_bytes(n, per_chunk, page_bytes)), n, parts,
+                         per_chunk, nsum)
         sb.pages = list(pages)
         self._spill_blocks.append(sb)
         for j, p in enumerate(pages):
@@ -1000,6 +1087,26 @@ class PagedKVCache:
             p.host_j = j
         return [(pool, pages[c0:c0 + per_chunk], sb, c0 // per_chunk)
                 for c0 in range(0, n, per_chunk)]
+
+    def _direct_ok(self, pool: DevicePagePool) -> bool:
+        """Whether spill records move between this pool and the arena through
+        the record kernels (pinned arena, slots of whole 64-byte lines)."""
+        return (self.direct_host and self.arena.pin and len(pool.tensors) <= 4
+                and all(ops.slot_codec_supported(t) for t in pool.tensors))
+
+    def _spill_record(self, item) -> None:
+        """Spill one record with voom_spill_record: the split kernel reads the
+        slot list from pinned memory and writes the planes and checksums
+        straight into the pinned record, on the current stream (which holds
+        the pages' writes), with no staging buffer and no copy."""
+        pool, cp, sb, rec = item
+        slots = self._host_i32([s for p in cp for s in p.slots])
+        ops.spill_record(pool.tensors, slots, sb.record(rec), sums=sb.nsum > 0)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._uploads.settle(ev)
+        sb.rec_ready[rec] = ev
+        sb.ready = ev
 
     def _spill_issuer(self):
         """A function taking spill work items (pool, pages, block, record) one
@@ -1159,11 +1266,30 @@ class PagedKVCache:
             self._release_block(sb)
 
     def _release_block(self, sb: _SpillBlock) -> None:
+        """Give a spill block's host memory back.  Kernels still reading it
+        (a direct reload just enqueued) keep it until they are done: it is
+        freed once ``last_use`` has passed (at the next spill or release)."""
         sb.wait_jobs()
         if sb.ready is not None:
             sb.ready.synchronize()
-        self.arena.free(sb.block)
         self._spill_blocks.remove(sb)
+        if sb.last_use is not None and not sb.last_use.query():
+            self._pending_frees.append((sb.last_use, sb.block))
+        else:
+            self.arena.free(sb.block)
+
+    def _reap_frees(self, wait: bool = False) -> None:
+        """Free the host blocks whose last reader has finished (all of them,
+        waiting, with ``wait``)."""
+        keep = []
+        for ev, block in self._pending_frees:
+            if wait:
+                ev.synchronize()
+            if wait or ev.query():
+                self.arena.free(block)
+            else:
+                keep.append((ev, block))
+        self._pending_frees = keep
 
     def _file_data(self, p: _Page):
         """Planes (low planes, then high planes) and checksums ([T, B] int32 or
@@ -1439,6 +1565,14 @@ class PagedKVCache:
         # chunks are produced job by job and issued a window at a time, so the
         # first copy starts before later jobs are even looked at
         for layer, pages, target, consume, transient in jobs:
+            if not transient and self._direct_ok(target):
+                held = [p for p in pages if p.host is not None]
+                if held:
+                    verified |= self._reload_records(layer, held, target, consume)
+                    n_pages += len(held)
+                    pages = [p for p in pages if p.host is None]
+                    if not pages:
+                        continue
             parts = self._plane_parts(target)
             nsum = self._nsum(target)
             verified |= nsum > 0
@@ -1462,13 +1596,62 @@ class PagedKVCache:
         self._stats.reloads += n_pages
         self._stats.reload_s += time.perf_counter() - t0
 
+    def _reload_records(self, layer: int, pages: list[_Page], target: DevicePagePool,
+                        consume) -> bool:
+        """Merge pages held in the arena back into fresh ``target`` slots with
+        voom_reload_record, one launch per run of consecutive pages of one
+        record, on the current stream: the kernel reads the pinned record
+        itself and checks each slot's checksum.  Returns whether checksums
+        were compared."""
+        B = self._batch
+        nsum = self._nsum(target)
+        runs: list = []  # [block, record, pages]
+        for p in pages:
+            sb, j = p.host, p.host_j
+            if nsum and not sb.nsum:
+                raise KVIntegrityError(f"layer {p.layer} page {p.index}: no checksums were "
+                                       "stored with the spilled page")
+            r = j // sb.chunk
+            last = runs[-1] if runs else None
+            if last is not None and last[0] is sb and last[1] == r and \
+                    last[2][-1].host_j + 1 == j:
+                last[2].append(p)
+            else:
+                runs.append([sb, r, [p]])
+        main = torch.cuda.current_stream()
+        blocks = {id(sb): sb for sb, _, _ in runs}
+        for sb in blocks.values():
+            if sb.ready is not None:
+                main.wait_event(sb.ready)
+        if nsum and self._status is None:
+            self._status = torch.zeros(2, dtype=torch.int32, device=self.device)
+        slots = target.allocate(B * len(pages))
+        k = 0
+        for sb, r, run in runs:
+            mine = slots[k:k + B * len(run)]
+            k += len(mine)
+            tag = self._tag(layer, run) if nsum else 0
+            ops.reload_record(sb.record(r), target.tensors, self._host_i32(mine),
+                              rec_slots=sb.record_pages(r) * B,
+                              first=(run[0].host_j - r * sb.chunk) * B, tag=tag,
+                              status=self._status if tag else None)
+            consume(run, mine)
+        done = torch.cuda.Event()
+        done.record(main)
+        self._uploads.settle(done)
+        for sb in blocks.values():
+            sb.last_use = done
+        return nsum > 0
+
     def reload(self, pages=None, stream: torch.cuda.Stream | None = None) -> int:
         """Make spilled pages resident again in fresh pool slots; returns the count.
 
-        Uploads run on the cache's side stream (or ``stream``), merges on the
-        current stream.  The host waits at the end for the pages' checksums
-        (KVIntegrityError when a page came back changed); compressed pages are
-        also decompressed on the host first.
+        Pages held in the pinned arena are merged by the record kernel, which
+        reads host memory itself, on the current stream.  Pages that live only
+        in page files are read (and decompressed) on the host, uploaded on the
+        cache's side stream (or ``stream``) and merged on the current stream.
+        The host waits at the end for the pages' checksums (KVIntegrityError
+        when a page came back changed).
         """
         self.check_integrity(wait=False)
         if pages is None:

@@ -13,6 +13,8 @@ Pool layouts (per layer):
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -328,6 +330,80 @@ def page_sums_verify(expected: torch.Tensor, got: torch.Tensor, tag: int,
     _require(tag != 0, "tag must be non-zero")
     _lib.call("voom_page_sums_verify", _ptr(expected), _ptr(got), expected.numel(), int(tag),
               _ptr(status), _stream(stream))
+
+
+def record_bytes(pools: list[torch.Tensor], rec_slots: int, sums: bool) -> int:
+    """Bytes of a spill record of ``rec_slots`` slots of every tensor in
+    ``pools``: both byte planes of each slot, plus int32 [T, rec_slots]
+    checksums with ``sums``."""
+    slot = sum(p[0].numel() * 2 for p in pools)
+    return rec_slots * slot + (4 * len(pools) * rec_slots if sums else 0)
+
+
+def _record_call_args(pools: list[torch.Tensor], slots: torch.Tensor, record: torch.Tensor,
+                      rec_slots: int, first: int, sums: bool):
+    _require(1 <= len(pools) <= 4, "a record holds 1 to 4 pool tensors")
+    for p in pools:
+        _u16_view(p)
+        _require(slot_codec_supported(p), "pool slots must be whole 64-byte lines")
+    _require_device(*pools)
+    _require(slots.dtype == torch.int32 and slots.dim() == 1 and slots.is_contiguous(),
+             "slots must be 1-D contiguous int32")
+    _require(slots.device == pools[0].device or (slots.device.type == "cpu" and slots.is_pinned()),
+             "slots must be on the pools' device or in pinned host memory")
+    _require(record.dtype == torch.uint8 and record.dim() == 1 and record.is_contiguous(),
+             "record must be a contiguous 1-D uint8 tensor")
+    _require(record.is_cuda or record.is_pinned(),
+             "record must be pinned host memory or device memory")
+    _require(0 <= first and first + slots.numel() <= rec_slots,
+             "listed slots run past the record")
+    _require(record.numel() >= record_bytes(pools, rec_slots, sums), "record too small")
+    n = len(pools)
+    ptrs = (ctypes.c_void_p * n)(*[p.data_ptr() for p in pools])
+    sbytes = (ctypes.c_size_t * n)(*[p[0].numel() * 2 for p in pools])
+    counts = (ctypes.c_int * n)(*[p.shape[0] for p in pools])
+    return ptrs, sbytes, counts
+
+
+def record_prepare() -> None:
+    """Set the spill-record kernels up on the current device ahead of the first
+    spill (their one-time launch setup costs about a millisecond each)."""
+    _lib.call("voom_record_prepare")
+
+
+def spill_record(pools: list[torch.Tensor], slots: torch.Tensor, record: torch.Tensor, *,
+                 rec_slots: int | None = None, first: int = 0, sums: bool = False,
+                 stream: torch.cuda.Stream | None = None) -> None:
+    """Byte-plane split of pool slots ``slots`` (of every tensor in ``pools``)
+    straight into ``record`` (pinned host memory, or device memory), as record
+    slots first .. first + len(slots) - 1, with their checksums when ``sums``.
+    ``slots`` may be pinned host memory, read by the kernel itself (keep it
+    unchanged until the call has run).  The record layout is the one
+    voom_spill_record documents."""
+    rec_slots = slots.numel() if rec_slots is None else int(rec_slots)
+    ptrs, sbytes, counts = _record_call_args(pools, slots, record, rec_slots, first, sums)
+    _lib.call("voom_spill_record", ctypes.cast(ptrs, ctypes.c_void_p), ctypes.addressof(sbytes),
+              ctypes.addressof(counts), len(pools), _ptr(slots), slots.numel(), _ptr(record),
+              rec_slots, int(first), int(bool(sums)), _stream(stream))
+
+
+def reload_record(record: torch.Tensor, pools: list[torch.Tensor], slots: torch.Tensor, *,
+                  rec_slots: int | None = None, first: int = 0, tag: int = 0,
+                  status: torch.Tensor | None = None,
+                  stream: torch.cuda.Stream | None = None) -> None:
+    """Byte-plane merge of record slots first .. first + len(slots) - 1 back
+    into pool slots ``slots``.  ``tag`` != 0 compares every merged slot with the
+    record's checksum and counts mismatches into ``status`` (device int32 [2],
+    as page_sums_verify)."""
+    rec_slots = slots.numel() if rec_slots is None else int(rec_slots)
+    ptrs, sbytes, counts = _record_call_args(pools, slots, record, rec_slots, first, bool(tag))
+    if tag:
+        _require(status is not None and status.is_cuda and status.dtype == torch.int32
+                 and status.numel() >= 2, "a tag needs a device int32 status of 2 words")
+    _lib.call("voom_reload_record", _ptr(record), rec_slots, int(first),
+              ctypes.cast(ptrs, ctypes.c_void_p), ctypes.addressof(sbytes),
+              ctypes.addressof(counts), len(pools), _ptr(slots), slots.numel(), int(tag),
+              _ptr(status) if tag else None, _stream(stream))
 
 
 def slot_codec_supported(pool: torch.Tensor) -> bool:
