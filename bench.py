@@ -36,13 +36,16 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def graph_seconds(calls, reps: int) -> float:
+def graph_seconds(calls, reps: int, rounds: int = 3) -> float:
     """Seconds per call of the launches in `calls` (a list of no-argument
     functions), captured once into a HIP graph and replayed `reps` times
-    between two events.  Replaying keeps the GPU busy back to back, so the
-    events measure the device, not the rate at which Python issues launches
-    (which, for calls of a few tens of microseconds, is the slower of the two).
-    Every call must already have run eagerly once, so its workspaces exist."""
+    between two events, in `rounds` separate rounds; the median round is
+    returned (short, MFMA-heavy calls vary by a few percent with the clock the
+    GPU runs at in a given moment).  Replaying keeps the GPU busy back to
+    back, so the events measure the device, not the rate at which Python
+    issues launches (which, for calls of a few tens of microseconds, is the
+    slower of the two).  Every call must already have run eagerly once, so its
+    workspaces exist."""
     import torch
 
     side = torch.cuda.Stream()
@@ -55,13 +58,16 @@ def graph_seconds(calls, reps: int) -> float:
     torch.cuda.current_stream().wait_stream(side)
     graph.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / (reps * len(calls))
+    times = []
+    for _ in range(rounds):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3 / (reps * len(calls)))
+    return sorted(times)[len(times) // 2]
 
 
 def profiled_traffic(name: str) -> int | None:
