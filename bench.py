@@ -721,6 +721,18 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
         full(i)
     torch.cuda.synchronize()
     t_full = graph_seconds([lambda i=i: full(i) for i in range(8)], max(1, steps // 8))
+
+    # the floor of one launch that streams one weight set's 16.8 MB: a plain
+    # read kernel over 8 rotating buffers of that size
+    w_bytes = 128 * 128 * 512 * 2  # H x dn x c of W_UK (= H x c x dv of W_UV)
+    floor_bufs = [torch.empty(w_bytes, dtype=torch.uint8, device="cuda") for _ in range(8)]
+    sink = torch.zeros(512, dtype=torch.int32, device="cuda")
+    for i in range(8):
+        ops.stream_read(floor_bufs[i], sink)
+    torch.cuda.synchronize()
+    t_floor = graph_seconds([lambda i=i: ops.stream_read(floor_bufs[i], sink) for i in range(8)],
+                            max(1, steps // 8))
+    del floor_bufs
     res = {
         "workload": "config 5: absorbed MLA decode, B=8, H=128, ctx 16384, latent 512+64 bf16 "
                     "in 64-token pages, 4 rotating input sets",
@@ -734,6 +746,10 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
         "absorption_gemms_us": t_gemm * 1e6,
         "absorption_gemms_note": "q_nope . W_UK with q_rope (one launch) + weighted_c . W_UV "
                                  "(head_gemv), packed weights, 8 rotating weight sets",
+        "stream_floor_us": t_floor * 1e6,
+        "stream_floor_note": "one launch of a plain read kernel over one weight set's bytes "
+                             "(16.8 MB), 8 rotating buffers: the floor of each absorption "
+                             "product, so two dependent products cost at least twice this",
         "decode_step_us": t_full * 1e6,
         "decode_step_note": "absorb_query + latent kernel + merge fused with the W_UV "
                             "projection (3 launches), rotating inputs and weights",
@@ -743,7 +759,8 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
     }
     log(f"config 5: latent kernel {t * 1e6:.1f} us, {res['hbm_gbs']:.0f} GB/s "
         f"({100 * res['hbm_frac']:.1f}% HBM), {res['mfma_tflops']:.0f} TFLOP/s; "
-        f"absorption GEMMs {t_gemm * 1e6:.1f} us; whole decode step {t_full * 1e6:.1f} us")
+        f"absorption GEMMs {t_gemm * 1e6:.1f} us (one 16.8 MB streaming launch: "
+        f"{t_floor * 1e6:.2f} us); whole decode step {t_full * 1e6:.1f} us")
     if cpu_sample:
         from oracle import mla as omla
 

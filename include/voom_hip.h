@@ -472,6 +472,15 @@ int voom_reload_record(const void* record, int rec_slots, int first, void* const
                        const int32_t* slots, int n_slots, int tag, int32_t* status,
                        hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Calibration (no counterpart in the reference): one launch that reads
+ * n_bytes of device memory (16-byte aligned) with `workgroups` workgroups of
+ * 256; sink[w] ^= the XOR of the words workgroup w read.  bench.py times
+ * it to give the floor of a single launch streaming a buffer of a given size.
+ * ------------------------------------------------------------------------- */
+int voom_stream_read(const void* src, size_t n_bytes, uint32_t* sink, int workgroups,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -365,6 +365,17 @@ def _record_call_args(pools: list[torch.Tensor], slots: torch.Tensor, record: to
     return ptrs, sbytes, counts
 
 
+def stream_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 512,
+                stream: torch.cuda.Stream | None = None) -> None:
+    """One launch reading all of ``src`` (device, contiguous, 16-byte multiple):
+    the calibration kernel bench.py uses for the single-launch streaming floor.
+    ``sink`` is a device int32 tensor of at least ``workgroups`` entries."""
+    _require_device(src, sink)
+    nbytes = src.numel() * src.element_size()
+    _require(sink.dtype == torch.int32 and sink.numel() >= workgroups, "sink too small")
+    _lib.call("voom_stream_read", _ptr(src), nbytes, _ptr(sink), int(workgroups), _stream(stream))
+
+
 def record_prepare() -> None:
     """Set the spill-record kernels up on the current device ahead of the first
     spill (their one-time launch setup costs about a millisecond each)."""
