@@ -842,8 +842,28 @@ def bench_position_free(steps: int, warmup: int, cpu_sample: bool) -> dict:
         "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, calibrated; "
                           "profiles/position_free_decode.md (attention kernel)",
     }
+    # the floor of this page pattern: a plain gather kernel reading the same
+    # K and V page rows (2 KiB each, the call's table), nothing else
+    sink = torch.zeros(2048, dtype=torch.int32, device="cuda")
+
+    def gather(i):
+        q, kp, vp, table = sets[i % 4]
+        ops.gather_read(kp, table, sink, base2=vp, workgroups=2048)
+
+    for i in range(4):
+        gather(i)
+    torch.cuda.synchronize()
+    t_g = graph_seconds([lambda i=i: gather(i) for i in range(4)], max(1, steps // 4))
+    g_bytes = TK * 2 * NKV * D * 2
+    res["page_gather_floor_us"] = t_g * 1e6
+    res["page_gather_floor_gbs"] = g_bytes / t_g / 1e9
+    res["page_gather_floor_note"] = ("plain gather kernel over the same K and V page rows "
+                                     "(one launch, 4 KiB per key): the rate this page "
+                                     "pattern delivers without any compute")
+    res["frac_of_page_gather_floor"] = res["hbm_gbs"] / res["page_gather_floor_gbs"]
     log(f"position-free: {t * 1e6:.1f} us per call, {res['hbm_gbs']:.0f} GB/s "
-        f"({100 * res['hbm_frac']:.1f}% HBM)")
+        f"({100 * res['hbm_frac']:.1f}% HBM); a plain gather of the same K/V pages runs at "
+        f"{res['page_gather_floor_gbs']:.0f} GB/s")
     if cpu_sample:
         from oracle import position_free as opf
 

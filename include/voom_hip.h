@@ -480,6 +480,14 @@ int voom_reload_record(const void* record, int rec_slots, int first, void* const
  * ------------------------------------------------------------------------- */
 int voom_stream_read(const void* src, size_t n_bytes, uint32_t* sink, int workgroups,
                      hipStream_t stream);
+/* The same for a row gather: reads row idx[i] (clamped into [0, n_base_rows))
+ * of row_bytes (1 to 4 KiB, whole KiB) from base, and from base2 when it is
+ * not NULL, for i < n_rows, four rows in flight per wavefront, 1 KiB per load
+ * instruction.  bench.py times it over the position-free workload's page ids
+ * in the K and V pools: the floor of reading those pages. */
+int voom_gather_read(const void* base, const void* base2, size_t row_bytes, int n_base_rows,
+                     const int32_t* idx, int n_rows, uint32_t* sink, int workgroups,
+                     hipStream_t stream);
 
 #ifdef __cplusplus
 }

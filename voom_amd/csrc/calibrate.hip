@@ -52,3 +52,75 @@ extern "C" int voom_stream_read(const void* src, size_t n_bytes, uint32_t* sink,
                      0, stream, static_cast<const u32x4*>(src), n_bytes / 16, sink);
   return VOOM_LAUNCH_CHECK("stream_read: launch");
 }
+
+namespace voom {
+namespace {
+
+// Row gather: wavefront v (of all the grid's) reads rows v, v + V, ... of the
+// index list, each row_bytes (a multiple of 1 KiB) at base + idx[r] *
+// row_bytes -- and the same row of base2 when given -- one 1 KiB piece per
+// instruction, four rows in flight.
+__global__ __launch_bounds__(kThreads) void gather_read_kernel(const uint8_t* __restrict__ base,
+                                                               const uint8_t* __restrict__ base2,
+                                                               size_t row_bytes,
+                                                               const int32_t* __restrict__ idx,
+                                                               int n_rows, int n_base_rows,
+                                                               uint32_t* __restrict__ sink) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int waves = static_cast<int>(gridDim.x) * (kThreads / kWave);
+  const int wv = static_cast<int>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  const int pieces = static_cast<int>(row_bytes / 1024);
+  const int tensors = base2 != nullptr ? 2 : 1;
+  uint32_t acc = 0;
+  for (int r0 = wv; r0 < n_rows; r0 += 4 * waves) {
+    u32x4 v[4][2][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = r0 + u * waves;
+      int row = r < n_rows ? idx[r] : 0;
+      row = static_cast<unsigned>(row) < static_cast<unsigned>(n_base_rows) ? row : 0;
+      const size_t off = static_cast<size_t>(row) * row_bytes + 16 * lane;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint8_t* src = (t == 0 ? base : base2) + off;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          v[u][t][p] = (r < n_rows && t < tensors && p < pieces)
+                           ? *reinterpret_cast<const u32x4*>(src + 1024 * p)
+                           : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) acc ^= v[u][t][p][0] ^ v[u][t][p][1] ^ v[u][t][p][2] ^ v[u][t][p][3];
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) acc ^= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc), o));
+  if (lane == 0) atomicXor(sink + blockIdx.x, acc);
+}
+
+}  // namespace
+}  // namespace voom
+
+extern "C" int voom_gather_read(const void* base, const void* base2, size_t row_bytes,
+                                int n_base_rows, const int32_t* idx, int n_rows, uint32_t* sink,
+                                int workgroups, hipStream_t stream) {
+  VOOM_REQUIRE(base && idx && sink, "gather_read: null pointer");
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(base2) % 16 == 0, "gather_read: base2 not 16-byte aligned");
+  VOOM_REQUIRE(row_bytes > 0 && row_bytes % 1024 == 0 && row_bytes <= 4096,
+               "gather_read: row_bytes %zu must be 1, 2, 3 or 4 KiB", row_bytes);
+  VOOM_REQUIRE(reinterpret_cast<uintptr_t>(base) % 16 == 0, "gather_read: base not 16-byte aligned");
+  VOOM_REQUIRE(n_rows >= 0 && n_base_rows > 0 && workgroups > 0 && workgroups <= (1 << 20),
+               "gather_read: bad sizes");
+  if (n_rows == 0) return VOOM_OK;
+  hipLaunchKernelGGL(gather_read_kernel, dim3(static_cast<unsigned>(workgroups)), dim3(kThreads),
+                     0, stream, static_cast<const uint8_t*>(base), static_cast<const uint8_t*>(base2),
+                     row_bytes, idx, n_rows, n_base_rows, sink);
+  return VOOM_LAUNCH_CHECK("gather_read: launch");
+}

@@ -376,6 +376,22 @@ def stream_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 512,
     _lib.call("voom_stream_read", _ptr(src), nbytes, _ptr(sink), int(workgroups), _stream(stream))
 
 
+def gather_read(base: torch.Tensor, idx: torch.Tensor, sink: torch.Tensor,
+                base2: torch.Tensor | None = None, workgroups: int = 512,
+                stream: torch.cuda.Stream | None = None) -> None:
+    """One launch reading rows ``base[idx[i]]`` (base [rows, ...], each row 1-4
+    KiB), and the same rows of ``base2`` (same shape) when given -- the
+    calibration kernel for the floor of a page gather."""
+    _require_device(base, idx, sink, base2)
+    row_bytes = base[0].numel() * base.element_size()
+    _require(base2 is None or (base2.shape == base.shape and base2.dtype == base.dtype),
+             "base2 must have base's shape and dtype")
+    _require(idx.dtype == torch.int32 and idx.dim() == 1, "idx must be 1-D int32")
+    _require(sink.dtype == torch.int32 and sink.numel() >= workgroups, "sink too small")
+    _lib.call("voom_gather_read", _ptr(base), _ptr(base2), row_bytes, base.shape[0], _ptr(idx),
+              idx.numel(), _ptr(sink), int(workgroups), _stream(stream))
+
+
 def record_prepare() -> None:
     """Set the spill-record kernels up on the current device ahead of the first
     spill (their one-time launch setup costs about a millisecond each)."""
