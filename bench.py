@@ -733,6 +733,30 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
     t_floor = graph_seconds([lambda i=i: ops.stream_read(floor_bufs[i], sink) for i in range(8)],
                             max(1, steps // 8))
     del floor_bufs
+    # floors of the latent kernel's loads: the same decomposition (16 ranges per
+    # sequence, the two 64-head groups of a range each filling its tiles into
+    # LDS) with no arithmetic, and one workgroup per range with twice the ranges
+    # (each tile filled into one CU only)
+    # ranges the latent kernel picks by default: enough (sequence, range, head
+    # group) workgroups for one per CU
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    nr = max(1, -(-cus // (8 * 2)))
+    rows_buf = torch.empty(8 * 2 * nr * 64 * 512, dtype=torch.float16, device="cuda")
+    tsink = torch.zeros(8 * 2 * nr, dtype=torch.int32, device="cuda")
+
+    def tile_pass(i, ranges, groups):
+        s_ = sets[i % 4]
+        ops.tile_read(s_.lat_pool, s_.block_table, 16384, ranges, groups, rows_buf, tsink,
+                      q=q_lats[i % 4])
+
+    load_floor = {}
+    for ranges, groups in ((nr, 2), (2 * nr, 1)):
+        for i in range(4):
+            tile_pass(i, ranges, groups)
+        torch.cuda.synchronize()
+        load_floor[groups] = graph_seconds(
+            [lambda i=i: tile_pass(i, ranges, groups) for i in range(8)], max(1, steps // 8))
+    del rows_buf
     res = {
         "workload": "config 5: absorbed MLA decode, B=8, H=128, ctx 16384, latent 512+64 bf16 "
                     "in 64-token pages, 4 rotating input sets",
@@ -750,6 +774,13 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
         "stream_floor_note": "one launch of a plain read kernel over one weight set's bytes "
                              "(16.8 MB), 8 rotating buffers: the floor of each absorption "
                              "product, so two dependent products cost at least twice this",
+        "latent_load_floor_us": load_floor[2] * 1e6,
+        "latent_load_floor_one_fill_us": load_floor[1] * 1e6,
+        "latent_load_floor_note": "voom_tile_read: the latent kernel's loads alone (q rows, "
+                                  "64-token tiles through two LDS buffers, fp16 partial-row "
+                                  "stores), at its decomposition (16 ranges x 2 head groups "
+                                  "filling each range's tiles) and with 32 ranges x 1 group "
+                                  "(each tile filled once; twice the partials)",
         "decode_step_us": t_full * 1e6,
         "decode_step_note": "absorb_query + latent kernel + merge fused with the W_UV "
                             "projection (3 launches), rotating inputs and weights",
@@ -760,7 +791,8 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
     log(f"config 5: latent kernel {t * 1e6:.1f} us, {res['hbm_gbs']:.0f} GB/s "
         f"({100 * res['hbm_frac']:.1f}% HBM), {res['mfma_tflops']:.0f} TFLOP/s; "
         f"absorption GEMMs {t_gemm * 1e6:.1f} us (one 16.8 MB streaming launch: "
-        f"{t_floor * 1e6:.2f} us); whole decode step {t_full * 1e6:.1f} us")
+        f"{t_floor * 1e6:.2f} us); whole decode step {t_full * 1e6:.1f} us; loads alone "
+        f"{load_floor[2] * 1e6:.1f} us (one fill per tile: {load_floor[1] * 1e6:.1f} us)")
     if cpu_sample:
         from oracle import mla as omla
 

@@ -488,6 +488,18 @@ int voom_stream_read(const void* src, size_t n_bytes, uint32_t* sink, int workgr
 int voom_gather_read(const void* base, const void* base2, size_t row_bytes, int n_base_rows,
                      const int32_t* idx, int n_rows, uint32_t* sink, int workgroups,
                      hipStream_t stream);
+/* The data movement of the MLA latent kernel with no arithmetic: batch x
+ * ranges x groups workgroups (the groups of a range on one XCD); each copies
+ * its 64 query rows of q ([batch, 64 groups, 576] bf16, skipped when NULL)
+ * and the 64-token tiles of its token range of pool ([num_slots, 64, 576]
+ * bf16, page ids table[b][0..]) into LDS, two tile buffers, and writes
+ * 64 x 512 fp16 of rows_out ([batch x ranges x groups, 64, 512]); sink has
+ * one entry per workgroup.  bench.py times it at the latent kernel's own
+ * decomposition (groups 2) and with one workgroup per range (groups 1): the
+ * floors of the two ways of splitting the heads. */
+int voom_tile_read(const void* pool, int num_slots, const int32_t* table, const void* q,
+                   int batch, int max_pages, int ctx, int ranges, int groups, void* rows_out,
+                   uint32_t* sink, hipStream_t stream);
 
 #ifdef __cplusplus
 }

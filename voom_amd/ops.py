@@ -392,6 +392,30 @@ def gather_read(base: torch.Tensor, idx: torch.Tensor, sink: torch.Tensor,
               idx.numel(), _ptr(sink), int(workgroups), _stream(stream))
 
 
+def tile_read(pool: torch.Tensor, table: torch.Tensor, ctx: int, ranges: int, groups: int,
+              rows: torch.Tensor, sink: torch.Tensor, q: torch.Tensor | None = None,
+              stream: torch.cuda.Stream | None = None) -> None:
+    """One launch with the data movement of the MLA latent kernel and no
+    arithmetic: ``table.shape[0] * ranges * groups`` workgroups stream the
+    64-token tiles of ``pool`` ([slots, 64, 576] bf16) for their token range
+    (and their 64 rows of ``q`` [B, 64 groups, 576] when given) through LDS
+    and write 64 x 512 fp16 of ``rows`` each -- the calibration kernel for the
+    floor of the latent contraction's loads."""
+    _require_device(pool, table, rows, sink, q)
+    _require(pool.dim() == 3 and tuple(pool.shape[1:]) == (64, 576) and pool.dtype == torch.bfloat16,
+             "pool must be [slots, 64, 576] bf16")
+    _require(table.dtype == torch.int32 and table.dim() == 2, "table must be [B, max_pages] int32")
+    batch = table.shape[0]
+    grid = batch * ranges * groups
+    _require(rows.numel() * rows.element_size() >= grid * 64 * 512 * 2, "rows too small")
+    _require(sink.dtype == torch.int32 and sink.numel() >= grid, "sink too small")
+    _require(q is None or (q.dtype == torch.bfloat16 and q.numel() >= batch * groups * 64 * 576),
+             "q must hold [B, 64 groups, 576] bf16")
+    _lib.call("voom_tile_read", _ptr(pool), pool.shape[0], _ptr(table), _ptr(q), batch,
+              table.shape[1], int(ctx), int(ranges), int(groups), _ptr(rows), _ptr(sink),
+              _stream(stream))
+
+
 def record_prepare() -> None:
     """Set the spill-record kernels up on the current device ahead of the first
     spill (their one-time launch setup costs about a millisecond each)."""
