@@ -132,10 +132,10 @@ def test_paging_invariance_is_bitwise():
     assert torch.equal(a, b2)
 
 
-def test_config5_full_size_two_sequences():
+def test_config5_full_size_every_sequence():
     print("[mla] config 5 full size", flush=True)
     inp = synthetic.mla_decode_inputs()
-    check_latent(inp, batches=[0, 7])
+    check_latent(inp)
 
 
 @pytest.mark.parametrize("B,H,K,N", [(8, 128, 128, 512), (8, 128, 512, 128), (3, 5, 40, 64),

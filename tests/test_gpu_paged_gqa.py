@@ -211,14 +211,14 @@ def test_merge_states_equals_full_attention():
                                atol=ATOL, rtol=RTOL)
 
 
-def test_config2_full_size_matches_oracle_on_four_sequences():
+def test_config2_full_size_matches_oracle_on_every_sequence():
     print("[gqa] case config-2 full size", flush=True)
     inp = synthetic.gqa_decode_inputs(device="cuda")
     out = ops.paged_gqa_decode(inp.q, inp.k_pool, inp.v_pool, inp.block_table, inp.ctx_lens,
                                scale=inp.scale)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
-    for b in (0, 5, 10, 15):
+    for b in range(inp.q.shape[0]):
         slots = inp.table_host[b, : -(-int(inp.ctx_host[b]) // 64)]
         idx = torch.from_numpy(slots.astype(np.int64)).cuda()
         k = inp.k_pool[idx].float().cpu().numpy()
