@@ -46,6 +46,57 @@ def test_latent_contraction_small(ctx):
     check_latent(inp)
 
 
+@pytest.mark.parametrize("ctx", [[1, 64], [63, 65, 200], [300, 1000, 4097]])
+def test_latent_contraction_small_128_heads(ctx):
+    print(f"[mla] latent 128 heads ctx={ctx}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=len(ctx), heads=128, ctx_lens=ctx, slack_pages=2)
+    check_latent(inp)
+
+
+@pytest.mark.parametrize("nr", [1, 3, 8, 40])
+def test_range_splits_agree_128_heads(nr):
+    print(f"[mla] 128 heads ranges={nr}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=2, heads=128, ctx_lens=[777, 2048])
+    check_latent(inp, num_ranges=nr)
+
+
+@pytest.mark.parametrize("heads", [64, 128])
+@pytest.mark.parametrize("jump", [[(0, 40), (1, 250)], [(0, 700 - 3), (1, 130)]])
+def test_restart_after_a_late_jump(heads, jump):
+    # Latent rows scaled so that the scores of a few tokens sit far more than
+    # 2^64 (log2 units) above the first tile's: the kernel keeps the first
+    # tile's maximum as the softmax reference and starts a range over when a
+    # later score exceeds it by that much.  Token 40 lies in the first tile
+    # of sequence 0, 697 in its last tile, 250 and 130 in later tiles of
+    # sequence 1.
+    print(f"[mla] restart heads={heads} jump={jump}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=2, heads=heads, ctx_lens=[700, 300])
+    lat = inp.lat_pool
+    lat.mul_(0.05)
+    for b, tok in jump:
+        slot = int(inp.table_host[b, tok // 64])
+        lat[slot, tok % 64] *= 2000.0
+    q_lat, _, _ = q_lat_of(inp)
+    ql = q_lat.float().cpu().numpy()
+    for nr in (1, 3):
+        wc, lse = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                                        scale=inp.scale, return_lse=True, num_ranges=nr)
+        torch.cuda.synchronize()
+        got = wc.float().cpu().numpy()
+        for b in range(2):
+            lat_b = synthetic.mla_logical_latent(inp, b)
+            ref = omla.absorbed_weighted_c(ql[b:b + 1, :, None, :], lat_b[None], 64, inp.scale,
+                                           bf16=True)[0, :, 0]
+            # the jump rows put outputs in the hundreds: the bar is taken
+            # relative to each sequence's largest output
+            top = float(np.abs(ref).max())
+            np.testing.assert_allclose(got[b] / top, ref / top, atol=ATOL, rtol=0)
+            s_ = (ql[b].astype(np.float64) @ lat_b.T.astype(np.float64)) * inp.scale
+            m = s_.max(axis=1)
+            ref_lse = m + np.log(np.exp(s_ - m[:, None]).sum(axis=1))
+            np.testing.assert_allclose(lse[b].cpu().numpy(), ref_lse, atol=1e-2, rtol=1e-3)
+
+
 @pytest.mark.parametrize("nr", [1, 3, 8])
 def test_range_splits_agree(nr):
     print(f"[mla] ranges={nr}", flush=True)
