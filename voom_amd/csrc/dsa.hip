@@ -17,11 +17,11 @@
 // (key i16, group g) then holds heads 4g + r of its key, so relu, the head
 // weights and the head sum stay in registers plus two cross-group adds.
 //
-// Top-k, three launches per call: (1) one workgroup per row places a
-// threshold T0 at a fixed rank of a strided sample of the row; (2) chunk
-// workgroups (4,096 keys each) move the keys >= T0, with their indices and in
-// index order, to per-chunk slots -- the row is read once, by many CUs;
-// (3) one workgroup per row gathers the candidates into LDS (at most 16,384)
+// Top-k, two launches per call: (1) chunk workgroups (4,096 keys each) each
+// place the same threshold T0 at a fixed rank of a strided sample of the row
+// and move the keys >= T0, with their indices and in index order, to
+// per-chunk slots -- the row is read once, by many CUs; (2) one workgroup
+// per row gathers the candidates into LDS (at most 16,384)
 // and runs the exact selection there: radix passes of up to 11 bits below the
 // leading bits every candidate shares find the k-th largest key T and how
 // many keys equal to T to keep, and an ordered write -- each wavefront owns a
@@ -162,7 +162,6 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* tmp, int& total)
 constexpr int kCandCap = 16384;  // candidate keys held in LDS
 constexpr int kSample = 4096;    // keys sampled to place the threshold
 constexpr int kChunkKeys = 4096; // keys per compaction workgroup
-constexpr int kCompactThreads = 256;
 
 // Over the 2048-entry histogram in descending bin order: the bin where the
 // running count from the top reaches `want` (found[0]) and the count of the
@@ -332,14 +331,20 @@ struct TopkWs {
 
 __host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys - 1) / kChunkKeys; }
 
-// 1. Threshold: rows of at most kCandCap keys take every key as a candidate
-// (T0 = 0).  Longer rows: T0 is the key of rank 1.5 x (the sample's share of
-// k) + 32 in a sample of kSample keys (runs of 4 adjacent keys spread evenly
-// over a 16-byte aligned row, else single keys at an even stride), found exactly by the radix
-// select in LDS -- about 1.5 k candidates, with margin, and no more than the
-// sample's ties at T0 allow.
+// 1. Threshold and compaction, one launch: one workgroup per chunk of
+// kChunkKeys keys of a row.  Each workgroup places the row's threshold T0
+// itself -- every one from the same sample with the same exact select, so all
+// agree -- while its chunk's keys are in flight, then moves every key >= T0,
+// with its index and in index order, to the chunk's slots.  Rows of at most
+// kCandCap keys take every key as a candidate (T0 = 0).  Longer rows: T0 is
+// the key of rank 1.5 x (the sample's share of k) + 32 in a sample of kSample
+// keys (runs of 4 adjacent keys spread evenly over a 16-byte aligned row, else
+// single keys at an even stride), found exactly by the radix select in LDS --
+// about 1.5 k candidates, with margin, and no more than the sample's ties at
+// T0 allow.  (As separate launches, the one-workgroup threshold kernel took
+// 9.2 us and the compaction 5.0 us behind it.)
 template <bool VEC>
-__global__ __launch_bounds__(kTopkThreads) void dsa_topk_threshold_kernel(
+__global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
     const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
     int K) {
   __shared__ uint32_t sample[kSample];
@@ -347,58 +352,6 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_threshold_kernel(
   __shared__ int scan_tmp[kTopkWaves];
   __shared__ int found[2];
   const int tid = threadIdx.x;
-  const int b = blockIdx.x;
-  int n = lens[b];
-  n = n < 0 ? 0 : (n > cap ? cap : n);
-  if (n <= kCandCap) {
-    if (tid == 0) ws.t0[b] = 0u;
-    return;
-  }
-  const float* sb = scores + static_cast<size_t>(b) * cap;
-  constexpr int kPer = kSample / kTopkThreads;
-  float v[kPer];
-  if (VEC) {
-    static_assert(kSample / kTopkThreads == 4, "one float4 of keys per thread");
-    // runs of kPer adjacent keys, one 16-byte load per thread, spread evenly
-    // over the row (n > kCandCap, so every run lies inside it)
-    const int j0 = static_cast<int>(static_cast<long long>(tid) * n / kTopkThreads) & ~(kPer - 1);
-    const float4 f = *reinterpret_cast<const float4*>(sb + j0);
-    v[0] = f.x;
-    v[1] = f.y;
-    v[2] = f.z;
-    v[3] = f.w;
-  } else {
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int j = tid + k * kTopkThreads;
-      v[k] = sb[static_cast<int>(static_cast<long long>(j) * n / kSample)];
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) sample[tid * kPer + k] = order_key(v[k]);
-  __syncthreads();
-  long long r = (static_cast<long long>(K) * kSample + n - 1) / n;
-  r = r + r / 2 + 32;
-  const int want = static_cast<int>(r > kSample ? kSample : r);
-  uint32_t T0;
-  int unused;
-  radix_select([&](int i) { return sample[i]; }, kSample, want, hist, scan_tmp, found, T0,
-               unused);
-  if (tid == 0) ws.t0[b] = T0;
-}
-
-// 2. Compaction: one workgroup per chunk of kChunkKeys keys of a row; every
-// key >= T0 goes, with its index and in index order, to the chunk's slots.
-// Each lane holds 16 keys in registers (the row is read once).
-template <bool VEC>
-__global__ __launch_bounds__(kCompactThreads) void dsa_topk_compact_kernel(
-    const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
-    int K) {
-  constexpr int kPerLane = kChunkKeys / kCompactThreads;  // 16, four groups of 4
-  __shared__ int wave_cnt[kCompactThreads / kWave];
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wv = tid / kWave;
   const int b = blockIdx.y;
   const int chunk = blockIdx.x;
   int n = lens[b];
@@ -407,61 +360,71 @@ __global__ __launch_bounds__(kCompactThreads) void dsa_topk_compact_kernel(
   const int c0 = chunk * kChunkKeys;
   if (c0 >= n) return;
   const float* sb = scores + static_cast<size_t>(b) * cap;
-  const uint32_t T0 = ws.t0[b];
-  // wave wv owns keys [c0 + wv*1024, +1024): 4 groups of 256, four keys per lane
-  const int base = c0 + wv * (kChunkKeys / (kCompactThreads / kWave));
-  float v[4][4];
+
+  // this chunk's keys c0 + 4 tid .. + 3, loaded first so that they are in
+  // flight while the threshold is placed
+  static_assert(kChunkKeys == 4 * kTopkThreads, "four keys of the chunk per thread");
+  const int i = c0 + 4 * tid;
+  float v[4];
+  if (VEC && i + 3 < n) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(sb + i);
+    v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
+  } else {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int i = base + k * 256 + 4 * lane;
-    if constexpr (VEC) {
-      if (i < n) {
-        const f32x4 t = *reinterpret_cast<const f32x4*>(sb + i);
-        v[k][0] = t[0]; v[k][1] = t[1]; v[k][2] = t[2]; v[k][3] = t[3];
-      }
+    for (int e = 0; e < 4; ++e) v[e] = i + e < n ? sb[i + e] : 0.f;
+  }
+
+  uint32_t T0 = 0u;
+  if (n > kCandCap) {
+    constexpr int kPer = kSample / kTopkThreads;
+    float sv[kPer];
+    if (VEC) {
+      static_assert(kSample / kTopkThreads == 4, "one float4 of sample keys per thread");
+      // runs of kPer adjacent keys, one 16-byte load per thread, spread evenly
+      // over the row (n > kCandCap, so every run lies inside it)
+      const int j0 =
+          static_cast<int>(static_cast<long long>(tid) * n / kTopkThreads) & ~(kPer - 1);
+      const float4 f = *reinterpret_cast<const float4*>(sb + j0);
+      sv[0] = f.x;
+      sv[1] = f.y;
+      sv[2] = f.z;
+      sv[3] = f.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[k][e] = i + e < n ? sb[i + e] : 0.f;
-    }
-  }
-  bool in[4][4];
-  int cnt[4];
-  int mine = 0;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    cnt[k] = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = base + k * 256 + 4 * lane + e;
-      in[k][e] = i < n && order_key(v[k][e]) >= T0;
-      cnt[k] += in[k][e] ? 1 : 0;
-    }
-    mine += cnt[k];
-  }
-  int wave_total = mine;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) wave_total += __shfl_xor(wave_total, o);
-  if (lane == 0) wave_cnt[wv] = wave_total;
-  __syncthreads();
-  int pos = 0;
-  int all = 0;
-  for (int k = 0; k < kCompactThreads / kWave; ++k) {
-    pos += k < wv ? wave_cnt[k] : 0;
-    all += wave_cnt[k];
-  }
-  uint2* slots = ws.cand + (static_cast<size_t>(b) * ws.chunks + chunk) * kChunkKeys;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int inc = wave_inclusive_scan(cnt[k], lane);
-    int at = pos + inc - cnt[k];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (in[k][e]) {
-        slots[at] = make_uint2(order_key(v[k][e]), static_cast<uint32_t>(base + k * 256 + 4 * lane + e));
-        ++at;
+      for (int k = 0; k < kPer; ++k) {
+        const int j = tid + k * kTopkThreads;
+        sv[k] = sb[static_cast<int>(static_cast<long long>(j) * n / kSample)];
       }
     }
-    pos += __shfl(inc, kWave - 1);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) sample[tid * kPer + k] = order_key(sv[k]);
+    __syncthreads();
+    long long r = (static_cast<long long>(K) * kSample + n - 1) / n;
+    r = r + r / 2 + 32;
+    const int want = static_cast<int>(r > kSample ? kSample : r);
+    int unused;
+    radix_select([&](int k) { return sample[k]; }, kSample, want, hist, scan_tmp, found, T0,
+                 unused);
+  }
+  if (chunk == 0 && tid == 0) ws.t0[b] = T0;
+
+  // keys >= T0 in index order: a scan over the workgroup places each thread's
+  bool in[4];
+  int cnt = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    in[e] = i + e < n && order_key(v[e]) >= T0;
+    cnt += in[e] ? 1 : 0;
+  }
+  int all;
+  int at = block_exclusive_scan(cnt, scan_tmp, all);
+  uint2* slots = ws.cand + (static_cast<size_t>(b) * ws.chunks + chunk) * kChunkKeys;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (in[e]) {
+      slots[at] = make_uint2(order_key(v[e]), static_cast<uint32_t>(i + e));
+      ++at;
+    }
   }
   if (tid == 0) ws.counts[static_cast<size_t>(b) * ws.chunks + chunk] = all;
 }
@@ -615,24 +578,15 @@ extern "C" int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* 
   ws.cand = reinterpret_cast<uint2*>(
       p + t0_bytes + ((static_cast<size_t>(batch) * ws.chunks * 4 + 255) & ~size_t(255)));
   const bool vec = cap % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0;
-  if (vec) {
-    hipLaunchKernelGGL(dsa_topk_threshold_kernel<true>, dim3(static_cast<unsigned>(batch)),
-                       dim3(kTopkThreads), 0, stream, scores, lens, ws, cap, k);
-  } else {
-    hipLaunchKernelGGL(dsa_topk_threshold_kernel<false>, dim3(static_cast<unsigned>(batch)),
-                       dim3(kTopkThreads), 0, stream, scores, lens, ws, cap, k);
-  }
-  int rc = VOOM_LAUNCH_CHECK("dsa_topk: threshold kernel launch");
-  if (rc) return rc;
   const dim3 cgrid(static_cast<unsigned>(ws.chunks), static_cast<unsigned>(batch));
   if (vec) {
-    hipLaunchKernelGGL(dsa_topk_compact_kernel<true>, cgrid, dim3(kCompactThreads), 0, stream,
+    hipLaunchKernelGGL(dsa_topk_compact_kernel<true>, cgrid, dim3(kTopkThreads), 0, stream,
                        scores, lens, ws, cap, k);
   } else {
-    hipLaunchKernelGGL(dsa_topk_compact_kernel<false>, cgrid, dim3(kCompactThreads), 0, stream,
+    hipLaunchKernelGGL(dsa_topk_compact_kernel<false>, cgrid, dim3(kTopkThreads), 0, stream,
                        scores, lens, ws, cap, k);
   }
-  rc = VOOM_LAUNCH_CHECK("dsa_topk: compaction kernel launch");
+  int rc = VOOM_LAUNCH_CHECK("dsa_topk: threshold + compaction kernel launch");
   if (rc) return rc;
   hipLaunchKernelGGL(dsa_topk_select_kernel, dim3(static_cast<unsigned>(batch)),
                      dim3(kTopkThreads), 0, stream, scores, lens, ws, sel, sel_lens, cap, k);
