@@ -165,17 +165,28 @@ def bench_gqa(steps: int, warmup: int, cpu_sample: bool) -> dict:
         step()
     torch.cuda.synchronize()
     log(f"warmup done ({warmup} steps); timing {steps} steps")
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    # the timed region: exactly `steps` decode ops back to back, nothing else
+    # on the stream between the two bracketing events
     t_all0 = torch.cuda.Event(enable_timing=True)
     t_all1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_all0.record(stream)
-    for i in range(steps):
-        step(evs[i])
+    for _ in range(steps):
+        step()
     t_all1.record(stream)
     torch.cuda.synchronize()
     total_ms = t_all0.elapsed_time(t_all1)
-    nxt = [evs[i + 1][0] for i in range(steps - 1)] + [t_all1]
+    # a second, instrumented pass for the per-kernel figures: an event before
+    # each half of every op (the events themselves add a few microseconds per
+    # step, which is why the timed region above has none)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        step(evs[i])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    nxt = [evs[i + 1][0] for i in range(steps - 1)] + [t_end]
     main_ms = sorted(e[0].elapsed_time(e[1]) for e in evs)
     comb_ms = sorted(e[1].elapsed_time(n) for e, n in zip(evs, nxt))
     op_ms = sorted(e[0].elapsed_time(n) for e, n in zip(evs, nxt))
