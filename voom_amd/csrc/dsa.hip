@@ -486,17 +486,31 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
   uint32_t T;
   int kk;
   if (fits) {
-    // flat candidate j -> its chunk by binary search over the offsets
-    for (int j = tid; j < C; j += kTopkThreads) {
-      int lo = 0, hi = nch;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (chunk_off[mid] <= j) lo = mid; else hi = mid;
+    // flat candidate j -> its chunk by binary search over the offsets; every
+    // thread's loads (at most kCandCap / kTopkThreads) are issued before the
+    // first is stored to LDS, so the gather costs one memory round trip
+    constexpr int kPerThread = kCandCap / kTopkThreads;
+    uint2 e[kPerThread];
+#pragma unroll
+    for (int r = 0; r < kPerThread; ++r) {
+      const int j = tid + r * kTopkThreads;
+      if (j < C) {
+        int lo = 0, hi = nch;
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (chunk_off[mid] <= j) lo = mid; else hi = mid;
+        }
+        e[r] = ws.cand[(static_cast<size_t>(b) * ws.chunks + lo) * kChunkKeys +
+                       (j - chunk_off[lo])];
       }
-      const uint2 e = ws.cand[(static_cast<size_t>(b) * ws.chunks + lo) * kChunkKeys +
-                              (j - chunk_off[lo])];
-      cand_key[j] = e.x;
-      cand_idx[j] = static_cast<int32_t>(e.y);
+    }
+#pragma unroll
+    for (int r = 0; r < kPerThread; ++r) {
+      const int j = tid + r * kTopkThreads;
+      if (j < C) {
+        cand_key[j] = e[r].x;
+        cand_idx[j] = static_cast<int32_t>(e[r].y);
+      }
     }
     __syncthreads();
     auto lds_key = [&](int i) { return cand_key[i]; };
