@@ -2,7 +2,7 @@
 """Benchmark of the paged-KV hot path on one MI355X.
 
 Headline (``value``): paged GQA decode-attention HBM throughput at the
-Llama-3-8B shape: batch 16, 32 q / 8 kv heads, head_dim
+Llama-3-8B shape (config 2): batch 16, 32 q / 8 kv heads, head_dim
 128, contexts U[1024, 32768], 64-token pages at random pool slots, one query
 token per sequence.  A step is one decode-attention call over the whole batch
 with every input already resident in HBM; value = algorithmic bytes per step
@@ -836,7 +836,7 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
 
 
 def bench_position_free(steps: int, warmup: int, cpu_sample: bool) -> dict:
-    """Position-free decode (SURVEY next row 3): Llama-3-8B shape, one request,
+    """Position-free decode: Llama-3-8B shape, one request,
     32768 keys in one-token pages drawn at random from a 40000-page pool,
     keys stored before RoPE and rotated in the kernel at positions 0..32767,
     one query at position 32767.  Four rotating page pools (4 x 164 MB) keep the
@@ -932,7 +932,7 @@ def bench_position_free(steps: int, warmup: int, cpu_sample: bool) -> dict:
 
 
 def bench_dsa(steps: int, warmup: int, cpu_sample: bool) -> dict:
-    """DSA decode step (SURVEY next row 4): B=1, 131,072 cached tokens, index
+    """DSA decode step: B=1, 131,072 cached tokens, index
     keys [131072, 128] bf16, 32 index heads, top-2048, then the absorbed-MLA
     contraction (128 heads, latent 576 in 64-token pages) over the selected
     rows only.  Eight rotating index-key sets (8 x 33.5 MB) keep the scoring

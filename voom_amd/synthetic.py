@@ -1,6 +1,6 @@
 """Seeded synthetic inputs for the paged-KV workloads (bench, smoke and tests).
 
-The shapes and seeds follow the BASELINE configurations of this build:
+The shapes and seeds are those of the benchmark configurations:
   gqa_decode_inputs   config 2 -- B=16, 32 q / 8 kv heads, D=128, contexts
                       U[1024, 32768] (seed 2), K,V ~ N(0,1) (seed 3) with
                       RoPE(theta=5e5) applied to K at positions U[0, 131072)
