@@ -527,6 +527,22 @@ __device__ __forceinline__ int group_swizzle(int r) {
   return ((r >> 2) ^ (((r >> 1) & 1) << 2)) & 7;
 }
 
+// Build knobs of mla_group64_kernel (measured defaults): k-steps of latent
+// rows read ahead of the score MFMAs, P.V steps of C^T read ahead, and one
+// next-tile load issued every VOOM_MLA_LOAD_EVERY score k-steps.
+#ifndef VOOM_MLA_SCORE_AHEAD
+#define VOOM_MLA_SCORE_AHEAD 5
+#endif
+#ifndef VOOM_MLA_PV_AHEAD
+#define VOOM_MLA_PV_AHEAD 2
+#endif
+#ifndef VOOM_MLA_LOAD_EVERY
+#define VOOM_MLA_LOAD_EVERY 2
+#endif
+static_assert((kLat / 16 + VOOM_MLA_LOAD_EVERY - 1) / VOOM_MLA_LOAD_EVERY >= kLoadsPerTile / 4,
+              "every next-tile load must fall on a score k-step");
+static_assert(VOOM_MLA_SCORE_AHEAD >= 1 && VOOM_MLA_PV_AHEAD >= 1, "read-ahead of at least one step");
+
 template <bool SPARSE>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void mla_group64_kernel(MlaArgs a) {
@@ -748,7 +764,7 @@ void mla_group64_kernel(MlaArgs a) {
     // until the memory pipeline has taken them. ----
     f32x16 sc = f32x16{};
     {
-      constexpr int kAhead = 5;
+      constexpr int kAhead = VOOM_MLA_SCORE_AHEAD;
       u32x4 ring[kAhead];
 #pragma unroll
       for (int s = 0; s < kAhead; ++s) {
@@ -766,8 +782,8 @@ void mla_group64_kernel(MlaArgs a) {
         }
         sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qv, sc, 0, 0, 0);
         __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-        if ((s & 1) == 0 && (s >> 1) < kGLoads) {
-          const int k = s >> 1;
+        if (s % VOOM_MLA_LOAD_EVERY == 0 && s / VOOM_MLA_LOAD_EVERY < kGLoads) {
+          const int k = s / VOOM_MLA_LOAD_EVERY;
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               nsrc, (lds_void*)(next + (w + kGWaves * k) * 512), 16,
               static_cast<int>(noff[k & 1] + 128 * (k >> 1)), 0, 0, 0);
@@ -816,7 +832,7 @@ void mla_group64_kernel(MlaArgs a) {
     // ---- operands of P.V: C^T by transposed reads of the tile, P from LDS
     // once every wavefront has written it.  The C^T operand of step (ks, dt)
     // is read two steps ahead, P one k-step ahead. ----
-    constexpr int kCAhead = 2;
+    constexpr int kCAhead = VOOM_MLA_PV_AHEAD;
     bf16x8 pb[2][2];
     bf16x8 cv[kCAhead + 1];
     auto read_c = [&](int i) {  // step i = 4 ks + dt
