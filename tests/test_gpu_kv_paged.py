@@ -317,6 +317,41 @@ def test_spill_dir_writes_page_files_like_the_reference(tmp_path, compress):
     assert not any(path.exists() for path in spill_paths)
 
 
+def test_incompressible_high_planes_stay_raw(tmp_path):
+    # runtime/warm_tier.py:56,79-81: a page that barely compresses is not kept
+    # compressed.  K of random bit patterns has random high bytes (ratio ~1);
+    # V of small values has high bytes of a few exponents (ratio well above
+    # 1.15).  Both come back bit-exact from the page files alone.
+    import json
+    import struct
+
+    print("[kv-disk] zstd admission: incompressible high planes stay raw", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    B, NKV, D, PT = 1, 2, 64, 16
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, spill_dir=tmp_path, page_positions=PT,
+                      resident_pages=0, compress_spill=True, host_max_bytes=1)
+    k = torch.randint(-32768, 32768, (B, NKV, 2 * PT, D), generator=gen, device="cuda",
+                      dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    v = (torch.randn((B, NKV, 2 * PT, D), generator=gen, device="cuda") * 0.01).to(
+        torch.bfloat16)
+    kv.append(0, k, v)
+    originals = [tuple(t.clone() for t in p.load()) for p in kv._pages[0]]
+    kv.spill([(0, 0), (0, 1)])  # host_max_bytes=1: the files are written, host copies dropped
+    for i, page in enumerate(kv._pages[0]):
+        assert page.path is not None and page.host is None  # on disk only
+        with open(page.path, "rb") as f:
+            (n,) = struct.unpack("<Q", f.read(8))
+            head = json.loads(f.read(n))
+        hz = {t["name"]: t["hi_z"] for t in head["tensors"]}
+        assert hz["k"] is None, hz
+        assert hz["v_t"] is not None and hz["v_t"] * 1.15 <= head["tensors"][1]["hi"], hz
+        lk, lv = page.load()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(lk), bits(originals[i][0]))
+        assert torch.equal(bits(lv), bits(originals[i][1]))
+    kv.release()
+
+
 def test_host_budget_moves_pages_to_disk_and_back(tmp_path):
     print("[kv-disk] host_max_bytes evicts host copies; attend/load/reload from files", flush=True)
     gen = torch.Generator(device="cuda").manual_seed(11)

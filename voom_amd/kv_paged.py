@@ -55,6 +55,12 @@ from .host_arena import HostArena, HostBlock
 from .page_pool import DevicePagePool, v_pages_to_tokens
 
 
+# A high plane is kept zstd-compressed only when it shrinks by at least this
+# factor; one that barely compresses is stored raw and costs no decompression
+# (the admission rule of runtime/warm_tier.py:56,79-81).
+MIN_COMPRESS_RATIO = 1.15
+
+
 @dataclass
 class KVStats:
     """Counters of kv_paged.py:35-53 (same fields and summary text)."""
@@ -1217,14 +1223,21 @@ class PagedKVCache:
             i = p.host_j - r * sb.chunk
             his = [rec[hi_off[t] + i * sb.parts[t]:hi_off[t] + (i + 1) * sb.parts[t]]
                    for t in range(T)]
-            frames = None
+            planes = his
+            packed = [False] * T
             if scratch is not None:
-                frames = []
+                planes = []
                 for t in range(T):
                     n = _zstd.compress_into(his[t], scratch, 1)
-                    comp += n
-                    # only a page file keeps the frame
-                    frames.append(scratch[:n].copy() if meta is not None else None)
+                    if n * MIN_COMPRESS_RATIO <= sb.parts[t]:
+                        comp += n
+                        packed[t] = True
+                        # only a page file keeps the frame
+                        planes.append(scratch[:n].copy() if meta is not None else None)
+                    else:
+                        # a plane that barely compresses stays raw
+                        comp += sb.parts[t]
+                        planes.append(his[t])
                 comp += sum(sb.parts)  # the raw low planes
                 raw += p.nbytes
                 p._compressed = True
@@ -1233,9 +1246,7 @@ class PagedKVCache:
                        for t in range(T)]
                 path = page_file.page_path(self.spill_dir, p.layer, p.index)
                 sums = sb.sums(p.host_j).tolist() if sb.nsum else None
-                page_file.write(path, p.layer, p.index, meta, los,
-                                frames if frames is not None else his,
-                                [frames is not None] * T, sums=sums)
+                page_file.write(path, p.layer, p.index, meta, los, planes, packed, sums=sums)
                 p._path = path
         if raw:
             with self._stats_lock:
