@@ -163,31 +163,6 @@ constexpr int kCandCap = 16384;  // candidate keys held in LDS
 constexpr int kSample = 4096;    // keys sampled to place the threshold
 constexpr int kChunkKeys = 4096; // keys per compaction workgroup
 
-// Over the 2048-entry histogram in descending bin order: the bin where the
-// running count from the top reaches `want` (found[0]) and the count of the
-// bins above it (found[1]).  Thread t holds bins 2047 - (E t + e), e < E.
-__device__ __forceinline__ void find_bin(const int* hist, int want, int* scan_tmp, int* found) {
-  const int tid = threadIdx.x;
-  int c[kBinsPerThread];
-  int mine = 0;
-#pragma unroll
-  for (int e = 0; e < kBinsPerThread; ++e) {
-    c[e] = hist[2047 - (kBinsPerThread * tid + e)];
-    mine += c[e];
-  }
-  int total;
-  int run = block_exclusive_scan(mine, scan_tmp, total);
-#pragma unroll
-  for (int e = 0; e < kBinsPerThread; ++e) {
-    if (run < want && run + c[e] >= want) {
-      found[0] = 2047 - (kBinsPerThread * tid + e);
-      found[1] = run;
-    }
-    run += c[e];
-  }
-  __syncthreads();
-}
-
 // Radix select over `count` keys read by key(i): the rank-th largest key T
 // (rank >= 1) and how many keys equal to T belong to the top `rank` (kk).
 // The digits start below the leading bits that every key shares (from a
@@ -195,12 +170,24 @@ __device__ __forceinline__ void find_bin(const int* hist, int want, int* scan_tm
 // exponent, and a first digit over those bits would send every key to a
 // handful of histogram bins, serialising the LDS atomics.  Passes of 11 bits
 // then walk down to bit 0; a thread adds runs of equal bins as one atomic.
+// Three barriers per pass: after the histogram; after each thread has
+// taken (and zeroed, for the next pass) its two bins and each wavefront has
+// left its scan total; after the thread holding the crossing has written it.
+// (Zeroing the histogram and the scan as separate steps cost six barriers a
+// pass, 5.5 k cycles; one wavefront scanning all 2048 bins hit 32-way LDS
+// bank conflicts.)
+// found[] holds the result, scan_tmp kTopkWaves ints; hist must hold 2048 ints.
 template <typename KeyFn>
-__device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* scan_tmp,
-                             int* found, uint32_t& T, int& kk_out) {
+__device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* scan_tmp, int* found,
+                             uint32_t& T, int& kk_out) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
+  for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
+  if (tid == 0) {
+    found[0] = static_cast<int>(0xFFFFFFFFu);
+    found[1] = 0;
+  }
   uint32_t lo_k = 0xFFFFFFFFu;
   uint32_t hi_k = 0u;
   for (int i = tid; i < count; i += kTopkThreads) {
@@ -215,20 +202,14 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
     lo_k = a < lo_k ? a : lo_k;
     hi_k = b > hi_k ? b : hi_k;
   }
+  __syncthreads();  // found[] and hist initialised
   if (lane == 0) {
-    scan_tmp[wv] = static_cast<int>(lo_k);
-    hist[wv] = static_cast<int>(hi_k);
+    atomicMin(reinterpret_cast<unsigned int*>(&found[0]), lo_k);
+    atomicMax(reinterpret_cast<unsigned int*>(&found[1]), hi_k);
   }
   __syncthreads();
-  lo_k = 0xFFFFFFFFu;
-  hi_k = 0u;
-  for (int k = 0; k < kTopkWaves; ++k) {
-    const uint32_t a = static_cast<uint32_t>(scan_tmp[k]);
-    const uint32_t b = static_cast<uint32_t>(hist[k]);
-    lo_k = a < lo_k ? a : lo_k;
-    hi_k = b > hi_k ? b : hi_k;
-  }
-  __syncthreads();
+  lo_k = static_cast<uint32_t>(found[0]);
+  hi_k = static_cast<uint32_t>(found[1]);
   // bits above `top` are common to every key
   int top = 31 - __clz(static_cast<int>(lo_k ^ hi_k));  // -1 when all keys are equal
   uint32_t prefix = top < 31 ? (hi_k & ~((2u << (top < 0 ? 0 : top)) - 1u)) : 0u;
@@ -241,8 +222,6 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
     const int width = top + 1 < 11 ? top + 1 : 11;
     const int shift = top + 1 - width;
     const int bins = 1 << width;
-    for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
-    __syncthreads();
     int run_bin = -1;
     int run_n = 0;
     for (int i = tid; i < count; i += kTopkThreads) {
@@ -258,15 +237,39 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
       }
     }
     if (run_n) atomicAdd(&hist[run_bin], run_n);
-    __syncthreads();
-    find_bin(hist, kk, scan_tmp, found);
+    __syncthreads();  // histogram complete (found[] of the previous pass read)
+    // thread t owns bins 2047 - (2 t + e), e < 2, in descending order
+    int c[kBinsPerThread];
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < kBinsPerThread; ++e) {
+      const int bin = 2047 - (kBinsPerThread * tid + e);
+      c[e] = hist[bin];
+      hist[bin] = 0;
+      mine += c[e];
+    }
+    const int inc = wave_inclusive_scan(mine, lane);
+    if (lane == kWave - 1) scan_tmp[wv] = inc;
+    __syncthreads();  // wave totals in scan_tmp, bins zero again
+    int run = inc - mine;
+#pragma unroll
+    for (int k = 0; k < kTopkWaves; ++k) run += k < wv ? scan_tmp[k] : 0;
+#pragma unroll
+    for (int e = 0; e < kBinsPerThread; ++e) {
+      if (run < kk && run + c[e] >= kk) {
+        found[0] = 2047 - (kBinsPerThread * tid + e);
+        found[1] = run;
+      }
+      run += c[e];
+    }
+    __syncthreads();  // result in found[]
     const int d = found[0];
     kk -= found[1];
     prefix |= static_cast<uint32_t>(d) << shift;
     pmask |= static_cast<uint32_t>(bins - 1) << shift;
     top = shift - 1;
-    __syncthreads();
   }
+  __syncthreads();  // found[] read by every thread before anyone reuses it
   T = prefix;
   kk_out = kk;
 }
