@@ -771,7 +771,10 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
     res = {
         "workload": "config 5: absorbed MLA decode, B=8, H=128, ctx 16384, latent 512+64 bf16 "
                     "in 64-token pages, 4 rotating input sets",
-        "latent_kernel_us": t * 1e6,
+        "latent_and_merge_us": t * 1e6,
+        "latent_and_merge_note": "the latent kernel and the merge of its range partials (two "
+                                 "launches per step, graph replay); the latent kernel alone "
+                                 "is in profiles/mla_config5.md's kernel trace",
         "hbm_gbs": nbytes / t / 1e9,
         "hbm_frac": nbytes / t / 1e9 / HBM_PEAK_GBS,
         "mfma_tflops": flops / t / 1e12,
@@ -799,7 +802,7 @@ def bench_mla(steps: int, warmup: int, cpu_sample: bool) -> dict:
         "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, calibrated; "
                           "profiles/mla_config5.md (latent kernel + reduce)",
     }
-    log(f"config 5: latent kernel {t * 1e6:.1f} us, {res['hbm_gbs']:.0f} GB/s "
+    log(f"config 5: latent kernel + merge {t * 1e6:.1f} us, {res['hbm_gbs']:.0f} GB/s "
         f"({100 * res['hbm_frac']:.1f}% HBM), {res['mfma_tflops']:.0f} TFLOP/s; "
         f"absorption GEMMs {t_gemm * 1e6:.1f} us (one 16.8 MB streaming launch: "
         f"{t_floor * 1e6:.2f} us); whole decode step {t_full * 1e6:.1f} us; loads alone "
