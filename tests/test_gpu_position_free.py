@@ -136,3 +136,60 @@ def test_pool_cache_sharing_matches_the_oracle():
     assert Kb.shape == (1, NKV, 80, D)
     b.release()
     assert pool.live_pages == 0
+
+
+@pytest.mark.parametrize("yarn", [False, True])
+def test_matches_the_rotated_page_cache(yarn):
+    """The reference's dense-versus-shared check (tests/test_kv_cache.py:359-447):
+    the same q, k, v through PositionFreeKVCache (unrotated keys, RoPE in the
+    kernel) and through PagedKVCache (keys rotated on the host in fp32, the
+    GQA kernel) -- a 7-token causal prefill, then one decode token -- with
+    plain RoPE and with static YaRN (explicit denominators; q and k scaled by
+    mscale before rotation, so the shared cache stores the scaled, unrotated
+    key).  Bar: 2e-2, the reference's tolerance for its decode comparison."""
+    from voom_amd.kv_paged import PagedKVCache
+    from voom_amd.position_free import PositionFreeKVCache, PositionFreePagePool
+    from voom_amd.synthetic import apply_rope_neox
+    print(f"[pf] against the rotated page cache, yarn={yarn}", flush=True)
+    NKV, NQ, D, T, theta = 2, 4, 64, 7, 10000.0  # 2 heads x 7 queries <= 16 columns
+    half = D // 2
+    g = torch.Generator().manual_seed(741)
+
+    def rnd(*shape):
+        return (torch.randn(shape, generator=g) * 0.5).to(torch.bfloat16)
+
+    q, k, v = rnd(1, NQ, T + 1, D), rnd(1, NKV, T + 1, D), rnd(1, NKV, T + 1, D)
+    den, mscale = None, 1.0
+    if yarn:
+        den = theta ** (torch.arange(half, dtype=torch.float32) / half)
+        den = den * torch.linspace(1.0, 4.0, half)
+        mscale = 1.1
+    k_store = (k.float() * mscale).to(torch.bfloat16)  # scaled, unrotated
+    cos, sin = ops.rope_cache(T + 1, D, theta, denominators=den, device="cuda")
+    cos, sin = cos.cpu(), sin.cpu()
+    q_rot = apply_rope_neox(q.float() * mscale, cos, sin).to(torch.bfloat16)
+    k_rot = apply_rope_neox(k_store, cos, sin).to(torch.bfloat16)
+    scale = D ** -0.5
+
+    pool = PositionFreePagePool(1, NKV, D, min_capacity=16, device="cuda")
+    shared = PositionFreeKVCache(pool)
+    dense = PagedKVCache(1, 1 << 30, page_positions=64)
+    outs = {}
+    for name, lo, hi in (("prefill", 0, T), ("decode", T, T + 1)):
+        shared.update_unrotated(0, k_store[:, :, lo:hi].cuda(), v[:, :, lo:hi].cuda())
+        dense.append(0, k_rot[:, :, lo:hi].cuda(), v[:, :, lo:hi].cuda())
+        qpos = torch.arange(lo, hi, dtype=torch.int32)
+        got = shared.paged_attention(0, q_rot[:, :, lo:hi].cuda(), qpos, theta=theta,
+                                     denominators=den, scale=scale)
+        if name == "prefill":
+            ref = dense.attend_prefill(0, q_rot[:, :, lo:hi].cuda(), scale)
+        else:
+            ref = dense.attend(0, q_rot[:, :, lo:hi].cuda(), scale)
+        torch.cuda.synchronize()
+        outs[name] = (got.float().cpu(), ref.float().cpu().reshape(got.shape))
+    assert shared.offset == dense.offset == T + 1
+    for name, (got, ref) in outs.items():
+        assert torch.allclose(got, ref, rtol=2e-2, atol=2e-2), \
+            f"{name}: max |diff| {float((got - ref).abs().max()):.4f}"
+    shared.release()
+    dense.release()
