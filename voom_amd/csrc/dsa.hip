@@ -128,8 +128,12 @@ __global__ __launch_bounds__(kScoreThreads) void dsa_scores_kernel(DsaScoreArgs 
 // ---------------------------------------------------------------- top-k ----
 
 constexpr int kTopkThreads = 1024;
-constexpr int kBinsPerThread = 2048 / kTopkThreads;
 constexpr int kTopkWaves = kTopkThreads / kWave;
+constexpr int kRadixBits = 12;                     // digit width of the radix select
+constexpr int kRadixBins = 1 << kRadixBits;
+constexpr int kBinsPerThread = kRadixBins / kTopkThreads;
+static_assert(kBinsPerThread == 4, "one int4 of histogram bins per thread");
+constexpr int kChunksPerThread = 2;                // select kernel: up to 2048 chunks
 
 // Order-preserving map of fp32 onto uint32: a > b  <=>  key(a) > key(b), and
 // -0 maps like +0 (they compare equal, so they tie).
@@ -165,51 +169,61 @@ constexpr int kChunkKeys = 4096; // keys per compaction workgroup
 
 // Radix select over `count` keys read by key(i): the rank-th largest key T
 // (rank >= 1) and how many keys equal to T belong to the top `rank` (kk).
-// The digits start below the leading bits that every key shares (from a
-// min/max reduction): scores of one row share their sign and most of their
-// exponent, and a first digit over those bits would send every key to a
-// handful of histogram bins, serialising the LDS atomics.  Passes of 11 bits
-// then walk down to bit 0; a thread adds runs of equal bins as one atomic.
-// Three barriers per pass: after the histogram; after each thread has
-// taken (and zeroed, for the next pass) its two bins and each wavefront has
-// left its scan total; after the thread holding the crossing has written it.
-// (Zeroing the histogram and the scan as separate steps cost six barriers a
-// pass, 5.5 k cycles; one wavefront scanning all 2048 bins hit 32-way LDS
-// bank conflicts.)
-// found[] holds the result, scan_tmp kTopkWaves ints; hist must hold 2048 ints.
+// The digits start below the leading bits that every key shares: scores of
+// one row share their sign and most of their exponent, and a first digit over
+// those bits would send every key to a handful of histogram bins, serialising
+// the LDS atomics.  The shared bits come from the keys' range [lo, hi], passed
+// in when the caller knows it (range_known) or found by a min/max reduction.
+// Passes of kRadixBits bits then walk down to bit 0 (or stop after
+// max_passes > 0 passes: T is then the lower edge of the crossing bin, a key
+// bound with at least `rank` keys at or above it, and kk is meaningless); a
+// thread adds runs of equal bins as one atomic.  Three barriers per pass:
+// after the histogram; after each thread has taken (and zeroed, for the next
+// pass) its int4 of bins and each wavefront has left its scan total; after
+// the thread holding the crossing has written it.  (Zeroing the histogram and
+// the scan as separate steps cost six barriers a pass, 5.5 k cycles; one
+// wavefront scanning every bin hit 32-way LDS bank conflicts.)
+// found[] holds the result, scan_tmp kTopkWaves ints; hist must hold
+// kRadixBins ints, 16-byte aligned.
 template <typename KeyFn>
 __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* scan_tmp, int* found,
+                             bool range_known, uint32_t lo_k, uint32_t hi_k, int max_passes,
                              uint32_t& T, int& kk_out) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
-  for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
-  if (tid == 0) {
-    found[0] = static_cast<int>(0xFFFFFFFFu);
-    found[1] = 0;
-  }
-  uint32_t lo_k = 0xFFFFFFFFu;
-  uint32_t hi_k = 0u;
-  for (int i = tid; i < count; i += kTopkThreads) {
-    const uint32_t u = key(i);
-    lo_k = u < lo_k ? u : lo_k;
-    hi_k = u > hi_k ? u : hi_k;
-  }
+  int4* hist4 = reinterpret_cast<int4*>(hist);
+  hist4[tid] = make_int4(0, 0, 0, 0);
+  if (range_known) {
+    __syncthreads();  // bins zero
+  } else {
+    if (tid == 0) {
+      found[0] = static_cast<int>(0xFFFFFFFFu);
+      found[1] = 0;
+    }
+    lo_k = 0xFFFFFFFFu;
+    hi_k = 0u;
+    for (int i = tid; i < count; i += kTopkThreads) {
+      const uint32_t u = key(i);
+      lo_k = u < lo_k ? u : lo_k;
+      hi_k = u > hi_k ? u : hi_k;
+    }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo_k), o));
-    const uint32_t b = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi_k), o));
-    lo_k = a < lo_k ? a : lo_k;
-    hi_k = b > hi_k ? b : hi_k;
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint32_t a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo_k), o));
+      const uint32_t b = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi_k), o));
+      lo_k = a < lo_k ? a : lo_k;
+      hi_k = b > hi_k ? b : hi_k;
+    }
+    __syncthreads();  // found[] and hist initialised
+    if (lane == 0) {
+      atomicMin(reinterpret_cast<unsigned int*>(&found[0]), lo_k);
+      atomicMax(reinterpret_cast<unsigned int*>(&found[1]), hi_k);
+    }
+    __syncthreads();
+    lo_k = static_cast<uint32_t>(found[0]);
+    hi_k = static_cast<uint32_t>(found[1]);
   }
-  __syncthreads();  // found[] and hist initialised
-  if (lane == 0) {
-    atomicMin(reinterpret_cast<unsigned int*>(&found[0]), lo_k);
-    atomicMax(reinterpret_cast<unsigned int*>(&found[1]), hi_k);
-  }
-  __syncthreads();
-  lo_k = static_cast<uint32_t>(found[0]);
-  hi_k = static_cast<uint32_t>(found[1]);
   // bits above `top` are common to every key
   int top = 31 - __clz(static_cast<int>(lo_k ^ hi_k));  // -1 when all keys are equal
   uint32_t prefix = top < 31 ? (hi_k & ~((2u << (top < 0 ? 0 : top)) - 1u)) : 0u;
@@ -217,9 +231,10 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
   uint32_t pmask = top < 31 ? ~((2u << (top < 0 ? 0 : top)) - 1u) : 0u;
   if (top < 0) pmask = 0xFFFFFFFFu;
   int kk = rank;
+  int passes = 0;
 #pragma unroll 1
-  while (top >= 0) {
-    const int width = top + 1 < 11 ? top + 1 : 11;
+  while (top >= 0 && (max_passes <= 0 || passes < max_passes)) {
+    const int width = top + 1 < kRadixBits ? top + 1 : kRadixBits;
     const int shift = top + 1 - width;
     const int bins = 1 << width;
     int run_bin = -1;
@@ -238,16 +253,14 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
     }
     if (run_n) atomicAdd(&hist[run_bin], run_n);
     __syncthreads();  // histogram complete (found[] of the previous pass read)
-    // thread t owns bins 2047 - (2 t + e), e < 2, in descending order
-    int c[kBinsPerThread];
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < kBinsPerThread; ++e) {
-      const int bin = 2047 - (kBinsPerThread * tid + e);
-      c[e] = hist[bin];
-      hist[bin] = 0;
-      mine += c[e];
-    }
+    // thread t owns the int4 of bins base .. base + 3, base = kRadixBins - 4 (t + 1),
+    // taken in descending order
+    const int q4 = kRadixBins / kBinsPerThread - 1 - tid;
+    const int4 h = hist4[q4];
+    hist4[q4] = make_int4(0, 0, 0, 0);
+    const int base = q4 * kBinsPerThread;
+    const int c[kBinsPerThread] = {h.w, h.z, h.y, h.x};
+    const int mine = h.x + h.y + h.z + h.w;
     const int inc = wave_inclusive_scan(mine, lane);
     if (lane == kWave - 1) scan_tmp[wv] = inc;
     __syncthreads();  // wave totals in scan_tmp, bins zero again
@@ -257,7 +270,7 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
 #pragma unroll
     for (int e = 0; e < kBinsPerThread; ++e) {
       if (run < kk && run + c[e] >= kk) {
-        found[0] = 2047 - (kBinsPerThread * tid + e);
+        found[0] = base + kBinsPerThread - 1 - e;
         found[1] = run;
       }
       run += c[e];
@@ -268,6 +281,7 @@ __device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* sca
     prefix |= static_cast<uint32_t>(d) << shift;
     pmask |= static_cast<uint32_t>(bins - 1) << shift;
     top = shift - 1;
+    ++passes;
   }
   __syncthreads();  // found[] read by every thread before anyone reuses it
   T = prefix;
@@ -324,10 +338,12 @@ __device__ void ordered_write(KeyFn key, IdxFn idx, int count, uint32_t T, int k
 }
 
 // Workspace of the top-k (per row): the threshold T0, per-chunk candidate
-// counts, and per-chunk candidate slots of (key, index) pairs.
+// counts and largest candidate keys, and per-chunk candidate slots of (key,
+// index) pairs.
 struct TopkWs {
   uint32_t* t0;     // [B]
   int* counts;      // [B, chunks]
+  uint32_t* cmax;   // [B, chunks]
   uint2* cand;      // [B, chunks, kChunkKeys]
   int chunks;
 };
@@ -342,19 +358,24 @@ __host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys -
 // kCandCap keys take every key as a candidate (T0 = 0).  Longer rows: T0 is
 // the key of rank 1.5 x (the sample's share of k) + 32 in a sample of kSample
 // keys (runs of 4 adjacent keys spread evenly over a 16-byte aligned row, else
-// single keys at an even stride), found exactly by the radix select in LDS --
-// about 1.5 k candidates, with margin, and no more than the sample's ties at
-// T0 allow.  (As separate launches, the one-workgroup threshold kernel took
-// 9.2 us and the compaction 5.0 us behind it.)
+// single keys at an even stride), placed by two passes of the radix select in
+// LDS: the lower edge of the bin (24 bits below the sample's shared leading
+// bits) that holds that rank -- about 1.5 k candidates, with margin.  Each
+// workgroup also records its candidates' largest key, which with T0 bounds
+// the select kernel's keys.  (As separate launches, the one-workgroup
+// threshold kernel took 9.2 us and the compaction 5.0 us behind it.)
 template <bool VEC>
 __global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
     const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
     int K) {
   __shared__ uint32_t sample[kSample];
-  __shared__ int hist[2048];
+  __shared__ __align__(16) int hist[kRadixBins];
   __shared__ int scan_tmp[kTopkWaves];
+  __shared__ uint32_t wave_max[kTopkWaves];
   __shared__ int found[2];
   const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
   const int b = blockIdx.y;
   const int chunk = blockIdx.x;
   int n = lens[b];
@@ -406,21 +427,42 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
     r = r + r / 2 + 32;
     const int want = static_cast<int>(r > kSample ? kSample : r);
     int unused;
-    radix_select([&](int k) { return sample[k]; }, kSample, want, hist, scan_tmp, found, T0,
-                 unused);
+    radix_select([&](int k) { return sample[k]; }, kSample, want, hist, scan_tmp, found,
+                 false, 0u, 0u, 2, T0, unused);
   }
   if (chunk == 0 && tid == 0) ws.t0[b] = T0;
 
   // keys >= T0 in index order: a scan over the workgroup places each thread's
+  // candidates; the same barrier collects the chunk's largest candidate key
   bool in[4];
   int cnt = 0;
+  uint32_t mx = 0u;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    in[e] = i + e < n && order_key(v[e]) >= T0;
+    const uint32_t u = order_key(v[e]);
+    in[e] = i + e < n && u >= T0;
     cnt += in[e] ? 1 : 0;
+    mx = in[e] && u > mx ? u : mx;
   }
-  int all;
-  int at = block_exclusive_scan(cnt, scan_tmp, all);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t y = static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), o));
+    mx = y > mx ? y : mx;
+  }
+  const int inc = wave_inclusive_scan(cnt, lane);
+  if (lane == kWave - 1) scan_tmp[wv] = inc;
+  if (lane == 0) wave_max[wv] = mx;
+  __syncthreads();
+  int at = inc - cnt;
+  int all = 0;
+  uint32_t cmax = 0u;
+#pragma unroll
+  for (int k = 0; k < kTopkWaves; ++k) {
+    const int t = scan_tmp[k];
+    at += k < wv ? t : 0;
+    all += t;
+    cmax = wave_max[k] > cmax ? wave_max[k] : cmax;
+  }
   uint2* slots = ws.cand + (static_cast<size_t>(b) * ws.chunks + chunk) * kChunkKeys;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -429,7 +471,10 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
       ++at;
     }
   }
-  if (tid == 0) ws.counts[static_cast<size_t>(b) * ws.chunks + chunk] = all;
+  if (tid == 0) {
+    ws.counts[static_cast<size_t>(b) * ws.chunks + chunk] = all;
+    ws.cmax[static_cast<size_t>(b) * ws.chunks + chunk] = cmax;
+  }
 }
 
 // 3. Select: one workgroup per row.  The chunks' candidates, in chunk order
@@ -442,13 +487,16 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
     int32_t* __restrict__ sel, int32_t* __restrict__ sel_lens, int cap, int K) {
   __shared__ uint32_t cand_key[kCandCap];
   __shared__ int32_t cand_idx[kCandCap];
-  __shared__ int hist[2048];
+  __shared__ __align__(16) int hist[kRadixBins];
   __shared__ int scan_tmp[kTopkWaves];
   __shared__ int found[2];
   __shared__ int wave_gt[kTopkWaves];
   __shared__ int wave_eq[kTopkWaves];
-  __shared__ int chunk_off[2049];
+  __shared__ uint32_t wave_max[kTopkWaves];
+  __shared__ int chunk_off[kChunksPerThread * kTopkThreads + 1];
   const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
   const int b = blockIdx.x;
   int n = lens[b];
   n = n < 0 ? 0 : (n > cap ? cap : n);
@@ -459,25 +507,37 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
     if (tid == 0) sel_lens[b] = n;
     return;
   }
-  // candidate offsets of the row's chunks (up to 2048 chunks in LDS)
+  // candidate offsets of the row's chunks (up to 2048 chunks in LDS), and the
+  // largest candidate key, which with T0 bounds every candidate
   const int nch = (n + kChunkKeys - 1) / kChunkKeys;
   const int* cnt = ws.counts + static_cast<size_t>(b) * ws.chunks;
+  const uint32_t* cmx = ws.cmax + static_cast<size_t>(b) * ws.chunks;
+  const uint32_t t0 = ws.t0[b];
   int C = 0;
-  bool fits = nch <= 2048;
+  bool fits = nch <= kChunksPerThread * kTopkThreads;
   if (fits) {
-    int c2[kBinsPerThread];
+    int c2[kChunksPerThread];
     int mine = 0;
+    uint32_t m2 = 0u;
 #pragma unroll
-    for (int e = 0; e < kBinsPerThread; ++e) {
-      const int ch = kBinsPerThread * tid + e;
+    for (int e = 0; e < kChunksPerThread; ++e) {
+      const int ch = kChunksPerThread * tid + e;
       c2[e] = ch < nch ? cnt[ch] : 0;
+      const uint32_t m = ch < nch ? cmx[ch] : 0u;
+      m2 = m > m2 ? m : m2;
       mine += c2[e];
     }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const uint32_t y = static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o));
+      m2 = y > m2 ? y : m2;
+    }
+    if (lane == 0) wave_max[wv] = m2;  // read after the scan's barriers
     int total;
     int run = block_exclusive_scan(mine, scan_tmp, total);
 #pragma unroll
-    for (int e = 0; e < kBinsPerThread; ++e) {
-      const int ch = kBinsPerThread * tid + e;
+    for (int e = 0; e < kChunksPerThread; ++e) {
+      const int ch = kChunksPerThread * tid + e;
       if (ch < nch) chunk_off[ch] = run;
       run += c2[e];
     }
@@ -516,13 +576,16 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
       }
     }
     __syncthreads();
+    uint32_t hi = 0u;
+#pragma unroll
+    for (int k = 0; k < kTopkWaves; ++k) hi = wave_max[k] > hi ? wave_max[k] : hi;
     auto lds_key = [&](int i) { return cand_key[i]; };
     auto lds_idx = [&](int i) { return cand_idx[i]; };
-    radix_select(lds_key, C, K, hist, scan_tmp, found, T, kk);
+    radix_select(lds_key, C, K, hist, scan_tmp, found, true, t0, hi, 0, T, kk);
     ordered_write(lds_key, lds_idx, C, T, kk, wave_gt, wave_eq, ob);
   } else {
     auto mem_key = [&](int i) { return order_key(sb[i]); };
-    radix_select(mem_key, n, K, hist, scan_tmp, found, T, kk);
+    radix_select(mem_key, n, K, hist, scan_tmp, found, false, 0u, 0u, 0, T, kk);
     ordered_write(mem_key, [](int i) { return i; }, n, T, kk, wave_gt, wave_eq, ob);
   }
   if (tid == 0) sel_lens[b] = K;
@@ -571,7 +634,7 @@ extern "C" size_t voom_dsa_topk_workspace_bytes(int batch, int cap) {
   if (batch <= 0 || cap <= 0) return 0;
   const size_t chunks = static_cast<size_t>(topk_chunks(cap));
   return ((static_cast<size_t>(batch) * 4 + 255) & ~size_t(255)) +
-         ((static_cast<size_t>(batch) * chunks * 4 + 255) & ~size_t(255)) +
+         2 * ((static_cast<size_t>(batch) * chunks * 4 + 255) & ~size_t(255)) +
          static_cast<size_t>(batch) * chunks * kChunkKeys * sizeof(uint2);
 }
 
@@ -590,10 +653,11 @@ extern "C" int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* 
   ws.chunks = topk_chunks(cap);
   char* p = static_cast<char*>(workspace);
   const size_t t0_bytes = (static_cast<size_t>(batch) * 4 + 255) & ~size_t(255);
+  const size_t per_chunk_bytes = (static_cast<size_t>(batch) * ws.chunks * 4 + 255) & ~size_t(255);
   ws.t0 = reinterpret_cast<uint32_t*>(p);
   ws.counts = reinterpret_cast<int*>(p + t0_bytes);
-  ws.cand = reinterpret_cast<uint2*>(
-      p + t0_bytes + ((static_cast<size_t>(batch) * ws.chunks * 4 + 255) & ~size_t(255)));
+  ws.cmax = reinterpret_cast<uint32_t*>(p + t0_bytes + per_chunk_bytes);
+  ws.cand = reinterpret_cast<uint2*>(p + t0_bytes + 2 * per_chunk_bytes);
   const bool vec = cap % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0;
   const dim3 cgrid(static_cast<unsigned>(ws.chunks), static_cast<unsigned>(batch));
   if (vec) {
