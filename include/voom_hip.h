@@ -60,7 +60,7 @@ int voom_abi_version(void);
  *            scores, or NULL.  Lets two calls over disjoint page sets be merged
  *            with voom_merge_attn_states.
  *   num_splits  number of wavefronts sharing the work (0 = library choice:
- *            a block table of at most 4096 tokens per sequence then runs one
+ *            a block table of at most 1024 tokens per sequence then runs one
  *            workgroup per (sequence, kv head) that merges its own waves and
  *            writes out directly -- one launch, workspace untouched; longer
  *            tables split-K over the default count); the workspace must hold

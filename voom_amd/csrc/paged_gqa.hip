@@ -787,9 +787,12 @@ int launch_partials(const GqaPlan& p, const void* q, const void* k_pool, const v
 }
 
 // Block tables of at most this many tokens per sequence use the one-launch
-// segment kernel when the caller leaves the split count to the library
-// (32 blocks per wavefront at most).
-constexpr long long kSegmentKernelTokens = 4096;
+// segment kernel when the caller leaves the split count to the library.  A
+// segment streams through one CU (about 39 GB/s), so its time grows by ~6.5 ns
+// per token at D = 64; measured against partials + combine at the default
+// split count for 3 to 384 segments, the segment kernel wins or ties at 1,024
+// tokens and loses from 1,536 (4,096 tokens, 3 segments: 29.7 against 12.9 us).
+constexpr long long kSegmentKernelTokens = 1024;
 // Wavefronts per segment workgroup.
 #ifndef VOOM_GQA_SEGMENT_WAVES
 #define VOOM_GQA_SEGMENT_WAVES 4
