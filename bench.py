@@ -36,6 +36,9 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+GRAPH_MIN_CALLS = 16
+
+
 def graph_seconds(calls, reps: int, rounds: int = 3) -> float:
     """Seconds per call of the launches in `calls` (a list of no-argument
     functions), captured once into a HIP graph and replayed `reps` times
@@ -44,10 +47,16 @@ def graph_seconds(calls, reps: int, rounds: int = 3) -> float:
     GPU runs at in a given moment).  Replaying keeps the GPU busy back to
     back, so the events measure the device, not the rate at which Python
     issues launches (which, for calls of a few tens of microseconds, is the
-    slower of the two).  Every call must already have run eagerly once, so its
-    workspaces exist."""
+    slower of the two).  The list is repeated in the graph up to at least
+    GRAPH_MIN_CALLS calls (and `reps` divided accordingly): the gap between
+    one replay and the next, about 17 us, would otherwise land on a few short
+    calls, while a decode loop's graph holds every layer's launches.  Every
+    call must already have run eagerly once, so its workspaces exist."""
     import torch
 
+    copies = -(-GRAPH_MIN_CALLS // len(calls))
+    calls = list(calls) * copies
+    reps = max(1, reps // copies)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
