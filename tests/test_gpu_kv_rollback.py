@@ -185,3 +185,47 @@ def test_prefetched_buffer_survives_a_spill_before_its_merge():
                                        atol=ATOL, rtol=RTOL)
     assert kv.prefetch_hits > 0
     kv.release()
+
+
+def test_repeated_spill_reload_cycles_hold_memory_steady():
+    """A serving loop spills and reloads the same cache again and again.  After
+    the first cycle, device memory, the pinned arena's capacity and its used
+    bytes are the same at the end of every cycle; attention over the spilled
+    pages (streamed in per call) repeats bit for bit and matches the oracle,
+    and after each reload it equals the all-resident result bit for bit."""
+    print("[kv] repeated spill/reload cycles", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    B, NKV, NQ, D, PT, L = 2, 4, 16, 128, 64, 2
+    kv = PagedKVCache(num_layers=L, max_bytes=1 << 40, page_positions=PT)
+    ks, vs = [], []
+    for layer in range(L):
+        k = randn_bf16((B, NKV, 5 * PT + 17, D), gen)
+        v = randn_bf16((B, NKV, 5 * PT + 17, D), gen)
+        kv.append(layer, k, v)
+        ks.append(k)
+        vs.append(v)
+    q = randn_bf16((B, NQ, 1, D), gen)
+    resident = [kv.attend(layer, q) for layer in range(L)]
+    torch.cuda.synchronize()
+    spilled_ref = None
+    marks = []
+    for cycle in range(6):
+        assert kv.spill([(layer, i) for layer in range(L) for i in range(4)]) == 4 * L
+        spilled = [kv.attend(layer, q) for layer in range(L)]
+        torch.cuda.synchronize()
+        if spilled_ref is None:
+            spilled_ref = spilled
+            for layer in range(L):
+                np.testing.assert_allclose(spilled[layer].float().cpu().numpy(),
+                                           oracle(q, ks[layer], vs[layer], D ** -0.5),
+                                           atol=ATOL, rtol=RTOL)
+        for a, b in zip(spilled, spilled_ref):
+            assert torch.equal(bits(a), bits(b)), f"cycle {cycle}: spilled attention changed"
+        assert kv.reload() == 4 * L
+        again = [kv.attend(layer, q) for layer in range(L)]
+        torch.cuda.synchronize()
+        for a, b in zip(again, resident):
+            assert torch.equal(bits(a), bits(b)), f"cycle {cycle}: reloaded attention changed"
+        marks.append((torch.cuda.memory_allocated(), kv.arena.capacity, kv.arena.used_bytes))
+    assert all(m == marks[1] for m in marks[1:]), marks
+    kv.release()
