@@ -229,3 +229,46 @@ def test_repeated_spill_reload_cycles_hold_memory_steady():
         marks.append((torch.cuda.memory_allocated(), kv.arena.capacity, kv.arena.used_bytes))
     assert all(m == marks[1] for m in marks[1:]), marks
     kv.release()
+
+
+@pytest.mark.parametrize("compress", [False, True])
+def test_repeated_latent_spill_reload_cycles_hold_memory_steady(compress):
+    """The same soak over a latent (absorbed-MLA) cache, with and without the
+    zstd high planes: steady device and pinned memory after the first cycle,
+    attend_mla bit-stable over spilled pages and bit-identical to the
+    all-resident result after each reload."""
+    from voom_amd import ops
+    print(f"[kv-latent] repeated spill/reload cycles compress={compress}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(22)
+    B, H, dn, dv, C, dr, PT = 2, 64, 128, 128, 512, 64, 64
+    kv_b = (torch.randn((H * (dn + dv), C), generator=gen, device="cuda") * C ** -0.5
+            ).to(torch.bfloat16)
+    w_uk, w_uv_t = ops.split_kv_b(kv_b, H, dn, dv)
+    w_uk, w_uv_t = ops.pack_head_weights(w_uk), ops.pack_head_weights(w_uv_t)
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, page_positions=PT,
+                      compress_spill=compress)
+    kv.append_latent(0, randn_bf16((B, 6 * PT + 5, C + dr), gen))
+    q_nope = randn_bf16((B, H, dn), gen)
+    q_rope = randn_bf16((B, H, dr), gen)
+    scale = (dn + dr) ** -0.5
+    resident = kv.attend_mla(0, q_nope, q_rope, w_uk, w_uv_t, scale)
+    torch.cuda.synchronize()
+    spilled_ref = None
+    marks = []
+    for cycle in range(5):
+        assert kv.spill([(0, i) for i in (0, 2, 3, 5)]) == 4
+        spilled = kv.attend_mla(0, q_nope, q_rope, w_uk, w_uv_t, scale)
+        torch.cuda.synchronize()
+        if spilled_ref is None:
+            spilled_ref = spilled
+            np.testing.assert_allclose(spilled.float().cpu().numpy(),
+                                       resident.float().cpu().numpy(), atol=ATOL, rtol=RTOL)
+        assert torch.equal(bits(spilled), bits(spilled_ref)), f"cycle {cycle}"
+        assert kv.reload() == 4
+        again = kv.attend_mla(0, q_nope, q_rope, w_uk, w_uv_t, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(again), bits(resident)), f"cycle {cycle}"
+        kv._wait_host_work()  # background zstd jobs of this cycle
+        marks.append((torch.cuda.memory_allocated(), kv.arena.capacity, kv.arena.used_bytes))
+    assert all(m == marks[1] for m in marks[1:]), marks
+    kv.release()
