@@ -41,7 +41,8 @@ extern "C" {
 const char* voom_last_error(void);
 
 /* ABI version, bumped on any signature or layout change (2: checksums in the
- * slot codec; 3: spill-record calls). */
+ * slot codec; 3: spill-record calls; 4: element and table types of the
+ * position-free call). */
 int voom_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -250,31 +251,75 @@ int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* sel, int32_
  * Position-free paged attention (keys stored before RoPE).
  *
  * Replaces position_free_paged_attention and its Metal kernel
- * (runtime/pic_attention.py:22-232): pages hold unrotated K and ordinary V,
- * [num_pages, num_kv_heads, block_size, head_dim] each; block_table
- * [ceil(num_keys / block_size)] int32 maps the logical keys (shared by all
- * batch rows; repeating a page id is legal and is how pages are shared);
- * key k is rotated at key_positions[k] with the fp32 NeoX tables
- * cos/sin [max_position, head_dim/2], rounded to bf16, and attended by query
- * tq iff key_positions[k] <= query_positions[tq].
- *   q    [batch, num_q_heads, num_queries, head_dim] bf16, already rotated
- *   out  same shape, bf16; rows with no visible key are zeros
- * head_dim in {64, 128}; (num_q_heads / num_kv_heads) * num_queries <= 16.
- * num_splits splits each (batch, kv head)'s keys over wavefronts (0 = library
+ * (runtime/pic_attention.py:22-232), with the same accepted inputs: pages
+ * hold unrotated K and ordinary V, [num_pages, num_kv_heads, block_size,
+ * head_dim] each; block_table [ceil(num_keys / block_size)] int32 maps the
+ * logical keys (shared by all batch rows; repeating a page id is legal and is
+ * how pages are shared); key k is rotated at key_positions[k] with the NeoX
+ * tables cos/sin [max_position, head_dim/2] in fp32, rounded to the element
+ * type, and attended by query tq iff key_positions[k] <= query_positions[tq].
+ *   q    [batch, num_q_heads, num_queries, head_dim], already rotated
+ *   out  same shape; rows with no visible key are zeros
+ * dtype: the element type of q, the pages and out (VOOM_DTYPE_BF16, _F16 or
+ * _F32; the reference's T).  table_dtype: VOOM_DTYPE_F32 or dtype (the
+ * reference's "FP32 or match the Q/K/V dtype", :210-211).  head_dim a
+ * multiple of 32 up to 256 (the reference: any multiple of 32); any query
+ * count and any num_q_heads / num_kv_heads.  bf16 at head_dim 64 or 128 runs
+ * on MFMA; other element types and head dims on an fp32 VALU kernel.
+ * num_splits splits each (batch, kv head)'s keys over workgroups (0 = library
  * default); the workspace must hold voom_position_free_workspace_bytes(...)
  * for the same values.  Page ids outside [0, num_pages) read page 0 and
- * positions are clamped to [0, max_position); callers validate them.
+ * table rows are read at positions clamped to [0, max_position); callers
+ * validate them (voom_check_position_free_pages does, see below).
  * ------------------------------------------------------------------------- */
-size_t voom_position_free_workspace_bytes(int batch, int num_kv_heads, int head_dim,
-                                          int num_keys, int num_splits);
+#define VOOM_DTYPE_BF16 0
+#define VOOM_DTYPE_F16 1
+#define VOOM_DTYPE_F32 2
+size_t voom_position_free_workspace_bytes(int batch, int num_q_heads, int num_queries,
+                                          int num_kv_heads, int head_dim, int num_keys,
+                                          int dtype, int num_splits);
 int voom_position_free_attention(const void* q, const void* k_pages, const void* v_pages,
                                  const int32_t* block_table, const int32_t* key_positions,
-                                 const int32_t* query_positions, const float* cos_table,
-                                 const float* sin_table, void* out, void* workspace,
+                                 const int32_t* query_positions, const void* cos_table,
+                                 const void* sin_table, void* out, void* workspace,
                                  size_t ws_bytes, int batch, int num_q_heads, int num_queries,
                                  int num_kv_heads, int head_dim, int block_size, int num_pages,
-                                 int num_keys, int max_position, float scale, int num_splits,
-                                 hipStream_t stream);
+                                 int num_keys, int max_position, int dtype, int table_dtype,
+                                 float scale, int num_splits, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Debug bounds checks of the attention calls' index arrays.
+ *
+ * The attention kernels never fault on a bad index (a slot or page id out of
+ * range reads slot 0; a position outside the RoPE tables is clamped), so a
+ * caller's bug would give plausible numbers.  The reference raises instead:
+ * IndexError/ValueError from its page pool (runtime/kv_cache.py:305-310,
+ * 357-476) and ValueError from the kernel wrapper (runtime/pic_attention.py:
+ * 197-213).  These calls count, into the caller-zeroed int32 status[4], what
+ * the matching attention call would read out of range; the host layer raises
+ * ValueError on a non-zero count.  Each is one launch; nothing traps.
+ *   voom_check_block_table           for voom_paged_gqa_* and the dense MLA
+ *       calls: status[0] += slot ids outside [0, num_slots) among the first
+ *       ceil(ctx_lens[b] / page_tokens) columns of row b (a spilled
+ *       column's -1 included); status[1] += ctx_lens outside
+ *       [0, max_pages * page_tokens].
+ *   voom_check_selection             for voom_mla_sparse_decode: status[0] +=
+ *       slot ids outside [0, num_slots) read by a used position; status[2] +=
+ *       used positions outside [0, max_pages * page_tokens); status[3] +=
+ *       sel_lens outside [0, k].
+ *   voom_check_position_free_pages   for voom_position_free_attention:
+ *       status[0] += keys whose page id lies outside [0, num_pages);
+ *       status[1] += key positions outside [0, max_position).
+ * ------------------------------------------------------------------------- */
+int voom_check_block_table(const int32_t* block_table, const int32_t* ctx_lens,
+                           int32_t* status, int batch, int max_pages, int page_tokens,
+                           int num_slots, hipStream_t stream);
+int voom_check_selection(const int32_t* sel, const int32_t* sel_lens, const int32_t* block_table,
+                         int32_t* status, int batch, int k, int max_pages, int page_tokens,
+                         int num_slots, hipStream_t stream);
+int voom_check_position_free_pages(const int32_t* block_table, const int32_t* key_positions,
+                                   int32_t* status, int num_keys, int block_size, int num_pages,
+                                   int max_position, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Decoder-block ops of the end-to-end decode harness (all bf16, memory-bound).

@@ -3,7 +3,8 @@
 Follows runtime/pic_attention.py:
   rope_tables      :150-167  angles = position / theta^(i / half), fp32
   rotate           :68-90    NeoX rotate-half of the stored key at its
-                             logical position, fp32, then rounded to bf16
+                             logical position, fp32, then rounded to the
+                             page element type T (bf16, fp16 or fp32)
   attention        :44-128   q * scale in fp32, visible iff key position <=
                              query position, softmax, zeros when nothing is
                              visible; page row ((blk * NKV + kvh) * BLOCK + off)
@@ -23,22 +24,42 @@ def rope_tables(max_position: int, head_dim: int, theta: float):
     return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
 
 
+def _store(x: np.ndarray, store: str) -> np.ndarray:
+    """x after a round trip through the page element type T."""
+    if store == "bf16":
+        return round_bf16(x)
+    if store == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    if store == "f32":
+        return x.astype(np.float32)
+    raise ValueError(f"unknown element type {store}")
+
+
 def rotate(k: np.ndarray, positions: np.ndarray, cos: np.ndarray, sin: np.ndarray, *,
-           bf16: bool = True) -> np.ndarray:
-    """Rotate rows k [..., N, D] at positions [N] (rotate-half)."""
+           bf16: bool = True, store: str | None = None) -> np.ndarray:
+    """Rotate rows k [..., N, D] at positions [N] (rotate-half) in fp32, then
+    round to the element type T (``store``: "bf16", "f16" or "f32"; default
+    "bf16" when ``bf16`` else "f32"), as pic_attention.py:81-90 does."""
+    store = store or ("bf16" if bf16 else "f32")
     half = k.shape[-1] // 2
-    c = cos[positions]
-    s = sin[positions]
+    c = np.asarray(cos, dtype=np.float32)[positions]
+    s = np.asarray(sin, dtype=np.float32)[positions]
     a = k[..., :half].astype(np.float32)
     b = k[..., half:].astype(np.float32)
     out = np.concatenate([a * c - b * s, b * c + a * s], axis=-1).astype(np.float32)
-    return round_bf16(out) if bf16 else out
+    return _store(out, store)
 
 
 def attention(q: np.ndarray, k_pages: np.ndarray, v_pages: np.ndarray, block_table: np.ndarray,
               key_positions: np.ndarray, query_positions: np.ndarray, cos: np.ndarray,
-              sin: np.ndarray, scale: float, *, bf16: bool = True) -> np.ndarray:
-    """Output [B, NQ, TQ, D] in fp32 (before the final bf16 store)."""
+              sin: np.ndarray, scale: float, *, bf16: bool = True, store: str | None = None,
+              acc=np.float32) -> np.ndarray:
+    """Output [B, NQ, TQ, D] in fp32 (before the final store in T).
+
+    ``store`` is the element type the rotated keys are rounded to (see
+    rotate); ``acc`` the type the scores, softmax and P.V are computed in
+    (np.float64 gives an fp64 reference for fp32 pages)."""
+    store = store or ("bf16" if bf16 else "f32")
     B, NQ, TQ, D = q.shape
     _, NKV, BLOCK, _ = k_pages.shape
     G = NQ // NKV
@@ -49,12 +70,12 @@ def attention(q: np.ndarray, k_pages: np.ndarray, v_pages: np.ndarray, block_tab
     out = np.zeros((B, NQ, TQ, D), dtype=np.float32)
     for kvh in range(NKV):
         k_rows = k_pages[pages, kvh, offs].astype(np.float32)     # [TK, D]
-        v_rows = v_pages[pages, kvh, offs].astype(np.float32)
-        k_rot = rotate(k_rows, key_positions, cos, sin, bf16=bf16)
+        v_rows = v_pages[pages, kvh, offs].astype(acc)
+        k_rot = rotate(k_rows, key_positions, cos, sin, store=store).astype(acc)
         for b in range(B):
             for j in range(G):
                 h = kvh * G + j
-                qv = q[b, h].astype(np.float32) * np.float32(scale)  # [TQ, D]
+                qv = q[b, h].astype(acc) * acc(scale)                 # [TQ, D]
                 s = qv @ k_rot.T                                      # [TQ, TK]
                 vis = key_positions[None, :] <= query_positions[:, None]
                 s = np.where(vis, s, -np.inf)

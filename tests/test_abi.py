@@ -44,7 +44,7 @@ def test_binding_covers_every_declared_symbol():
 
 def test_abi_version_and_workspace_query():
     lib = _lib.lib()
-    assert lib.voom_abi_version() == 3
+    assert lib.voom_abi_version() == 4
     assert lib.voom_paged_gqa_workspace_bytes(16, 32, 8, 128, 2048) > 0
     assert lib.voom_paged_gqa_workspace_bytes(0, 32, 8, 128, 2048) == 0
 

@@ -13,14 +13,18 @@ pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-2, 1e-2
 
 
+STORE = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
 def run(B, NQ, NKV, TQ, D, BLOCK, TK, P, *, seed, kpos=None, qpos=None, table=None,
-        num_splits=0, max_pos=None):
+        num_splits=0, max_pos=None, dtype=torch.bfloat16, table_dtype=torch.float32,
+        scale_in=1.0, atol=ATOL, rtol=RTOL):
     print(f"[pf] B={B} NQ={NQ} NKV={NKV} TQ={TQ} D={D} BLOCK={BLOCK} TK={TK} P={P} "
-          f"splits={num_splits}", flush=True)
+          f"splits={num_splits} dtype={dtype} tables={table_dtype}", flush=True)
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn((B, NQ, TQ, D), generator=g).to(torch.bfloat16)
-    kp = torch.randn((P, NKV, BLOCK, D), generator=g).to(torch.bfloat16)
-    vp = torch.randn((P, NKV, BLOCK, D), generator=g).to(torch.bfloat16)
+    q = (torch.randn((B, NQ, TQ, D), generator=g) * scale_in).to(dtype)
+    kp = (torch.randn((P, NKV, BLOCK, D), generator=g) * scale_in).to(dtype)
+    vp = (torch.randn((P, NKV, BLOCK, D), generator=g) * scale_in).to(dtype)
     nblk = (TK + BLOCK - 1) // BLOCK
     if table is None:
         table = torch.randint(0, P, (nblk,), generator=g, dtype=torch.int32)
@@ -30,15 +34,19 @@ def run(B, NQ, NKV, TQ, D, BLOCK, TK, P, *, seed, kpos=None, qpos=None, table=No
         qpos = torch.arange(TK - TQ, TK, dtype=torch.int32).clamp(min=0)
     max_pos = max_pos or max(int(kpos.max()) + 1 if TK else 1, int(qpos.max()) + 1)
     cos, sin = ops.rope_cache(max_pos, D, 10000.0, device="cuda")
+    cos, sin = cos.to(table_dtype), sin.to(table_dtype)
     out = ops.position_free_paged_attention(
         q.cuda(), kp.cuda(), vp.cuda(), table.cuda(), kpos.cuda(), qpos.cuda(), cos, sin,
         scale=D ** -0.5, num_splits=num_splits)
     torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == q.shape
+    f64 = dtype == torch.float32
     ref = opf.attention(q.float().numpy(), kp.float().numpy(), vp.float().numpy(),
                         table.numpy().astype(np.int64), kpos.numpy().astype(np.int64),
-                        qpos.numpy().astype(np.int64), cos.cpu().numpy(), sin.cpu().numpy(),
-                        D ** -0.5)
-    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+                        qpos.numpy().astype(np.int64), cos.float().cpu().numpy(),
+                        sin.float().cpu().numpy(), D ** -0.5, store=STORE[dtype],
+                        acc=np.float64 if f64 else np.float32)
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=atol, rtol=rtol)
     return out
 
 
@@ -74,6 +82,98 @@ def test_nothing_visible_and_empty_key_set():
     assert torch.all(out == 0)
     out = run(1, 4, 2, 1, 64, 4, 0, 3, seed=6, qpos=torch.tensor([5], dtype=torch.int32))
     assert torch.all(out == 0)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.bfloat16, 64),
+                                     (torch.bfloat16, 128), (torch.float16, 64)])
+def test_reference_geometry_across_element_types(dtype, D):
+    """tests/test_pic_attention.py:11-49: B=1, 4q/2kv, 3 queries at positions
+    16..18, 19 keys in 4-key pages, RoPE tables of 32 positions in the element
+    type (fp32 for fp32), inputs N(0, 0.1).  Bar: 2e-5 for fp32 (here against
+    the fp64 oracle), 2e-2 for bf16 (the reference's), 2e-3 for fp16."""
+    tol = {torch.float32: 2e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3}[dtype]
+    run(1, 4, 2, 3, D, 4, 19, 5, seed=713, table=torch.arange(5, dtype=torch.int32),
+        qpos=torch.tensor([16, 17, 18], dtype=torch.int32), max_pos=32, dtype=dtype,
+        table_dtype=dtype, scale_in=0.1, atol=tol, rtol=tol)
+
+
+def test_reference_shared_page_at_two_positions_fp32():
+    """tests/test_pic_attention.py:52-81: pages A, B, A (table [0, 1, 0]) of 4
+    keys, 2 q / 2 kv heads, D = 64, one query at position 11, fp32 pages and
+    tables; 2e-5 against the fp64 oracle."""
+    run(1, 2, 2, 1, 64, 4, 12, 2, seed=19, table=torch.tensor([0, 1, 0], dtype=torch.int32),
+        qpos=torch.tensor([11], dtype=torch.int32), max_pos=16, dtype=torch.float32,
+        scale_in=0.1, atol=2e-5, rtol=2e-5)
+
+
+@pytest.mark.parametrize("NQ,NKV,TQ", [(28, 4, 3), (28, 4, 4), (64, 8, 4), (16, 1, 4),
+                                       (48, 1, 2)])
+def test_column_passes_for_large_groups(NQ, NKV, TQ):
+    """More (head, query) columns than one MFMA tile holds: Qwen2.5-7B's 28q/4kv
+    at 3- and 4-token verify windows (the reference's position-free gate model,
+    runtime/kv_cache.py:566 allows 4 queries), 64q/8kv at 4, and groups of 16
+    and 48 (2 to 6 passes)."""
+    run(1, NQ, NKV, TQ, 128, 16, 700, 60, seed=31 + NQ + TQ)
+
+
+def test_column_passes_with_batch_and_splits():
+    run(3, 64, 8, 4, 128, 8, 333, 50, seed=41, num_splits=5)
+    run(2, 28, 4, 4, 64, 1, 257, 300, seed=42, num_splits=2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("NQ,NKV,TQ", [(4, 2, 3), (28, 4, 4), (16, 1, 4)])
+def test_fp32_and_fp16_pages(dtype, NQ, NKV, TQ):
+    tol = 2e-5 if dtype == torch.float32 else 2e-3
+    run(2, NQ, NKV, TQ, 128, 16, 450, 40, seed=51, dtype=dtype, scale_in=0.3, atol=tol,
+        rtol=tol)
+
+
+@pytest.mark.parametrize("D", [32, 96, 160, 256])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_other_head_dims(D, dtype):
+    """Head dims the MFMA kernel does not take (any multiple of 32 up to 256);
+    256 at 16 columns asks for 85 KB of LDS."""
+    tol = 2e-5 if dtype == torch.float32 else 2e-2
+    run(1, 16, 2, 2, D, 8, 300, 50, seed=61 + D, dtype=dtype, scale_in=0.3, atol=tol,
+        rtol=tol if dtype == torch.float32 else RTOL)
+
+
+def test_bf16_tables_on_the_mfma_kernel():
+    run(2, 8, 2, 2, 128, 16, 600, 50, seed=71, table_dtype=torch.bfloat16)
+    run(1, 28, 4, 4, 64, 4, 200, 60, seed=72, table_dtype=torch.bfloat16)
+
+
+def test_int64_indices_are_accepted():
+    """The reference casts the table and positions to int32
+    (runtime/pic_attention.py:223-224)."""
+    g = torch.Generator().manual_seed(81)
+    q = torch.randn((1, 4, 1, 64), generator=g).to(torch.bfloat16).cuda()
+    kp = torch.randn((6, 2, 4, 64), generator=g).to(torch.bfloat16).cuda()
+    cos, sin = ops.rope_cache(24, 64, 1e4, device="cuda")
+    t32 = torch.tensor([3, 1, 4, 0, 5], dtype=torch.int32, device="cuda")
+    k32 = torch.arange(20, dtype=torch.int32, device="cuda")
+    q32 = torch.tensor([19], dtype=torch.int32, device="cuda")
+    a = ops.position_free_paged_attention(q, kp, kp, t32, k32, q32, cos, sin, scale=0.125)
+    b = ops.position_free_paged_attention(q, kp, kp, t32.long(), k32.long(), q32.long(), cos,
+                                          sin, scale=0.125)
+    assert torch.equal(a, b)
+
+
+def test_dtype_and_table_errors_match_the_reference():
+    q = torch.zeros((1, 4, 1, 64), dtype=torch.bfloat16, device="cuda")
+    kp = torch.zeros((3, 2, 4, 64), dtype=torch.bfloat16, device="cuda")
+    cos, sin = ops.rope_cache(16, 64, 1e4, device="cuda")
+    i32 = lambda *v: torch.tensor(v, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="dtypes must match"):
+        ops.position_free_paged_attention(q, kp.float(), kp.float(), i32(0), i32(0), i32(0),
+                                          cos, sin, scale=1.0)
+    with pytest.raises(ValueError, match="RoPE cache must be FP32 or match"):
+        ops.position_free_paged_attention(q, kp, kp, i32(0), i32(0), i32(0), cos.half(),
+                                          sin.half(), scale=1.0)
+    with pytest.raises(ValueError, match="RoPE cache must be FP32 or match"):
+        ops.position_free_paged_attention(q, kp, kp, i32(0), i32(0), i32(0), cos, sin.bfloat16(),
+                                          scale=1.0)
 
 
 def test_validation_matches_the_reference_errors():

@@ -105,3 +105,48 @@ def test_all_visible_is_softmax_attention_over_rotated_keys():
             qq = q[b, 2 * kvh:2 * kvh + 2, 0].astype(np.float64)
             ref = opa.sdpa_decode(qq, kr[None], vrow[None].astype(np.float64), 0.125)
             np.testing.assert_allclose(out[b, 2 * kvh:2 * kvh + 2, 0], ref, atol=1e-5)
+
+
+def test_fp64_accumulation_matches_a_complex_rotation_brute_force():
+    """store="f32", acc=float64 (the reference for fp32 pages) against an
+    independent fp64 computation: keys rotated by complex multiplication,
+    masked softmax by explicit loops."""
+    rng = np.random.default_rng(5)
+    q, kp, vp, table = _case(rng, B=1, NQ=4, NKV=2, TQ=3, D=64, BLOCK=4, TK=19, P=5)
+    cos, sin = pf.rope_tables(32, 64, 10000.0)
+    kpos = np.arange(19)
+    qpos = np.array([5, 17, 18])
+    out = pf.attention(q, kp, vp, table, kpos, qpos, cos, sin, 0.125, store="f32",
+                       acc=np.float64)
+    for h in range(4):
+        kvh = h // 2
+        for t in range(3):
+            num = np.zeros(64)
+            den = 0.0
+            scores = []
+            for key in range(19):
+                if kpos[key] > qpos[t]:
+                    continue
+                krow = kp[table[key // 4], kvh, key % 4].astype(np.float64)
+                z = (krow[:32] + 1j * krow[32:]) * np.exp(1j * np.arctan2(
+                    sin[kpos[key]].astype(np.float64), cos[kpos[key]].astype(np.float64)))
+                kr = np.concatenate([z.real, z.imag])
+                scores.append((float(q[0, h, t].astype(np.float64) @ kr) * 0.125, key))
+            m = max(s for s, _ in scores)
+            for s, key in scores:
+                w = np.exp(s - m)
+                num += w * vp[table[key // 4], kvh, key % 4].astype(np.float64)
+                den += w
+            np.testing.assert_allclose(out[0, h, t], num / den, atol=2e-6)
+
+
+def test_half_store_rounds_the_rotated_keys_to_fp16():
+    rng = np.random.default_rng(6)
+    cos, sin = pf.rope_tables(50, 64, 10000.0)
+    k = rng.standard_normal((7, 64)).astype(np.float32)
+    pos = np.arange(40, 47)
+    full = pf.rotate(k, pos, cos, sin, store="f32")
+    half = pf.rotate(k, pos, cos, sin, store="f16")
+    assert np.array_equal(half, half.astype(np.float16).astype(np.float32))  # representable
+    assert np.all(np.abs(half - full) <= np.abs(full) * 2.0 ** -11 + 2.0 ** -25)
+    assert not np.array_equal(half, full)

@@ -10,6 +10,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -41,19 +43,38 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every kernel source into one shared library and return its path."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, sources())]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+    return err
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel source into one shared library and return its path.
+
+    Each source is compiled to an object in its own hipcc process (in
+    parallel; every translation unit holds its kernels and their launchers,
+    so no relocatable device code is needed), then the objects are linked."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cc = hipcc()
+    jobs = max(1, min(len(sources()), int(os.environ.get("MAX_JOBS", "") or os.cpu_count() or 1)))
+    with tempfile.TemporaryDirectory(prefix="voom_build_") as tdir:
+        objs = [Path(tdir) / (src.name + ".o") for src in sources()]
+        cmds = [[cc, *HIP_FLAGS, "-c", "-o", str(obj), str(src)]
+                for src, obj in zip(sources(), objs)]
+        if verbose:
+            for cmd in cmds:
+                print(" ".join(cmd), flush=True)
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            errs = list(pool.map(_run, cmds))
+        errs.append(_run([cc, *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, objs)]))
+    if verbose:
+        for err in errs:
+            if err.strip():
+                print(err, file=sys.stderr)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -68,10 +68,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                     _P]),
     "voom_add_rms_norm_gemv": (c_int, [_P, _P, _P, c_float, _P, _P, _P, c_int, c_int, c_int,
                                        _P]),
-    "voom_position_free_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "voom_position_free_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int,
+                                                      c_int, c_int]),
     "voom_position_free_attention": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_size_t,
                                              c_int, c_int, c_int, c_int, c_int, c_int, c_int,
-                                             c_int, c_int, c_float, c_int, _P]),
+                                             c_int, c_int, c_int, c_int, c_float, c_int, _P]),
+    "voom_check_block_table": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, _P]),
+    "voom_check_selection": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, _P]),
+    "voom_check_position_free_pages": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, _P]),
     "voom_append_kv": (c_int, [_P, _P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int,
                                c_int, c_int, _P]),
     "voom_gather_kv": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int,

@@ -14,6 +14,7 @@ Pool layouts (per layer):
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -58,6 +59,86 @@ def workspace(device: torch.device, nbytes: int, tag: int = 0) -> torch.Tensor:
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+# ---- debug bounds checks ------------------------------------------------------
+# Off by default (each check costs a launch and a host synchronisation).  When
+# on, every attention call first counts the slot / page ids and positions its
+# kernel would read out of range and raises ValueError instead of attending:
+# the kernels themselves read slot 0 for a bad id and clamp a bad position.
+_BOUNDS_CHECKS = os.environ.get("VOOM_BOUNDS_CHECK", "") not in ("", "0")
+
+
+def set_bounds_checks(enabled: bool) -> None:
+    """Turn the debug bounds checks of the attention calls on or off (also
+    VOOM_BOUNDS_CHECK=1 in the environment)."""
+    global _BOUNDS_CHECKS
+    _BOUNDS_CHECKS = bool(enabled)
+
+
+def bounds_checks_enabled() -> bool:
+    return _BOUNDS_CHECKS
+
+
+def check_block_table(block_table: torch.Tensor, ctx_lens: torch.Tensor, num_slots: int,
+                      page_tokens: int, *, stream: torch.cuda.Stream | None = None) -> None:
+    """Raise ValueError if a slot id inside some sequence's context lies outside
+    [0, num_slots) (a spilled column's -1 included) or a context length does
+    not fit the table."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("bounds checks synchronise and cannot run under graph capture")
+    B, max_pages = block_table.shape
+    status = torch.zeros(4, dtype=torch.int32, device=block_table.device)
+    _lib.call("voom_check_block_table", _ptr(block_table), _ptr(ctx_lens), _ptr(status), B,
+              max_pages, int(page_tokens), int(num_slots), _stream(stream))
+    bad = status.cpu().tolist()
+    if bad[1]:
+        raise ValueError(f"{bad[1]} context lengths lie outside [0, {max_pages * page_tokens}]")
+    if bad[0]:
+        raise ValueError(f"block table holds {bad[0]} slot ids outside [0, {num_slots}) "
+                         "inside the context")
+
+
+def check_selection(sel: torch.Tensor, sel_lens: torch.Tensor, block_table: torch.Tensor,
+                    num_slots: int, page_tokens: int, *,
+                    stream: torch.cuda.Stream | None = None) -> None:
+    """Raise ValueError if a used selected position lies outside the block
+    table, reads a slot id outside [0, num_slots), or a selection count lies
+    outside [0, k]."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("bounds checks synchronise and cannot run under graph capture")
+    B, k = sel.shape
+    max_pages = block_table.shape[1]
+    status = torch.zeros(4, dtype=torch.int32, device=sel.device)
+    _lib.call("voom_check_selection", _ptr(sel), _ptr(sel_lens), _ptr(block_table),
+              _ptr(status), B, k, max_pages, int(page_tokens), int(num_slots), _stream(stream))
+    bad = status.cpu().tolist()
+    if bad[3]:
+        raise ValueError(f"{bad[3]} selection counts lie outside [0, {k}]")
+    if bad[2]:
+        raise ValueError(f"selection holds {bad[2]} positions outside the block table")
+    if bad[0]:
+        raise ValueError(f"selection reads {bad[0]} slot ids outside [0, {num_slots})")
+
+
+def check_position_free_pages(block_table: torch.Tensor, key_positions: torch.Tensor,
+                              block_size: int, num_pages: int, max_position: int,
+                              *, stream: torch.cuda.Stream | None = None) -> None:
+    """Raise ValueError if a key's page id lies outside [0, num_pages) or a key
+    position outside the RoPE cache [0, max_position)."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("bounds checks synchronise and cannot run under graph capture")
+    TK = key_positions.numel()
+    if TK == 0:
+        return
+    status = torch.zeros(4, dtype=torch.int32, device=key_positions.device)
+    _lib.call("voom_check_position_free_pages", _ptr(block_table), _ptr(key_positions),
+              _ptr(status), TK, int(block_size), int(num_pages), int(max_position), _stream(stream))
+    bad = status.cpu().tolist()
+    if bad[0]:
+        raise ValueError(f"block table holds {bad[0]} page ids outside [0, {num_pages})")
+    if bad[1]:
+        raise ValueError(f"{bad[1]} key positions lie outside the RoPE cache [0, {max_position})")
 
 
 def default_splits() -> int:
@@ -127,6 +208,8 @@ def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     q_shape = q.shape
     q, (B, NQ, NKV, D, PT, max_pages, slots), scale, num_splits, ws, need = _gqa_plan(
         q, k_pool, v_pool, block_table, ctx_lens, out, scale, num_splits, ws)
+    if _BOUNDS_CHECKS:
+        check_block_table(block_table, ctx_lens, slots, PT, stream=stream)
     if out is None:
         out = torch.empty((B, NQ, D), dtype=torch.bfloat16, device=q.device)
     lse = torch.empty((B, NQ), dtype=torch.float32, device=q.device) if return_lse else None
@@ -489,6 +572,8 @@ def mla_latent_decode(q_lat: torch.Tensor, lat_pool: torch.Tensor, block_table: 
              "block_table and ctx_lens must be int32")
     _require(block_table.dim() == 2 and block_table.shape[0] == B and tuple(ctx_lens.shape) == (B,),
              "block_table [B, max_pages], ctx_lens [B]")
+    if _BOUNDS_CHECKS:
+        check_block_table(block_table, ctx_lens, slots, PT, stream=stream)
     need = mla_workspace_bytes(B, H, num_ranges)
     if ws is None:
         ws = workspace(dev, need, tag=2)
@@ -525,6 +610,8 @@ def mla_sparse_decode(q_lat: torch.Tensor, lat_pool: torch.Tensor, block_table: 
     _require(block_table.dim() == 2 and block_table.shape[0] == B and sel.dim() == 2
              and sel.shape[0] == B and tuple(sel_lens.shape) == (B,),
              "block_table [B, max_pages], sel [B, k], sel_lens [B]")
+    if _BOUNDS_CHECKS:
+        check_selection(sel, sel_lens, block_table, slots, PT, stream=stream)
     need = int(_lib.lib().voom_mla_sparse_workspace_bytes(B, H, sel.shape[1], int(num_ranges)))
     if ws is None:
         ws = workspace(dev, need, tag=2)
@@ -866,6 +953,8 @@ def mla_latent_decode_project(q_lat: torch.Tensor, lat_pool: torch.Tensor,
     w_uv = pack_head_weights(w_uv_t, stream=stream)
     _require(w_uv.packed.device == dev and w_uv.heads == H and w_uv.k == 512,
              "W_UV^T must be [H, 512, dv]")
+    if _BOUNDS_CHECKS:
+        check_block_table(block_table, ctx_lens, slots, PT, stream=stream)
     need = mla_workspace_bytes(B, H, num_ranges)
     if ws is None:
         ws = workspace(dev, need, tag=2)
@@ -953,10 +1042,26 @@ def rope_cache(max_position: int, head_dim: int, theta: float, *,
     return torch.cos(angles).contiguous(), torch.sin(angles).contiguous()
 
 
-def position_free_workspace_bytes(batch: int, num_kv_heads: int, head_dim: int, num_keys: int,
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}  # VOOM_DTYPE_*
+
+
+def position_free_workspace_bytes(batch: int, num_q_heads: int, num_queries: int,
+                                  num_kv_heads: int, head_dim: int, num_keys: int,
+                                  dtype: torch.dtype = torch.bfloat16,
                                   num_splits: int = 0) -> int:
-    return int(_lib.lib().voom_position_free_workspace_bytes(batch, num_kv_heads, head_dim,
-                                                            num_keys, num_splits))
+    return int(_lib.lib().voom_position_free_workspace_bytes(
+        batch, num_q_heads, num_queries, num_kv_heads, head_dim, num_keys, DTYPE_CODES[dtype],
+        num_splits))
+
+
+def _as_int32(t: torch.Tensor) -> torch.Tensor:
+    """Integer index tensors go to the kernel as int32, as the reference casts
+    them (runtime/pic_attention.py:223-224)."""
+    if t.dtype == torch.int32:
+        return t
+    _require(not t.is_floating_point() and not t.is_complex(),
+             "block table and positions must be integer tensors")
+    return t.to(torch.int32)
 
 
 def position_free_paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
@@ -967,7 +1072,9 @@ def position_free_paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_page
     """Attend rotated q [B, Nq, Tq, D] to unrotated K / V pages [P, Nkv, BLOCK, D]
     through block_table [ceil(Tk / BLOCK)], rotating each key at its logical
     position (runtime/pic_attention.py:184-232, same arguments and checks).
-    Repeating a physical block id is legal and is the sharing primitive."""
+    Repeating a physical block id is legal and is the sharing primitive.  q and
+    the pages share one dtype (bf16, fp16 or fp32); the RoPE tables are fp32
+    or that dtype."""
     _require_device(q, k_pages, v_pages, block_table, key_positions, query_positions, cos, sin)
     if q.dim() != 4 or k_pages.dim() != 4 or tuple(v_pages.shape) != tuple(k_pages.shape):
         raise ValueError("invalid Q/K/V page ranks or shapes")
@@ -980,17 +1087,28 @@ def position_free_paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_page
         raise ValueError("block table does not cover logical key positions")
     if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] * 2 != D:
         raise ValueError("RoPE cache does not match head dimension")
-    if not (q.dtype == k_pages.dtype == v_pages.dtype == torch.bfloat16):
-        raise ValueError("Q/K/V page dtypes must match (bfloat16)")
-    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
-        raise ValueError("RoPE cache must be FP32")
-    _require(block_table.dtype == key_positions.dtype == query_positions.dtype == torch.int32,
-             "block table and positions must be int32")
-    need = position_free_workspace_bytes(B, NKV, D, TK, num_splits)
+    if not (q.dtype == k_pages.dtype == v_pages.dtype):
+        raise ValueError("Q/K/V page dtypes must match")
+    if q.dtype not in DTYPE_CODES:
+        raise ValueError(f"unsupported Q/K/V dtype {q.dtype}")
+    if cos.dtype != sin.dtype or cos.dtype not in (torch.float32, q.dtype):
+        raise ValueError("RoPE cache must be FP32 or match the Q/K/V dtype")
+    if D > 256:
+        raise ValueError(f"head_dim {D} unsupported (a multiple of 32 up to 256)")
+    for t in (q, k_pages, v_pages, cos, sin):
+        _require(t.is_contiguous(), "tensors must be contiguous")
+    block_table = _as_int32(block_table)
+    key_positions = _as_int32(key_positions)
+    query_positions = _as_int32(query_positions)
+    if bounds_checks_enabled():
+        check_position_free_pages(block_table, key_positions, BLOCK, P, cos.shape[0],
+                                  stream=stream)
+    need = position_free_workspace_bytes(B, NQ, TQ, NKV, D, TK, q.dtype, num_splits)
     ws = workspace(q.device, need, tag=3)
     out = torch.empty_like(q)
     _lib.call("voom_position_free_attention", _ptr(q), _ptr(k_pages), _ptr(v_pages),
               _ptr(block_table), _ptr(key_positions), _ptr(query_positions), _ptr(cos),
               _ptr(sin), _ptr(out), _ptr(ws), need, B, NQ, TQ, NKV, D, BLOCK, P, TK,
-              cos.shape[0], float(scale), int(num_splits), _stream(stream))
+              cos.shape[0], DTYPE_CODES[q.dtype], DTYPE_CODES[cos.dtype], float(scale),
+              int(num_splits), _stream(stream))
     return out
