@@ -104,7 +104,7 @@ int voom_paged_gqa_decode_noalloc(const void* q, const void* k_pool, const void*
  *   voom_paged_gqa_combine   merges each head's partial states into out and
  *                            lse_out (the online-softmax merge of
  *                            runtime/pic_attention.py:106-129).
- * voom_paged_gqa_decode(...) with num_splits > 0, or a table longer than 4096
+ * voom_paged_gqa_decode(...) with num_splits > 0, or a table longer than 1024
  * tokens, is exactly partials followed by combine. */
 int voom_paged_gqa_partials(const void* q, const void* k_pool, const void* v_pool,
                             const int32_t* block_table, const int32_t* ctx_lens,
@@ -516,35 +516,6 @@ int voom_reload_record(const void* record, int rec_slots, int first, void* const
                        const size_t* slot_bytes, const int* num_slots, int n_tensors,
                        const int32_t* slots, int n_slots, int tag, int32_t* status,
                        hipStream_t stream);
-
-/* ---------------------------------------------------------------------------
- * Calibration (no counterpart in the reference): one launch that reads
- * n_bytes of device memory (16-byte aligned) with `workgroups` workgroups of
- * 256; sink[w] ^= the XOR of the words workgroup w read.  bench.py times
- * it to give the floor of a single launch streaming a buffer of a given size.
- * ------------------------------------------------------------------------- */
-int voom_stream_read(const void* src, size_t n_bytes, uint32_t* sink, int workgroups,
-                     hipStream_t stream);
-/* The same for a row gather: reads row idx[i] (clamped into [0, n_base_rows))
- * of row_bytes (1 to 4 KiB, whole KiB) from base, and from base2 when it is
- * not NULL, for i < n_rows, four rows in flight per wavefront, 1 KiB per load
- * instruction.  bench.py times it over the position-free workload's page ids
- * in the K and V pools: the floor of reading those pages. */
-int voom_gather_read(const void* base, const void* base2, size_t row_bytes, int n_base_rows,
-                     const int32_t* idx, int n_rows, uint32_t* sink, int workgroups,
-                     hipStream_t stream);
-/* The data movement of the MLA latent kernel with no arithmetic: batch x
- * ranges x groups workgroups (the groups of a range on one XCD); each copies
- * its 64 query rows of q ([batch, 64 groups, 576] bf16, skipped when NULL)
- * and the 64-token tiles of its token range of pool ([num_slots, 64, 576]
- * bf16, page ids table[b][0..]) into LDS, two tile buffers, and writes
- * 64 x 512 fp16 of rows_out ([batch x ranges x groups, 64, 512]); sink has
- * one entry per workgroup.  bench.py times it at the latent kernel's own
- * decomposition (groups 2) and with one workgroup per range (groups 1): the
- * floors of the two ways of splitting the heads. */
-int voom_tile_read(const void* pool, int num_slots, const int32_t* table, const void* q,
-                   int batch, int max_pages, int ctx, int ranges, int groups, void* rows_out,
-                   uint32_t* sink, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -46,3 +46,16 @@ def select(q_idx: np.ndarray, w_head: np.ndarray, k_idx: np.ndarray, n: int, k: 
 def gather(latent: np.ndarray, sel: np.ndarray) -> np.ndarray:
     """The selected latent rows, in selection order (runtime/glm.py:288)."""
     return latent[sel]
+
+
+def select_torch(q_idx, w_head, k_idx, k: int, scale: float):
+    """Scores and top-k of one decode query in torch on the CPU (the timed CPU
+    baseline): q_idx [NH, D], w_head [NH], k_idx [S, D] -> ascending indices
+    of the k highest scores (torch.topk; ties in unspecified order)."""
+    import torch
+
+    s = torch.relu((q_idx.float() @ k_idx.float().T) * scale)          # [NH, S]
+    scores = (s * w_head.float()[:, None]).sum(dim=0)
+    if scores.numel() <= k:
+        return torch.arange(scores.numel())
+    return torch.sort(torch.topk(scores, k).indices).values

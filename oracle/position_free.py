@@ -86,3 +86,32 @@ def attention(q: np.ndarray, k_pages: np.ndarray, v_pages: np.ndarray, block_tab
                 o = p @ v_rows
                 out[b, h] = np.where(ok[:, None], o / np.where(l > 0, l, 1)[:, None], 0.0)
     return out
+
+
+def attention_torch(q, k_pages, v_pages, block_table, key_positions, query_positions, cos, sin,
+                    scale: float):
+    """The same attention in torch on the CPU (the timed CPU baseline): gather
+    the logical keys through the table, rotate them in fp32 at their positions
+    and round to the page dtype, then masked fp32 SDPA with the GQA broadcast.
+    q [B, NQ, TQ, D], pages [P, NKV, BLOCK, D] (any float dtype) -> fp32."""
+    import torch
+    import torch.nn.functional as F
+
+    B, NQ, TQ, D = q.shape
+    _, NKV, BLOCK, _ = k_pages.shape
+    half = D // 2
+    TK = key_positions.numel()
+    keys = torch.arange(TK)
+    pages = block_table.long()[keys // BLOCK]
+    offs = keys % BLOCK
+    k = k_pages[pages, :, offs].float()                       # [TK, NKV, D]
+    v = v_pages[pages, :, offs].float()
+    c = cos.float()[key_positions.long()][:, None, :]
+    s = sin.float()[key_positions.long()][:, None, :]
+    a, b = k[..., :half], k[..., half:]
+    k = torch.cat([a * c - b * s, b * c + a * s], dim=-1).to(k_pages.dtype).float()
+    mask = key_positions.long()[None, :] <= query_positions.long()[:, None]   # [TQ, TK]
+    out = F.scaled_dot_product_attention(q.float(), k.permute(1, 0, 2)[None],
+                                         v.permute(1, 0, 2)[None], attn_mask=mask,
+                                         scale=scale, enable_gqa=True)
+    return torch.where(mask.any(dim=1)[None, None, :, None], out, torch.zeros_like(out))

@@ -14,10 +14,11 @@ from voom_amd import _lib
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "voom_hip.h"
+CALIB_HEADER = ROOT / "include" / "voom_calibrate.h"
 
 
-def declared_symbols():
-    text = HEADER.read_text()
+def declared_symbols(header=HEADER):
+    text = header.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(voom_[a-z0-9_]+)\s*\(", text)))
 
@@ -40,6 +41,24 @@ def test_library_exports_every_declared_symbol():
 
 def test_binding_covers_every_declared_symbol():
     assert set(declared_symbols()) <= set(_lib.SIGNATURES)
+
+
+def test_calibration_probes_live_in_their_own_library():
+    """The bench's probe kernels are declared in voom_calibrate.h, exported by
+    libvoom_calibrate.so and bound by voom_amd.calibrate -- not by the
+    paged-KV library or its header."""
+    from voom_amd import calibrate
+    from voom_amd._build import CALIB_LIB_PATH
+
+    probes = declared_symbols(CALIB_HEADER)
+    assert set(probes) == {"voom_stream_read", "voom_gather_read", "voom_tile_read"}
+    assert not set(probes) & set(declared_symbols())
+    _lib.lib()  # the probe library links against the paged-KV library
+    cal = ctypes.CDLL(str(CALIB_LIB_PATH))
+    assert all(hasattr(cal, n) for n in probes)
+    product = ctypes.CDLL(str(_lib.LIB_PATH))
+    assert not any(hasattr(product, n) for n in probes)
+    assert set(probes) == set(calibrate.SIGNATURES)
 
 
 def test_abi_version_and_workspace_query():

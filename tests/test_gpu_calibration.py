@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from voom_amd import ops
+from voom_amd import calibrate, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -25,7 +25,7 @@ def test_stream_read_reads_every_word(nbytes, wgs):
     g = torch.Generator(device="cuda").manual_seed(nbytes)
     buf = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=g)
     sink = torch.zeros(wgs, dtype=torch.int32, device="cuda")
-    ops.stream_read(buf, sink, workgroups=wgs)
+    calibrate.stream_read(buf, sink, workgroups=wgs)
     torch.cuda.synchronize()
     assert sink_xor(sink) == xor_words(buf)
 
@@ -40,7 +40,7 @@ def test_gather_read_reads_the_listed_rows(row_kib, two):
                           generator=g) if two else None
     idx = torch.randint(0, rows, (1000,), dtype=torch.int32, device="cuda", generator=g)
     sink = torch.zeros(64, dtype=torch.int32, device="cuda")
-    ops.gather_read(base, idx, sink, base2=base2, workgroups=64)
+    calibrate.gather_read(base, idx, sink, base2=base2, workgroups=64)
     torch.cuda.synchronize()
     want = xor_words(base[idx.long()])
     if two:
@@ -59,7 +59,7 @@ def test_tile_read_stores_its_fold(ranges, groups):
     grid = B * ranges * groups
     rows = torch.empty(grid * 64 * 512, dtype=torch.float16, device="cuda")
     sink = torch.zeros(grid, dtype=torch.int32, device="cuda")
-    ops.tile_read(pool, table, 64 * pages - 5, ranges, groups, rows, sink, q=q)
+    calibrate.tile_read(pool, table, 64 * pages - 5, ranges, groups, rows, sink, q=q)
     torch.cuda.synchronize()
     # wavefront w stores its own fold into rows 16 w .. 16 w + 15 of the
     # workgroup; the sink holds wavefront 0's

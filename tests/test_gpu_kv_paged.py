@@ -392,3 +392,63 @@ def test_host_budget_moves_pages_to_disk_and_back(tmp_path):
     torch.cuda.synchronize()
     assert torch.equal(bits(after), bits(before))
     kv.release()
+
+
+@pytest.mark.parametrize("B,H,offset,L,spill", [(1, 64, 3, 5, False), (1, 128, 0, 64, False),
+                                                (2, 64, 150, 40, True)])
+def test_attend_mla_prefill_is_causal_absorbed_mla(B, H, offset, L, spill):
+    """attend_mla_prefill against oracle/mla.absorbed with L > 1 (the causal
+    branch of runtime/glm.py:142-153): the reference known-answer test's
+    query window (L = 5 after 3 cached tokens, tests/test_mla_absorbed.py:
+    115-222) at the kernel's latent width, a 64-token prompt at 128 heads, and
+    a window over spilled pages.  2e-2 abs / 1e-2 rel in bf16."""
+    from oracle import mla as omla
+    print(f"[kv-latent] attend_mla_prefill B={B} H={H} offset={offset} L={L} spill={spill}",
+          flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(11 + L)
+    dn, dv, C, dr, PT = 128, 128, 512, 64, 64
+    kv_b = (torch.randn((H * (dn + dv), C), generator=gen, device="cuda") * C ** -0.5
+            ).to(torch.bfloat16)
+    w_uk, w_uv_t = ops.split_kv_b(kv_b, H, dn, dv)
+    page_bytes = B * (C + dr) * 2 * PT
+    kv = PagedKVCache(num_layers=1, max_bytes=(2 * page_bytes if spill else 1 << 40),
+                      page_positions=PT, resident_pages=1)
+    lat = torch.randn((B, offset + L, C + dr), generator=gen, device="cuda").to(torch.bfloat16)
+    if offset:
+        kv.append_latent(0, lat[:, :offset])
+    kv.append_latent(0, lat[:, offset:])
+    if spill:
+        assert any(not p.resident for p in kv._pages[0])
+    q_nope = torch.randn((B, H, L, dn), generator=gen, device="cuda").to(torch.bfloat16)
+    q_rope = torch.randn((B, H, L, dr), generator=gen, device="cuda").to(torch.bfloat16)
+    scale = (dn + dr) ** -0.5
+    out, wc = kv.attend_mla_prefill(0, q_nope, q_rope, w_uk, w_uv_t, scale,
+                                    return_weighted_c=True)
+    torch.cuda.synchronize()
+    assert out.shape == (B, H, L, dv) and wc.shape == (B, H, L, C)
+    ref_out, ref_wc = omla.absorbed(q_nope.float().cpu().numpy(), q_rope.float().cpu().numpy(),
+                                    lat.float().cpu().numpy(), kv_b.float().cpu().numpy(), dn, dv,
+                                    offset=offset, bf16=True)
+    np.testing.assert_allclose(wc.float().cpu().numpy(), ref_wc, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
+    kv.release()
+
+
+def test_attend_mla_prefill_of_one_token_is_attend_mla_bitwise():
+    print("[kv-latent] attend_mla_prefill L=1 vs attend_mla", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    B, H, dn, dv, C, dr, PT = 3, 128, 128, 128, 512, 64, 64
+    kv_b = (torch.randn((H * (dn + dv), C), generator=gen, device="cuda") * C ** -0.5
+            ).to(torch.bfloat16)
+    w_uk, w_uv_t = ops.split_kv_b(kv_b, H, dn, dv)
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, page_positions=PT)
+    kv.append_latent(0, torch.randn((B, 777, C + dr), generator=gen, device="cuda")
+                     .to(torch.bfloat16))
+    q_nope = torch.randn((B, H, 1, dn), generator=gen, device="cuda").to(torch.bfloat16)
+    q_rope = torch.randn((B, H, 1, dr), generator=gen, device="cuda").to(torch.bfloat16)
+    scale = (dn + dr) ** -0.5
+    a, wa = kv.attend_mla_prefill(0, q_nope, q_rope, w_uk, w_uv_t, scale, return_weighted_c=True)
+    b, wb = kv.attend_mla(0, q_nope[:, :, 0], q_rope[:, :, 0], w_uk, w_uv_t, scale,
+                          return_weighted_c=True)
+    assert torch.equal(bits(a[:, :, 0]), bits(b)) and torch.equal(bits(wa[:, :, 0]), bits(wb))
+    kv.release()

@@ -91,3 +91,20 @@ def test_single_head_ranks_by_relu_dot():
     pos = np.flatnonzero(dots > 0)
     want = np.sort(pos[np.argsort(-dots[pos])][:10])
     assert odsa.topk(sc, 200, 10).tolist() == want.tolist()
+
+
+def test_torch_cpu_selection_matches_numpy_for_distinct_scores():
+    """The torch-CPU selection (the timed CPU baseline) equals the pinned numpy
+    selection when no two scores tie."""
+    import torch
+
+    from oracle import dsa as odsa
+
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((8, 64)).astype(np.float32)
+    w = rng.standard_normal(8).astype(np.float32)
+    k = rng.standard_normal((3000, 64)).astype(np.float32)
+    ref = odsa.select(q, w, k, 3000, 256, 0.125)
+    got = odsa.select_torch(torch.from_numpy(q), torch.from_numpy(w), torch.from_numpy(k), 256,
+                            0.125)
+    assert np.array_equal(got.numpy(), ref)

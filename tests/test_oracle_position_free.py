@@ -150,3 +150,22 @@ def test_half_store_rounds_the_rotated_keys_to_fp16():
     assert np.array_equal(half, half.astype(np.float16).astype(np.float32))  # representable
     assert np.all(np.abs(half - full) <= np.abs(full) * 2.0 ** -11 + 2.0 ** -25)
     assert not np.array_equal(half, full)
+
+
+def test_torch_cpu_restatement_matches_numpy():
+    """The torch-CPU attention (the timed CPU baseline) agrees with the pinned
+    numpy restatement, masked rows and repeated pages included."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    q, kp, vp, table = _case(rng, B=2, NQ=6, NKV=3, TQ=3, D=64, BLOCK=4, TK=23, P=6)
+    cos, sin = pf.rope_tables(64, 64, 10000.0)
+    kpos = np.arange(23)
+    qpos = np.array([0, 10, 22])
+    ref = pf.attention(q, kp, vp, table, kpos, qpos, cos, sin, 0.125, store="f32")
+    got = pf.attention_torch(*(torch.from_numpy(np.ascontiguousarray(x)) for x in
+                               (q, kp, vp, table, kpos, qpos, cos, sin)), 0.125)
+    np.testing.assert_allclose(got.numpy(), ref, atol=2e-5)
+    none = pf.attention_torch(*(torch.from_numpy(np.ascontiguousarray(x)) for x in
+                                (q, kp, vp, table, np.full(23, 50), qpos, cos, sin)), 0.125)
+    assert torch.all(none == 0)

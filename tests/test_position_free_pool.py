@@ -227,3 +227,21 @@ def test_release_is_atomic_and_reserve_growth_prevents_regrowth():
     assert cache.block_table().tolist() == list(cache.page_ids)[:10]
     cache.update_unrotated(0, *values_of(0, 2))
     assert cache.block_table().tolist() == list(cache.page_ids)
+
+
+def test_recycled_ids_come_out_in_the_reference_order():
+    """The reference frees a page at the occurrence that drops its last
+    reference (runtime/kv_cache.py:402-414) and hands out _free[-k:] in list
+    order (:367-371): pin the exact ids, repeated releases included."""
+    pool = PositionFreePagePool(1, 2, 8, device="cpu")
+    ids = pool.allocate(6)
+    assert ids == (0, 1, 2, 3, 4, 5)
+    pool.release([1, 3, 2])                  # free list [1, 3, 2]
+    assert pool.allocate(2) == (3, 2)        # _free[-2:]
+    assert pool.allocate(2) == (1, 6)        # [1] + one fresh id
+    k, v = kv(4)
+    pool.write(0, [0, 3, 4, 5], k, v)
+    pool.retain([4])                         # page 4 held twice
+    pool.release([4, 5, 4])                  # 5 dies first, 4 at its second occurrence
+    assert pool.allocate(1) == (4,)
+    assert pool.allocate(1) == (5,)

@@ -94,3 +94,84 @@ def test_noalloc_rejects_partials_beyond_its_array():
     rc = noalloc(inp, out, lse, 1 << 20)  # 1M splits need far more than the array
     assert rc == _lib.VOOM_EINVAL
     assert "scratch" in _lib.last_error()
+
+
+def _graph_case(seed):
+    return synthetic.gqa_decode_inputs(batch=4, ctx_lens=[33, 900, 2049, 64], num_q_heads=16,
+                                       num_kv_heads=4, head_dim=128, page_tokens=64,
+                                       seed_base=seed, device="cuda")
+
+
+def test_noalloc_replays_from_a_captured_graph():
+    """The entry point's reason to exist: a call captured in a HIP graph and
+    replayed.  Three replays, each after eager workspace calls on other
+    inputs; every replay is bit-equal to the eager workspace result."""
+    print("[noalloc] graph capture + replays", flush=True)
+    inp = _graph_case(41)
+    other = _graph_case(42)
+    want, want_lse = with_workspace(inp, 0)
+    out = torch.empty_like(inp.q)
+    lse = torch.empty_like(want_lse)
+    assert noalloc(inp, out, lse, 0) == 0, _lib.last_error()  # warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out.zero_()
+        with torch.cuda.graph(g, stream=s):
+            assert noalloc(inp, out, lse, 0) == 0, _lib.last_error()
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        out.zero_()
+        lse.zero_()
+        with_workspace(other, 0)
+        assert noalloc(other, torch.empty_like(out), torch.empty_like(lse), 64) == 0
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+        assert torch.equal(lse, want_lse)
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from tests.test_zz_no_alloc import _graph_case, noalloc, with_workspace
+from voom_amd import _lib
+inp = _graph_case(43)
+out = torch.empty_like(inp.q)
+lse = torch.empty((inp.q.shape[0], inp.q.shape[1]), dtype=torch.float32, device="cuda")
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+s = torch.cuda.Stream()
+with torch.cuda.stream(s):
+    with torch.cuda.graph(g, stream=s):
+        rc = noalloc(inp, out, lse, 0)   # the process's first call of the entry point
+assert rc == 0, _lib.last_error()
+torch.cuda.synchronize()
+want, want_lse = with_workspace(inp, 0)
+for _ in range(2):
+    out.zero_()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(lse, want_lse)
+print("FIRST_CALL_IN_CAPTURE_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_a_capture():
+    """A fresh process whose first call of the entry point is made under graph
+    capture (the scratch array's address is resolved inside the capture)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    print("[noalloc] first call under capture, fresh process", flush=True)
+    root = str(Path(__file__).resolve().parent.parent)
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, root], cwd=root,
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0 and "FIRST_CALL_IN_CAPTURE_OK" in res.stdout, (
+        res.stdout[-2000:] + res.stderr[-3000:])

@@ -18,6 +18,8 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libvoom_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+# bench-only probe kernels (csrc/bench), linked against LIB_NAME
+CALIB_LIB_PATH = PKG_DIR / "libvoom_calibrate.so"
 ARCH = "gfx950"
 
 # Packed-fp32 instructions are disabled for every device pass (the flag is
@@ -52,30 +54,40 @@ def _run(cmd: list[str]) -> str:
     return err
 
 
+def _link(cc: str, objs: list[Path], out: Path, extra: list[str]) -> str:
+    tmp = out.with_suffix(".so.tmp")
+    err = _run([cc, *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, objs), *extra])
+    os.replace(tmp, out)
+    return err
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every kernel source into one shared library and return its path.
+    """Compile every kernel source into one shared library and return its path;
+    the bench-only probes (csrc/bench) go into libvoom_calibrate.so beside it.
 
     Each source is compiled to an object in its own hipcc process (in
     parallel; every translation unit holds its kernels and their launchers,
     so no relocatable device code is needed), then the objects are linked."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
     cc = hipcc()
-    jobs = max(1, min(len(sources()), int(os.environ.get("MAX_JOBS", "") or os.cpu_count() or 1)))
+    srcs = sources()
+    bench_srcs = sorted((CSRC / "bench").glob("*.hip"))
+    every = srcs + bench_srcs
+    jobs = max(1, min(len(every), int(os.environ.get("MAX_JOBS", "") or os.cpu_count() or 1)))
     with tempfile.TemporaryDirectory(prefix="voom_build_") as tdir:
-        objs = [Path(tdir) / (src.name + ".o") for src in sources()]
-        cmds = [[cc, *HIP_FLAGS, "-c", "-o", str(obj), str(src)]
-                for src, obj in zip(sources(), objs)]
+        objs = [Path(tdir) / f"{i}_{src.name}.o" for i, src in enumerate(every)]
+        cmds = [[cc, *HIP_FLAGS, "-c", "-o", str(obj), str(src)] for src, obj in zip(every, objs)]
         if verbose:
             for cmd in cmds:
                 print(" ".join(cmd), flush=True)
         with ThreadPoolExecutor(max_workers=jobs) as pool:
             errs = list(pool.map(_run, cmds))
-        errs.append(_run([cc, *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, objs)]))
+        errs.append(_link(cc, objs[:len(srcs)], LIB_PATH, []))
+        errs.append(_link(cc, objs[len(srcs):], CALIB_LIB_PATH,
+                          [f"-L{PKG_DIR}", "-lvoom_hip", "-Wl,-rpath,$ORIGIN"]))
     if verbose:
         for err in errs:
             if err.strip():
                 print(err, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
 

@@ -88,9 +88,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_byteplane_merge_slots": (c_int, [_P, _P, _P, _P, c_int, c_size_t, c_int, _P, _P]),
     "voom_page_sums_verify": (c_int, [_P, _P, c_int, c_int, _P, _P]),
     "voom_record_prepare": (c_int, []),
-    "voom_stream_read": (c_int, [_P, c_size_t, _P, c_int, _P]),
-    "voom_gather_read": (c_int, [_P, _P, c_size_t, c_int, _P, c_int, _P, c_int, _P]),
-    "voom_tile_read": (c_int, [_P, c_int, _P, _P, c_int, c_int, c_int, c_int, c_int, _P, _P, _P]),
     "voom_spill_record": (c_int, [_P, _P, _P, c_int, _P, c_int, _P, c_int, c_int, c_int, _P]),
     "voom_reload_record": (c_int, [_P, c_int, c_int, _P, _P, _P, c_int, _P, c_int, c_int, _P,
                                    _P]),

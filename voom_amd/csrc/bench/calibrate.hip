@@ -1,7 +1,9 @@
-// Calibration kernel for the benchmark: the time one launch needs to stream a
+// Calibration kernels for the benchmark (libvoom_calibrate.so, not the
+// paged-KV library): the time one launch needs to stream a
 // buffer from HBM, the floor any single kernel reading that many bytes runs
 // into (launch, first-byte latency, ramp).  No counterpart in the reference.
-#include "common.h"
+#include "../common.h"
+#include "../../../include/voom_calibrate.h"
 
 namespace voom {
 namespace {

@@ -333,9 +333,9 @@ class _PinnedUploads:
         self.np = self.buf.numpy()
         self.pos = 0
         # regions whose readers may still be running, oldest first: [lo, hi,
-        # event or None while staged and not yet settled]; regions are handed
-        # out in address order, so the ones a new region overlaps are always
-        # at the front
+        # event or None while staged and not yet settled].  A region still
+        # pending from an earlier lap of the ring can sit ahead of the ones a
+        # new region overlaps, so every pending region is checked.
         self.inflight: deque = deque()
         self._own: list = []  # (event or None, dedicated buffer) of oversized lists
 
@@ -345,11 +345,17 @@ class _PinnedUploads:
             self.pos = 0
         lo, hi = self.pos, self.pos + n
         q = self.inflight
-        while q and (q[0][0] < hi and q[0][1] > lo or (q[0][2] is not None and q[0][2].query())):
-            if q[0][2] is None:
-                raise RuntimeError("pinned list ring: a staged region was never settled")
-            q[0][2].synchronize()
+        while q and q[0][2] is not None and q[0][2].query():  # finished readers
             q.popleft()
+        keep: deque = deque()
+        for region in q:
+            if region[0] < hi and region[1] > lo:
+                if region[2] is None:
+                    raise RuntimeError("pinned list ring: a staged region was never settled")
+                region[2].synchronize()  # its reader must be done before the rewrite
+            else:
+                keep.append(region)
+        self.inflight = keep
         self.np[lo:hi] = arr.reshape(-1)
         self.pos = hi
         return lo, hi
@@ -1842,6 +1848,63 @@ class PagedKVCache:
         wc = self._attend_pages(layer, run)
         out = ops.mla_project_out(wc, w_uv_t)
         return (out, wc) if return_weighted_c else out
+
+    def attend_mla_prefill(self, layer: int, q_nope: torch.Tensor, q_rope: torch.Tensor,
+                           w_uk, w_uv_t, scale: float, return_weighted_c: bool = False):
+        """Causal absorbed-MLA attention of the layer's newest L tokens.
+
+        q_nope [B, H, L, dn] and q_rope [B, H, L, dr] hold the queries of
+        positions S-L .. S-1, whose latent rows were just appended: the L > 1
+        branch of _mla_absorbed_attention (runtime/glm.py:142-153), where key
+        t' is visible to query t iff t' <= offset + t, with the dense path's
+        cast points (fp32 scores, bf16 P, bf16 weighted_c; :157-164).  As in
+        ``attend_prefill``, every query row becomes its own entry of the paged
+        latent kernel -- the same block-table row with the context cut at its
+        own position + 1 -- and the absorption products run on the decode
+        kernels, 16 rows per launch, so L = 1 gives ``attend_mla``'s bits.
+        Spilled pages of the layer are made resident first.  Returns the
+        per-head output [B, H, L, dv] (and weighted_c [B, H, L, 512]).
+        """
+        self._require_kind(layer, "latent")
+        if q_nope.dim() != 4 or q_rope.dim() != 4:
+            raise ValueError("q_nope [B, H, L, dn] and q_rope [B, H, L, dr]")
+        B, H, L, dn = q_nope.shape
+        dr = q_rope.shape[-1]
+        if tuple(q_rope.shape[:3]) != (B, H, L) or B != self._batch:
+            raise ValueError(f"q_rope must be [{self._batch}, {H}, {L}, dr]")
+        S = self._len[layer]
+        if L > S:
+            raise ValueError(f"{L} queries but the layer holds {S} tokens")
+        spilled = [p for p in self._pages[layer] if not p.resident]
+        if spilled:
+            self.reload(spilled)
+        pool = self._pool(layer)
+        w_uk = ops.pack_head_weights(w_uk)
+        w_uv = ops.pack_head_weights(w_uv_t)
+        R = B * L
+        rows_n = q_nope.permute(0, 2, 1, 3).reshape(R, H, dn).contiguous()
+        rows_r = q_rope.permute(0, 2, 1, 3).reshape(R, H, dr).contiguous()
+        q_lat = torch.empty((R, H, w_uk.n + dr), dtype=torch.bfloat16, device=self.device)
+        for r0 in range(0, R, 16):  # the head products take at most 16 rows
+            r1 = min(R, r0 + 16)
+            q_lat[r0:r1] = ops.mla_absorb_query(rows_n[r0:r1], rows_r[r0:r1], w_uk)
+        table = self._tables[layer].repeat_interleave(L, dim=0)
+        ctx = (torch.arange(S - L + 1, S + 1, dtype=torch.int32, device=self.device)
+               .repeat(B))
+        wc = torch.empty((R, H, w_uk.n), dtype=torch.bfloat16, device=self.device)
+        step = 256  # query rows per latent launch (bounds the range partials)
+        for r0 in range(0, R, step):
+            r1 = min(R, r0 + step)
+            wc[r0:r1] = ops.mla_latent_decode(q_lat[r0:r1], pool.lat, table[r0:r1].contiguous(),
+                                              ctx[r0:r1].contiguous(), scale=scale)
+        out = torch.empty((R, H, w_uv.n), dtype=torch.bfloat16, device=self.device)
+        for r0 in range(0, R, 16):
+            r1 = min(R, r0 + 16)
+            out[r0:r1] = ops.mla_project_out(wc[r0:r1], w_uv)
+        out = out.reshape(B, L, H, w_uv.n).permute(0, 2, 1, 3)
+        if return_weighted_c:
+            return out, wc.reshape(B, L, H, w_uk.n).permute(0, 2, 1, 3)
+        return out
 
     def _attend_selected(self, layer: int, q_lat: torch.Tensor, selection, scale: float):
         if isinstance(selection, tuple):

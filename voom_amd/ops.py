@@ -51,6 +51,25 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
+def _side_stream(stream: torch.cuda.Stream | None) -> torch.cuda.Stream | None:
+    """``stream`` when it is not the current stream (work enqueued there reads
+    tensors the current stream made), else None."""
+    if stream is None or stream == torch.cuda.current_stream():
+        return None
+    return stream
+
+
+def _used_on(stream: torch.cuda.Stream | None, *tensors: torch.Tensor | None) -> None:
+    """Tensors allocated on the current stream but read or written by work on a
+    side stream: the caching allocator must not hand their memory out again
+    before that work has run (record_stream)."""
+    if stream is None:
+        return
+    for t in tensors:
+        if t is not None:
+            t.record_stream(stream)
+
+
 def workspace(device: torch.device, nbytes: int, tag: int = 0) -> torch.Tensor:
     """Per-device cached uint8 scratch tensor of at least ``nbytes`` bytes."""
     key = (device.index if device.index is not None else torch.cuda.current_device(), tag)
@@ -448,57 +467,6 @@ def _record_call_args(pools: list[torch.Tensor], slots: torch.Tensor, record: to
     return ptrs, sbytes, counts
 
 
-def stream_read(src: torch.Tensor, sink: torch.Tensor, workgroups: int = 512,
-                stream: torch.cuda.Stream | None = None) -> None:
-    """One launch reading all of ``src`` (device, contiguous, 16-byte multiple):
-    the calibration kernel bench.py uses for the single-launch streaming floor.
-    ``sink`` is a device int32 tensor of at least ``workgroups`` entries."""
-    _require_device(src, sink)
-    nbytes = src.numel() * src.element_size()
-    _require(sink.dtype == torch.int32 and sink.numel() >= workgroups, "sink too small")
-    _lib.call("voom_stream_read", _ptr(src), nbytes, _ptr(sink), int(workgroups), _stream(stream))
-
-
-def gather_read(base: torch.Tensor, idx: torch.Tensor, sink: torch.Tensor,
-                base2: torch.Tensor | None = None, workgroups: int = 512,
-                stream: torch.cuda.Stream | None = None) -> None:
-    """One launch reading rows ``base[idx[i]]`` (base [rows, ...], each row 1-4
-    KiB), and the same rows of ``base2`` (same shape) when given -- the
-    calibration kernel for the floor of a page gather."""
-    _require_device(base, idx, sink, base2)
-    row_bytes = base[0].numel() * base.element_size()
-    _require(base2 is None or (base2.shape == base.shape and base2.dtype == base.dtype),
-             "base2 must have base's shape and dtype")
-    _require(idx.dtype == torch.int32 and idx.dim() == 1, "idx must be 1-D int32")
-    _require(sink.dtype == torch.int32 and sink.numel() >= workgroups, "sink too small")
-    _lib.call("voom_gather_read", _ptr(base), _ptr(base2), row_bytes, base.shape[0], _ptr(idx),
-              idx.numel(), _ptr(sink), int(workgroups), _stream(stream))
-
-
-def tile_read(pool: torch.Tensor, table: torch.Tensor, ctx: int, ranges: int, groups: int,
-              rows: torch.Tensor, sink: torch.Tensor, q: torch.Tensor | None = None,
-              stream: torch.cuda.Stream | None = None) -> None:
-    """One launch with the data movement of the MLA latent kernel and no
-    arithmetic: ``table.shape[0] * ranges * groups`` workgroups stream the
-    64-token tiles of ``pool`` ([slots, 64, 576] bf16) for their token range
-    (and their 64 rows of ``q`` [B, 64 groups, 576] when given) through LDS
-    and write 64 x 512 fp16 of ``rows`` each -- the calibration kernel for the
-    floor of the latent contraction's loads."""
-    _require_device(pool, table, rows, sink, q)
-    _require(pool.dim() == 3 and tuple(pool.shape[1:]) == (64, 576) and pool.dtype == torch.bfloat16,
-             "pool must be [slots, 64, 576] bf16")
-    _require(table.dtype == torch.int32 and table.dim() == 2, "table must be [B, max_pages] int32")
-    batch = table.shape[0]
-    grid = batch * ranges * groups
-    _require(rows.numel() * rows.element_size() >= grid * 64 * 512 * 2, "rows too small")
-    _require(sink.dtype == torch.int32 and sink.numel() >= grid, "sink too small")
-    _require(q is None or (q.dtype == torch.bfloat16 and q.numel() >= batch * groups * 64 * 576),
-             "q must hold [B, 64 groups, 576] bf16")
-    _lib.call("voom_tile_read", _ptr(pool), pool.shape[0], _ptr(table), _ptr(q), batch,
-              table.shape[1], int(ctx), int(ranges), int(groups), _ptr(rows), _ptr(sink),
-              _stream(stream))
-
-
 def record_prepare() -> None:
     """Set the spill-record kernels up on the current device ahead of the first
     spill (their one-time launch setup costs about a millisecond each)."""
@@ -852,12 +820,16 @@ class HeadWeights:
     def __init__(self, w: torch.Tensor, *, stream: torch.cuda.Stream | None = None):
         dev = _require_device(w)
         _require(w.dtype == torch.bfloat16 and w.dim() == 3, "w must be bf16 [H, K, N]")
+        side = _side_stream(stream)
         w = w.contiguous()
         self.heads, self.k, self.n = (int(v) for v in w.shape)
         nbytes = int(_lib.lib().voom_mla_head_weights_bytes(self.heads, self.k, self.n))
         self.packed = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev)
+        if side is not None:
+            side.wait_stream(torch.cuda.current_stream())  # w (and its copy) are ready
         _lib.call("voom_mla_pack_head_weights", _ptr(w), _ptr(self.packed), self.heads, self.k,
                   self.n, _stream(stream))
+        _used_on(side, w, self.packed)
 
     @property
     def shape(self):
@@ -924,8 +896,12 @@ def head_gemv(x: torch.Tensor, w, *, out: torch.Tensor | None = None,
     _require(out.dtype == x.dtype and out.device == dev and out.dim() == 3 and
              tuple(out.shape[:2]) == (B, H) and out.shape[2] >= N and out.is_contiguous(),
              "out [B, H, >= N] contiguous bf16")
+    side = _side_stream(stream)
+    if side is not None:
+        side.wait_stream(torch.cuda.current_stream())  # x's contiguous copy and out are ready
     _lib.call("voom_mla_head_gemv", _ptr(x), _ptr(w.packed), _ptr(out), B, H, K, N, K,
               out.shape[2], _stream(stream))
+    _used_on(side, x, out)
     return out
 
 
@@ -966,6 +942,7 @@ def mla_latent_decode_project(q_lat: torch.Tensor, lat_pool: torch.Tensor,
               _ptr(ctx_lens), _ptr(w_uv.packed), w_uv.n, _ptr(y), _ptr(wc), _ptr(lse), _ptr(ws),
               need, B, H, LD, 512, PT, block_table.shape[1], slots, float(scale), int(num_ranges),
               _stream(stream))
+    _used_on(_side_stream(stream), y, wc, lse, ws)
     res = (y,) + ((wc,) if return_weighted_c else ()) + ((lse,) if return_lse else ())
     return res if len(res) > 1 else y
 

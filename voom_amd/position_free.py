@@ -166,7 +166,9 @@ class PositionFreePagePool:
         take = min(count, self._nfree)
         fresh = count - take
         self._grow(self._high + fresh)
-        recycled = self._stack[self._nfree - take:self._nfree][::-1]
+        # the top `take` free ids in the order they were freed: the reference
+        # hands out _free[-take:] as a list slice (runtime/kv_cache.py:367-371)
+        recycled = self._stack[self._nfree - take:self._nfree]
         ids = np.concatenate([recycled, np.arange(self._high, self._high + fresh)])
         if np.any(self._refs[ids] != 0):
             raise RuntimeError("position-free allocator recycled a live page")
@@ -207,7 +209,7 @@ class PositionFreePagePool:
         ids = _ids(page_ids)
         if ids.size == 0:
             return
-        uniq, first, counts = np.unique(ids, return_index=True, return_counts=True)
+        uniq, counts = np.unique(ids, return_counts=True)
         valid = (uniq >= 0) & (uniq < self._high)
         over = ~valid
         over[valid] = self._refs[uniq[valid]] < counts[valid]
@@ -216,8 +218,10 @@ class PositionFreePagePool:
         self._refs[uniq] -= counts
         gone = self._refs[uniq] == 0
         if gone.any():
-            # pushed in the order the ids were given: the last one is handed out first
-            dead = uniq[gone][np.argsort(first[gone], kind="stable")]
+            # freed in the order the reference's loop frees them: a page dies at
+            # its last occurrence in page_ids (runtime/kv_cache.py:402-414)
+            last = ids.size - 1 - np.unique(ids[::-1], return_index=True)[1]
+            dead = uniq[gone][np.argsort(last[gone], kind="stable")]
             self._written[:, dead] = False
             self._stack[self._nfree:self._nfree + dead.size] = dead
             self._nfree += dead.size
