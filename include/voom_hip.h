@@ -42,7 +42,7 @@ const char* voom_last_error(void);
 
 /* ABI version, bumped on any signature or layout change (2: checksums in the
  * slot codec; 3: spill-record calls; 4: element and table types of the
- * position-free call). */
+ * position-free call; 5: the top-k workspace's zeroed row counters). */
 int voom_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -236,8 +236,11 @@ int voom_mla_sparse_decode(const void* q_lat, const void* lat_pool, const int32_
  * scores of keys s < lens[b] (causal for a decode step at position
  * lens[b] - 1), written to sel [batch, k] as ascending indices, with
  * sel_lens[b] = min(lens[b], k).  Among keys tied at the k-th score the
- * lowest indices are kept.  The workspace (candidate slots) must hold
- * voom_dsa_topk_workspace_bytes(batch, cap) bytes.
+ * lowest indices are kept.  One launch.  The workspace (candidate slots and
+ * one arrival counter per row) must hold voom_dsa_topk_workspace_bytes(batch,
+ * cap) bytes, and its first 4 * batch bytes must be zero before the first
+ * call (allocate it zeroed); every call leaves them zero again.  Calls that
+ * share a workspace must not overlap.
  * ------------------------------------------------------------------------- */
 int voom_dsa_index_scores(const void* q_idx, const float* w_head, const void* k_idx,
                           const int32_t* lens, float* scores, int batch, int num_heads,

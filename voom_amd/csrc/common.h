@@ -93,12 +93,19 @@ __device__ __forceinline__ float wave_max_uniform(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Inclusive prefix sum over the 64 lanes (lane l gets x_0 + ... + x_l), all
+// by DPP: shifts right by 1, 2, 4 and 8 within each 16-lane row (a lane with
+// no source adds 0), then lane 15 of rows 0 and 2 added into rows 1 and 3,
+// and lane 31 into rows 2 and 3.  A shuffle ladder would take six round
+// trips through the LDS crossbar instead.
 __device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
+  (void)lane;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15, rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31, rows 2 and 3
   return x;
 }
 

@@ -17,18 +17,18 @@
 // (key i16, group g) then holds heads 4g + r of its key, so relu, the head
 // weights and the head sum stay in registers plus two cross-group adds.
 //
-// Top-k, two launches per call: (1) chunk workgroups (4,096 keys each) each
-// place the same threshold T0 at a fixed rank of a strided sample of the row
-// and move the keys >= T0, with their indices and in index order, to
-// per-chunk slots -- the row is read once, by many CUs; (2) one workgroup
-// per row gathers the candidates into LDS (at most 16,384)
-// and runs the exact selection there: radix passes of up to 11 bits below the
-// leading bits every candidate shares find the k-th largest key T and how
-// many keys equal to T to keep, and an ordered write -- each wavefront owns a
-// contiguous range, counts its keys above and equal to T, and after an
-// exclusive scan over wavefronts writes its indices -- leaves the output
-// sorted without a sort.  Scores map to order-preserving 32-bit keys.  When
-// the sample misjudges the row (fewer than k or more than 16,384
+// Top-k, one launch per call: chunk workgroups (4,096 keys each) each place
+// the same threshold T0 at a fixed rank of a strided sample of the row and
+// move the keys >= T0, with their indices and in index order, to per-chunk
+// slots -- the row is read once, by many CUs; the row's last chunk workgroup
+// to finish (an arrival counter in the workspace) gathers the candidates (at
+// most 16,384) into registers and runs the exact selection there: radix
+// passes over offsets from the candidates' smallest key find the k-th largest
+// key T and how many keys equal to T to keep, and an ordered write -- each
+// wavefront owns a contiguous range of candidates, counts its keys above and
+// equal to T, and after a prefix over wavefronts writes its indices -- leaves
+// the output sorted without a sort.  Scores map to order-preserving 32-bit
+// keys.  When the sample misjudges the row (fewer than k or more than 16,384
 // candidates), the same exact selection runs over the row in memory.
 #include "common.h"
 
@@ -133,7 +133,13 @@ constexpr int kRadixBits = 12;                     // digit width of the radix s
 constexpr int kRadixBins = 1 << kRadixBits;
 constexpr int kBinsPerThread = kRadixBins / kTopkThreads;
 static_assert(kBinsPerThread == 4, "one int4 of histogram bins per thread");
-constexpr int kChunksPerThread = 2;                // select kernel: up to 2048 chunks
+constexpr int kChunksPerThread = 2;                // up to 2048 chunks per row
+constexpr int kCandCap = 16384;                    // candidates selected from registers
+constexpr int kRegKeys = kCandCap / kTopkThreads;  // candidates per thread
+constexpr int kSample = 4096;                      // keys sampled to place the threshold
+constexpr int kChunkKeys = 4096;                   // keys per chunk workgroup
+static_assert(kChunkKeys == 4 * kTopkThreads, "four keys of the chunk per thread");
+static_assert(kSample == 4 * kTopkThreads, "four sample keys per thread");
 
 // Order-preserving map of fp32 onto uint32: a > b  <=>  key(a) > key(b), and
 // -0 maps like +0 (they compare equal, so they tie).
@@ -141,6 +147,32 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
   u = u == 0x80000000u ? 0u : u;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// Largest and smallest of a uint32 over the 64 lanes, the same in every lane
+// (quad swaps and row mirrors by DPP, then the four rows read out).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  uint32_t t;
+  t = dpp_u32<0xB1>(v);  v = t > v ? t : v;
+  t = dpp_u32<0x4E>(v);  v = t > v ? t : v;
+  t = dpp_u32<0x141>(v); v = t > v ? t : v;
+  t = dpp_u32<0x140>(v); v = t > v ? t : v;
+  uint32_t r = 0u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t x = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16 * k));
+    r = x > r ? x : r;
+  }
+  return r;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return ~wave_max_u32(~v);
 }
 
 // Exclusive scan of one int per thread over the workgroup; returns the
@@ -163,138 +195,271 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* tmp, int& total)
   return before + inc - x;
 }
 
-constexpr int kCandCap = 16384;  // candidate keys held in LDS
-constexpr int kSample = 4096;    // keys sampled to place the threshold
-constexpr int kChunkKeys = 4096; // keys per compaction workgroup
+// Radix select over keys held in registers: thread t holds up to N keys,
+// key[r] in use iff r < nregs (the same in every thread) and bit r of
+// `valid`, every one within [lo, hi].  T becomes the rank-th largest key (1
+// <= rank <= the number of keys) and kk how many keys equal to T belong to
+// the top `rank`.  With max_passes > 0 the passes may stop early -- after
+// max_passes passes, or after any pass whose crossing bin holds at most
+// `enough` keys: T is then the lower edge of the bin holding the rank-th
+// largest key (at least `rank` keys are >= T, at most rank - 1 + enough) and
+// kk is meaningless.
+//
+// Bins are offsets from the range's lower end: a pass over [base, base +
+// span] counts (key - base) >> shift in 2^width bins, width = min(bits of
+// span, kRadixBits), so the bins cover the keys' range however many leading
+// bits its ends share (scores on both sides of a power of two share none,
+// yet may lie close together); the bin holding the rank-th largest key is
+// the next range.  A range narrower than 2^24 takes two passes.
+//
+// Per pass: the histogram (LDS atomics); a barrier; thread t takes bins 4 q4
+// .. 4 q4 + 3 (q4 = 1023 - t, so the bins run in descending order over the
+// threads), clears the same int4 of the other histogram buffer, and each
+// wavefront scans its counts (DPP) and leaves its total; a barrier;
+// wavefront 0 alone finds the crossing -- the totals name the wavefront whose
+// bins hold it, whose 256 bins it reads and scans -- and leaves it in
+// found[]; a barrier.  (Every wavefront finding it for itself saves that
+// barrier but costs more: sixteen wavefronts share four SIMDs.)  The two
+// buffers alternate between passes, so pass p's is cleared in pass p + 1,
+// after every wavefront has passed pass p.
+// hist2: 2 * kRadixBins ints, 16-byte aligned; totals: kTopkWaves ints,
+// 16-byte aligned; found: 3 ints.  Every wavefront must have finished with
+// them since its last barrier.
+template <int N>
+__device__ void radix_select_regs(const uint32_t (&key)[N], uint32_t valid, int nregs, int rank,
+                                  int* hist2, int* totals, int* found, uint32_t lo, uint32_t hi,
+                                  int max_passes, int enough, uint32_t& T, int& kk_out) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = tid / kWave;
+  int4* h4 = reinterpret_cast<int4*>(hist2);
+  h4[tid] = make_int4(0, 0, 0, 0);
+  h4[tid + kRadixBins / 4] = make_int4(0, 0, 0, 0);
+  __syncthreads();  // both buffers clear
+  uint32_t base = lo;
+  uint32_t span = hi - lo;
+  int kk = rank;
+#pragma unroll 1
+  for (int pass = 0; span != 0u && (max_passes <= 0 || pass < max_passes); ++pass) {
+    const int cur = pass & 1;
+    int* hist = hist2 + cur * kRadixBins;
+    const int bits = 32 - __clz(static_cast<int>(span));
+    const int width = bits < kRadixBits ? bits : kRadixBits;
+    const int shift = bits - width;
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+      if (r < nregs) {
+        const uint32_t d = key[r] - base;
+        if (((valid >> r) & 1u) && d <= span) atomicAdd(&hist[d >> shift], 1);
+      }
+    }
+    __syncthreads();  // histogram complete
+    const int q4 = kRadixBins / 4 - 1 - tid;
+    const int4 h = reinterpret_cast<const int4*>(hist)[q4];
+    h4[(cur ^ 1) * (kRadixBins / 4) + q4] = make_int4(0, 0, 0, 0);
+    const int mine = h.x + h.y + h.z + h.w;
+    const int inc = wave_inclusive_scan(mine, lane);
+    if (lane == kWave - 1) totals[wv] = inc;
+    __syncthreads();  // wavefront totals in LDS; the other buffer clear
+    if (wv == 0) {
+      // cw: the wavefront whose bins hold the crossing; above: the keys in
+      // the (higher) bins of the wavefronts before it
+      int cw = 0;
+      int above = 0;
+      int cum = 0;
+#pragma unroll
+      for (int k4 = 0; k4 < kTopkWaves / 4; ++k4) {
+        const int4 t = reinterpret_cast<const int4*>(totals)[k4];
+        const int tk[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          cum += tk[e];
+          if (cum < kk) {
+            cw = 4 * k4 + e + 1;
+            above = cum;
+          }
+        }
+      }
+      const int cq4 = kRadixBins / 4 - 1 - (cw * kWave + lane);
+      const int4 hc = reinterpret_cast<const int4*>(hist)[cq4];
+      const int c[kBinsPerThread] = {hc.w, hc.z, hc.y, hc.x};  // bins 4 cq4 + 3 .. 4 cq4
+      const int m = hc.x + hc.y + hc.z + hc.w;
+      int run = above + wave_inclusive_scan(m, lane) - m;  // keys in higher bins
+#pragma unroll
+      for (int e = 0; e < kBinsPerThread; ++e) {
+        if (run < kk && run + c[e] >= kk) {  // exactly one bin of one lane
+          found[0] = 4 * cq4 + 3 - e;
+          found[1] = run;
+          found[2] = c[e];
+        }
+        run += c[e];
+      }
+    }
+    __syncthreads();  // crossing in found[]
+    const uint32_t off = static_cast<uint32_t>(found[0]) << shift;
+    kk -= found[1];
+    base += off;
+    const uint32_t bin_m1 = (1u << shift) - 1u;
+    span = span - off < bin_m1 ? span - off : bin_m1;
+    if (max_passes > 0 && found[2] <= enough) break;
+  }
+  T = base;
+  kk_out = kk;
+}
 
-// Radix select over `count` keys read by key(i): the rank-th largest key T
-// (rank >= 1) and how many keys equal to T belong to the top `rank` (kk).
-// The digits start below the leading bits that every key shares: scores of
-// one row share their sign and most of their exponent, and a first digit over
-// those bits would send every key to a handful of histogram bins, serialising
-// the LDS atomics.  The shared bits come from the keys' range [lo, hi], passed
-// in when the caller knows it (range_known) or found by a min/max reduction.
-// Passes of kRadixBits bits then walk down to bit 0 (or stop after
-// max_passes > 0 passes: T is then the lower edge of the crossing bin, a key
-// bound with at least `rank` keys at or above it, and kk is meaningless); a
-// thread adds runs of equal bins as one atomic.  Three barriers per pass:
-// after the histogram; after each thread has taken (and zeroed, for the next
-// pass) its int4 of bins and each wavefront has left its scan total; after
-// the thread holding the crossing has written it.  (Zeroing the histogram and
-// the scan as separate steps cost six barriers a pass, 5.5 k cycles; one
-// wavefront scanning every bin hit 32-way LDS bank conflicts.)
-// found[] holds the result, scan_tmp kTopkWaves ints; hist must hold
-// kRadixBins ints, 16-byte aligned.
+// Ordered selection write from registers: key[r] / idx[r] of thread (wave w,
+// lane l) is candidate w * per + 64 r + l, candidates in index order, in use
+// iff r < nregs (the same in every thread) and bit r of `valid`.  counts: 2 *
+// kTopkWaves ints of LDS, 16-byte aligned.  Every key > T and the first kk keys == T go to out[]
+// in index order: counts per wavefront, a prefix over the wavefronts, then
+// ballots place each index.  counts: 2 * kTopkWaves ints of LDS.
+template <int N>
+__device__ void ordered_write_regs(const uint32_t (&key)[N], const int32_t (&idx)[N],
+                                   uint32_t valid, int nregs, uint32_t T, int kk, int* counts,
+                                   int32_t* out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  int gt = 0;
+  int eq = 0;
+#pragma unroll
+  for (int r = 0; r < N; ++r) {
+    if (r < nregs) {
+      const bool v = (valid >> r) & 1u;
+      gt += __popcll(__ballot(v && key[r] > T));
+      eq += __popcll(__ballot(v && key[r] == T));
+    }
+  }
+  if (lane == 0) {
+    counts[wv] = gt;
+    counts[kTopkWaves + wv] = eq;
+  }
+  __syncthreads();
+  int gt_before = 0;
+  int eq_before = 0;
+#pragma unroll
+  for (int k4 = 0; k4 < kTopkWaves / 4; ++k4) {
+    const int4 g = reinterpret_cast<const int4*>(counts)[k4];
+    const int4 q = reinterpret_cast<const int4*>(counts + kTopkWaves)[k4];
+    gt_before += (4 * k4 < wv ? g.x : 0) + (4 * k4 + 1 < wv ? g.y : 0) +
+                 (4 * k4 + 2 < wv ? g.z : 0) + (4 * k4 + 3 < wv ? g.w : 0);
+    eq_before += (4 * k4 < wv ? q.x : 0) + (4 * k4 + 1 < wv ? q.y : 0) +
+                 (4 * k4 + 2 < wv ? q.z : 0) + (4 * k4 + 3 < wv ? q.w : 0);
+  }
+  int pos = gt_before + (eq_before < kk ? eq_before : kk);  // selections before this wave
+  int eq_seen = eq_before;
+  const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int r = 0; r < N; ++r) {
+    if (r < nregs) {
+      const bool v = (valid >> r) & 1u;
+      const bool is_gt = v && key[r] > T;
+      const bool is_eq = v && key[r] == T;
+      const unsigned long long eq_mask = __ballot(is_eq);
+      const int eq_rank = eq_seen + __popcll(eq_mask & below);
+      const bool take = is_gt || (is_eq && eq_rank < kk);
+      const unsigned long long take_mask = __ballot(take);
+      if (take) out[pos + __popcll(take_mask & below)] = idx[r];
+      pos += __popcll(take_mask);
+      eq_seen += __popcll(eq_mask);
+    }
+  }
+}
+
+// Radix select over keys read by key(i), i < count, from memory: the
+// fallback for a row whose sampled threshold left fewer than k or more than
+// kCandCap candidates.  Same digits and result as radix_select_regs (exact:
+// no pass limit), one histogram buffer and three barriers per pass; the
+// range comes from a min/max pass over the keys.  hist: kRadixBins ints,
+// 16-byte aligned; scan_tmp kTopkWaves ints; found 2 ints.
 template <typename KeyFn>
-__device__ void radix_select(KeyFn key, int count, int rank, int* hist, int* scan_tmp, int* found,
-                             bool range_known, uint32_t lo_k, uint32_t hi_k, int max_passes,
-                             uint32_t& T, int& kk_out) {
+__device__ void radix_select_mem(KeyFn key, int count, int rank, int* hist, int* scan_tmp,
+                                 int* found, uint32_t& T, int& kk_out) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
   int4* hist4 = reinterpret_cast<int4*>(hist);
   hist4[tid] = make_int4(0, 0, 0, 0);
-  if (range_known) {
-    __syncthreads();  // bins zero
-  } else {
-    if (tid == 0) {
-      found[0] = static_cast<int>(0xFFFFFFFFu);
-      found[1] = 0;
-    }
-    lo_k = 0xFFFFFFFFu;
-    hi_k = 0u;
-    for (int i = tid; i < count; i += kTopkThreads) {
-      const uint32_t u = key(i);
-      lo_k = u < lo_k ? u : lo_k;
-      hi_k = u > hi_k ? u : hi_k;
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const uint32_t a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lo_k), o));
-      const uint32_t b = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi_k), o));
-      lo_k = a < lo_k ? a : lo_k;
-      hi_k = b > hi_k ? b : hi_k;
-    }
-    __syncthreads();  // found[] and hist initialised
-    if (lane == 0) {
-      atomicMin(reinterpret_cast<unsigned int*>(&found[0]), lo_k);
-      atomicMax(reinterpret_cast<unsigned int*>(&found[1]), hi_k);
-    }
-    __syncthreads();
-    lo_k = static_cast<uint32_t>(found[0]);
-    hi_k = static_cast<uint32_t>(found[1]);
+  uint32_t lo = 0xFFFFFFFFu;
+  uint32_t hi = 0u;
+  for (int i = tid; i < count; i += kTopkThreads) {
+    const uint32_t u = key(i);
+    lo = u < lo ? u : lo;
+    hi = u > hi ? u : hi;
   }
-  // bits above `top` are common to every key
-  int top = 31 - __clz(static_cast<int>(lo_k ^ hi_k));  // -1 when all keys are equal
-  uint32_t prefix = top < 31 ? (hi_k & ~((2u << (top < 0 ? 0 : top)) - 1u)) : 0u;
-  if (top < 0) prefix = hi_k;
-  uint32_t pmask = top < 31 ? ~((2u << (top < 0 ? 0 : top)) - 1u) : 0u;
-  if (top < 0) pmask = 0xFFFFFFFFu;
+  lo = wave_min_u32(lo);
+  hi = wave_max_u32(hi);
+  if (lane == 0) {
+    scan_tmp[wv] = static_cast<int>(lo);
+    found[0] = 0;
+  }
+  __syncthreads();
+  uint32_t l2 = 0xFFFFFFFFu;
+#pragma unroll
+  for (int k = 0; k < kTopkWaves; ++k) {
+    const uint32_t x = static_cast<uint32_t>(scan_tmp[k]);
+    l2 = x < l2 ? x : l2;
+  }
+  __syncthreads();
+  if (lane == 0) scan_tmp[wv] = static_cast<int>(hi);
+  __syncthreads();
+  uint32_t h2 = 0u;
+#pragma unroll
+  for (int k = 0; k < kTopkWaves; ++k) {
+    const uint32_t x = static_cast<uint32_t>(scan_tmp[k]);
+    h2 = x > h2 ? x : h2;
+  }
+  __syncthreads();
+  uint32_t base = l2;
+  uint32_t span = h2 - l2;
   int kk = rank;
-  int passes = 0;
 #pragma unroll 1
-  while (top >= 0 && (max_passes <= 0 || passes < max_passes)) {
-    const int width = top + 1 < kRadixBits ? top + 1 : kRadixBits;
-    const int shift = top + 1 - width;
-    const int bins = 1 << width;
-    int run_bin = -1;
-    int run_n = 0;
+  while (span != 0u) {
+    const int bits = 32 - __clz(static_cast<int>(span));
+    const int width = bits < kRadixBits ? bits : kRadixBits;
+    const int shift = bits - width;
     for (int i = tid; i < count; i += kTopkThreads) {
-      const uint32_t u = key(i);
-      if ((u & pmask) == prefix) {
-        const int bin = static_cast<int>((u >> shift) & static_cast<uint32_t>(bins - 1));
-        if (bin != run_bin) {
-          if (run_n) atomicAdd(&hist[run_bin], run_n);
-          run_bin = bin;
-          run_n = 0;
-        }
-        ++run_n;
-      }
+      const uint32_t d = key(i) - base;
+      if (d <= span) atomicAdd(&hist[d >> shift], 1);
     }
-    if (run_n) atomicAdd(&hist[run_bin], run_n);
-    __syncthreads();  // histogram complete (found[] of the previous pass read)
-    // thread t owns the int4 of bins base .. base + 3, base = kRadixBins - 4 (t + 1),
-    // taken in descending order
-    const int q4 = kRadixBins / kBinsPerThread - 1 - tid;
+    __syncthreads();  // histogram complete
+    const int q4 = kRadixBins / 4 - 1 - tid;
     const int4 h = hist4[q4];
     hist4[q4] = make_int4(0, 0, 0, 0);
-    const int base = q4 * kBinsPerThread;
     const int c[kBinsPerThread] = {h.w, h.z, h.y, h.x};
     const int mine = h.x + h.y + h.z + h.w;
     const int inc = wave_inclusive_scan(mine, lane);
     if (lane == kWave - 1) scan_tmp[wv] = inc;
-    __syncthreads();  // wave totals in scan_tmp, bins zero again
+    __syncthreads();  // wave totals in scan_tmp, bins clear again
     int run = inc - mine;
 #pragma unroll
     for (int k = 0; k < kTopkWaves; ++k) run += k < wv ? scan_tmp[k] : 0;
 #pragma unroll
     for (int e = 0; e < kBinsPerThread; ++e) {
       if (run < kk && run + c[e] >= kk) {
-        found[0] = base + kBinsPerThread - 1 - e;
+        found[0] = 4 * q4 + 3 - e;
         found[1] = run;
       }
       run += c[e];
     }
-    __syncthreads();  // result in found[]
-    const int d = found[0];
+    __syncthreads();  // crossing in found[]
+    const uint32_t off = static_cast<uint32_t>(found[0]) << shift;
     kk -= found[1];
-    prefix |= static_cast<uint32_t>(d) << shift;
-    pmask |= static_cast<uint32_t>(bins - 1) << shift;
-    top = shift - 1;
-    ++passes;
+    base += off;
+    const uint32_t bin_m1 = (1u << shift) - 1u;
+    span = span - off < bin_m1 ? span - off : bin_m1;
   }
   __syncthreads();  // found[] read by every thread before anyone reuses it
-  T = prefix;
+  T = base;
   kk_out = kk;
 }
 
-// Ordered selection write: keys i < count in index order; every key > T and
-// the first kk keys == T go to out[] in that order, as idx(i).  Wavefront w
-// owns a contiguous range of i; counts, an exclusive scan over wavefronts,
-// then ballots place each index.
+// Ordered selection write over keys read from memory (the fallback's):
+// keys i < count in index order; every key > T and the first kk keys == T go
+// to out[] in that order, as idx(i).  Wavefront w owns a contiguous range of
+// i; counts, a prefix over wavefronts, then ballots place each index.
 template <typename KeyFn, typename IdxFn>
-__device__ void ordered_write(KeyFn key, IdxFn idx, int count, uint32_t T, int kk, int* wave_gt,
-                              int* wave_eq, int32_t* out) {
+__device__ void ordered_write_mem(KeyFn key, IdxFn idx, int count, uint32_t T, int kk, int* wave_gt,
+                                  int* wave_eq, int32_t* out) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
   const int per = ((count + kTopkWaves - 1) / kTopkWaves + kWave - 1) / kWave * kWave;
@@ -319,7 +484,7 @@ __device__ void ordered_write(KeyFn key, IdxFn idx, int count, uint32_t T, int k
     gt_before += wave_gt[k];
     eq_before += wave_eq[k];
   }
-  int pos = gt_before + (eq_before < kk ? eq_before : kk);  // selections before this wave
+  int pos = gt_before + (eq_before < kk ? eq_before : kk);
   int eq_seen = eq_before;
   for (int i0 = lo; i0 < hi; i0 += kWave) {
     const int i = i0 + lane;
@@ -334,14 +499,13 @@ __device__ void ordered_write(KeyFn key, IdxFn idx, int count, uint32_t T, int k
     pos += __popcll(take_mask);
     eq_seen += __popcll(eq_mask);
   }
-  __syncthreads();
 }
 
-// Workspace of the top-k (per row): the threshold T0, per-chunk candidate
-// counts and largest candidate keys, and per-chunk candidate slots of (key,
-// index) pairs.
+// Workspace of the top-k (per row): the arrival counter of the row's chunk
+// workgroups (zero between calls), per-chunk candidate counts and largest
+// candidate keys, and per-chunk candidate slots of (key, index) pairs.
 struct TopkWs {
-  uint32_t* t0;     // [B]
+  int* arrive;      // [B]
   int* counts;      // [B, chunks]
   uint32_t* cmax;   // [B, chunks]
   uint2* cand;      // [B, chunks, kChunkKeys]
@@ -350,29 +514,40 @@ struct TopkWs {
 
 __host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys - 1) / kChunkKeys; }
 
-// 1. Threshold and compaction, one launch: one workgroup per chunk of
-// kChunkKeys keys of a row.  Each workgroup places the row's threshold T0
-// itself -- every one from the same sample with the same exact select, so all
-// agree -- while its chunk's keys are in flight, then moves every key >= T0,
-// with its index and in index order, to the chunk's slots.  Rows of at most
-// kCandCap keys take every key as a candidate (T0 = 0).  Longer rows: T0 is
-// the key of rank 1.5 x (the sample's share of k) + 32 in a sample of kSample
-// keys (runs of 4 adjacent keys spread evenly over a 16-byte aligned row, else
-// single keys at an even stride), placed by two passes of the radix select in
-// LDS: the lower edge of the bin (24 bits below the sample's shared leading
-// bits) that holds that rank -- about 1.5 k candidates, with margin.  Each
-// workgroup also records its candidates' largest key, which with T0 bounds
-// the select kernel's keys.  (As separate launches, the one-workgroup
-// threshold kernel took 9.2 us and the compaction 5.0 us behind it.)
+// The top-k of a row, one launch: one workgroup per chunk of kChunkKeys keys.
+//
+// 1. Threshold.  Each workgroup places the row's threshold T0 itself -- every
+//    one from the same sample with the same passes, so all agree -- while its
+//    chunk's keys are in flight.  Rows of at most kCandCap keys take every key
+//    as a candidate (T0 = 0).  Longer rows: T0 is the lower edge of the bin
+//    holding the key of rank 1.5 x (the sample's share of k) + 32 in a sample
+//    of kSample keys (runs of 4 adjacent keys spread evenly over a 16-byte
+//    aligned row, else single keys at an even stride) -- after one pass of
+//    radix_select_regs (bins of the sample's span / 4096) when that bin holds
+//    at most 32 sample keys, else after a second (span / 2^24): about 1.5 k
+//    candidates, with margin.
+// 2. Compaction.  The workgroup moves its keys >= T0, with their indices and
+//    in index order, to the chunk's slots, with their count and largest key.
+// 3. Selection, by the row's last workgroup to finish (an arrival counter;
+//    its stores released to every XCD before the count, the others' acquired
+//    after it): between k and kCandCap candidates are gathered, in chunk (so
+//    index) order, straight into registers, kRegKeys per thread; the exact
+//    select over the range [T0, largest candidate] and the ordered write run
+//    from there.  Otherwise -- a threshold the sample misplaced -- the exact
+//    selection runs over the row in memory.
+// The counter is back at zero when the launch ends.
 template <bool VEC>
-__global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
-    const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws, int cap,
-    int K) {
-  __shared__ uint32_t sample[kSample];
-  __shared__ __align__(16) int hist[kRadixBins];
-  __shared__ int scan_tmp[kTopkWaves];
-  __shared__ uint32_t wave_max[kTopkWaves];
-  __shared__ int found[2];
+__global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
+    const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws,
+    int32_t* __restrict__ sel, int32_t* __restrict__ sel_lens, int cap, int K) {
+  __shared__ __align__(16) int hist2[2 * kRadixBins];
+  __shared__ __align__(16) int totals[kTopkWaves];
+  __shared__ __align__(16) int scan_tmp[kTopkWaves];
+  __shared__ __align__(16) uint32_t wave_red[2 * kTopkWaves];
+  __shared__ int chunk_off[kChunksPerThread * kTopkThreads + 1];
+  __shared__ __align__(16) int wcount[2 * kTopkWaves];
+  __shared__ int found[3];
+  __shared__ int is_last;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
@@ -380,14 +555,20 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
   const int chunk = blockIdx.x;
   int n = lens[b];
   n = n < 0 ? 0 : (n > cap ? cap : n);
-  if (n <= K) return;  // the select kernel takes every key; nothing to compact
+  int32_t* ob = sel + static_cast<size_t>(b) * K;
+  if (n <= K) {  // every key is selected
+    if (chunk == 0) {
+      for (int i = tid; i < n; i += kTopkThreads) ob[i] = i;
+      if (tid == 0) sel_lens[b] = n;
+    }
+    return;
+  }
+  const int nch = (n + kChunkKeys - 1) / kChunkKeys;
   const int c0 = chunk * kChunkKeys;
   if (c0 >= n) return;
   const float* sb = scores + static_cast<size_t>(b) * cap;
 
-  // this chunk's keys c0 + 4 tid .. + 3, loaded first so that they are in
-  // flight while the threshold is placed
-  static_assert(kChunkKeys == 4 * kTopkThreads, "four keys of the chunk per thread");
+  // this chunk's keys c0 + 4 tid .. + 3, in flight while T0 is placed
   const int i = c0 + 4 * tid;
   float v[4];
   if (VEC && i + 3 < n) {
@@ -400,40 +581,53 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
 
   uint32_t T0 = 0u;
   if (n > kCandCap) {
-    constexpr int kPer = kSample / kTopkThreads;
-    float sv[kPer];
+    uint32_t sk[4];
     if (VEC) {
-      static_assert(kSample / kTopkThreads == 4, "one float4 of sample keys per thread");
-      // runs of kPer adjacent keys, one 16-byte load per thread, spread evenly
+      // runs of 4 adjacent keys, one 16-byte load per thread, spread evenly
       // over the row (n > kCandCap, so every run lies inside it)
-      const int j0 =
-          static_cast<int>(static_cast<long long>(tid) * n / kTopkThreads) & ~(kPer - 1);
-      const float4 f = *reinterpret_cast<const float4*>(sb + j0);
-      sv[0] = f.x;
-      sv[1] = f.y;
-      sv[2] = f.z;
-      sv[3] = f.w;
+      const int j0 = static_cast<int>(static_cast<long long>(tid) * n / kTopkThreads) & ~3;
+      const f32x4 f = *reinterpret_cast<const f32x4*>(sb + j0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sk[k] = order_key(f[k]);
     } else {
 #pragma unroll
-      for (int k = 0; k < kPer; ++k) {
+      for (int k = 0; k < 4; ++k) {
         const int j = tid + k * kTopkThreads;
-        sv[k] = sb[static_cast<int>(static_cast<long long>(j) * n / kSample)];
+        sk[k] = order_key(sb[static_cast<int>(static_cast<long long>(j) * n / kSample)]);
       }
     }
+    uint32_t lo = sk[0];
+    uint32_t hi = sk[0];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) sample[tid * kPer + k] = order_key(sv[k]);
+    for (int k = 1; k < 4; ++k) {
+      lo = sk[k] < lo ? sk[k] : lo;
+      hi = sk[k] > hi ? sk[k] : hi;
+    }
+    lo = wave_min_u32(lo);
+    hi = wave_max_u32(hi);
+    if (lane == 0) {
+      wave_red[wv] = lo;
+      wave_red[kTopkWaves + wv] = hi;
+    }
     __syncthreads();
+    lo = 0xFFFFFFFFu;
+    hi = 0u;
+#pragma unroll
+    for (int k = 0; k < kTopkWaves; ++k) {
+      lo = wave_red[k] < lo ? wave_red[k] : lo;
+      hi = wave_red[kTopkWaves + k] > hi ? wave_red[kTopkWaves + k] : hi;
+    }
     long long r = (static_cast<long long>(K) * kSample + n - 1) / n;
     r = r + r / 2 + 32;
     const int want = static_cast<int>(r > kSample ? kSample : r);
     int unused;
-    radix_select([&](int k) { return sample[k]; }, kSample, want, hist, scan_tmp, found,
-                 false, 0u, 0u, 2, T0, unused);
+    // a second pass only when the first one's crossing bin holds more than
+    // 32 sample keys (about 1,000 more candidates than the rank asks for)
+    radix_select_regs(sk, 0xFu, 4, want, hist2, totals, found, lo, hi, 2, 32, T0, unused);
   }
-  if (chunk == 0 && tid == 0) ws.t0[b] = T0;
 
-  // keys >= T0 in index order: a scan over the workgroup places each thread's
-  // candidates; the same barrier collects the chunk's largest candidate key
+  // keys >= T0 in index order: a scan over the workgroup places each
+  // thread's candidates; the same barrier collects the chunk's largest
   bool in[4];
   int cnt = 0;
   uint32_t mx = 0u;
@@ -444,24 +638,26 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
     cnt += in[e] ? 1 : 0;
     mx = in[e] && u > mx ? u : mx;
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t y = static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), o));
-    mx = y > mx ? y : mx;
-  }
+  mx = wave_max_u32(mx);
   const int inc = wave_inclusive_scan(cnt, lane);
   if (lane == kWave - 1) scan_tmp[wv] = inc;
-  if (lane == 0) wave_max[wv] = mx;
+  if (lane == 0) wave_red[wv] = mx;
   __syncthreads();
   int at = inc - cnt;
   int all = 0;
   uint32_t cmax = 0u;
 #pragma unroll
-  for (int k = 0; k < kTopkWaves; ++k) {
-    const int t = scan_tmp[k];
-    at += k < wv ? t : 0;
-    all += t;
-    cmax = wave_max[k] > cmax ? wave_max[k] : cmax;
+  for (int k4 = 0; k4 < kTopkWaves / 4; ++k4) {
+    const int4 t4 = reinterpret_cast<const int4*>(scan_tmp)[k4];
+    const uint4 m4 = reinterpret_cast<const uint4*>(wave_red)[k4];
+    const int t[4] = {t4.x, t4.y, t4.z, t4.w};
+    const uint32_t m[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      at += 4 * k4 + e < wv ? t[e] : 0;
+      all += t[e];
+      cmax = m[e] > cmax ? m[e] : cmax;
+    }
   }
   uint2* slots = ws.cand + (static_cast<size_t>(b) * ws.chunks + chunk) * kChunkKeys;
 #pragma unroll
@@ -475,45 +671,31 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_compact_kernel(
     ws.counts[static_cast<size_t>(b) * ws.chunks + chunk] = all;
     ws.cmax[static_cast<size_t>(b) * ws.chunks + chunk] = cmax;
   }
-}
 
-// 3. Select: one workgroup per row.  The chunks' candidates, in chunk order
-// (index order), go to LDS when there are between k and kCandCap of them;
-// the exact selection and the ordered write run there.  Otherwise -- a
-// threshold that the sample misplaced -- the exact selection runs over the
-// row in memory.
-__global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
-    const float* __restrict__ scores, const int32_t* __restrict__ lens, TopkWs ws,
-    int32_t* __restrict__ sel, int32_t* __restrict__ sel_lens, int cap, int K) {
-  __shared__ uint32_t cand_key[kCandCap];
-  __shared__ int32_t cand_idx[kCandCap];
-  __shared__ __align__(16) int hist[kRadixBins];
-  __shared__ int scan_tmp[kTopkWaves];
-  __shared__ int found[2];
-  __shared__ int wave_gt[kTopkWaves];
-  __shared__ int wave_eq[kTopkWaves];
-  __shared__ uint32_t wave_max[kTopkWaves];
-  __shared__ int chunk_off[kChunksPerThread * kTopkThreads + 1];
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wv = tid / kWave;
-  const int b = blockIdx.x;
-  int n = lens[b];
-  n = n < 0 ? 0 : (n > cap ? cap : n);
-  const float* sb = scores + static_cast<size_t>(b) * cap;
-  int32_t* ob = sel + static_cast<size_t>(b) * K;
-  if (n <= K) {  // every key is selected
-    for (int i = tid; i < n; i += kTopkThreads) ob[i] = i;
-    if (tid == 0) sel_lens[b] = n;
-    return;
+  // Publish, then count the arrival: every wavefront waits for its stores to
+  // reach its XCD's L2, one release fence writes that L2 back for the other
+  // XCDs, and the last workgroup to arrive acquires theirs.
+  wait_vmem_all();
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    const int last = atomicAdd(&ws.arrive[b], 1) == nch - 1;
+    if (last) {
+      atomicExch(&ws.arrive[b], 0);  // zero again for the next call
+      __threadfence();
+    }
+    is_last = last;
   }
-  // candidate offsets of the row's chunks (up to 2048 chunks in LDS), and the
-  // largest candidate key, which with T0 bounds every candidate
-  const int nch = (n + kChunkKeys - 1) / kChunkKeys;
-  const int* cnt = ws.counts + static_cast<size_t>(b) * ws.chunks;
-  const uint32_t* cmx = ws.cmax + static_cast<size_t>(b) * ws.chunks;
-  const uint32_t t0 = ws.t0[b];
+  __syncthreads();
+  if (!is_last) return;
+
+  // ---- selection over the row's candidates ----
+  // candidate offsets of the row's chunks and the largest candidate key,
+  // which with T0 bounds every candidate
+  const int* cnt_row = ws.counts + static_cast<size_t>(b) * ws.chunks;
+  const uint32_t* cmx_row = ws.cmax + static_cast<size_t>(b) * ws.chunks;
   int C = 0;
+  uint32_t hi = 0u;
   bool fits = nch <= kChunksPerThread * kTopkThreads;
   if (fits) {
     int c2[kChunksPerThread];
@@ -522,17 +704,13 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
 #pragma unroll
     for (int e = 0; e < kChunksPerThread; ++e) {
       const int ch = kChunksPerThread * tid + e;
-      c2[e] = ch < nch ? cnt[ch] : 0;
-      const uint32_t m = ch < nch ? cmx[ch] : 0u;
+      c2[e] = ch < nch ? cnt_row[ch] : 0;
+      const uint32_t m = ch < nch ? cmx_row[ch] : 0u;
       m2 = m > m2 ? m : m2;
       mine += c2[e];
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const uint32_t y = static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o));
-      m2 = y > m2 ? y : m2;
-    }
-    if (lane == 0) wave_max[wv] = m2;  // read after the scan's barriers
+    m2 = wave_max_u32(m2);
+    if (lane == 0) wave_red[wv] = m2;  // read after the scan's barriers
     int total;
     int run = block_exclusive_scan(mine, scan_tmp, total);
 #pragma unroll
@@ -542,51 +720,58 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_select_kernel(
       run += c2[e];
     }
     if (tid == 0) chunk_off[nch] = total;
+#pragma unroll
+    for (int k = 0; k < kTopkWaves; ++k) hi = wave_red[k] > hi ? wave_red[k] : hi;
     C = total;
     fits = C >= K && C <= kCandCap;
-    __syncthreads();
+    __syncthreads();  // chunk_off complete
   }
   uint32_t T;
   int kk;
   if (fits) {
-    // flat candidate j -> its chunk by binary search over the offsets; every
-    // thread's loads (at most kCandCap / kTopkThreads) are issued before the
-    // first is stored to LDS, so the gather costs one memory round trip
-    constexpr int kPerThread = kCandCap / kTopkThreads;
-    uint2 e[kPerThread];
+    // wavefront w holds candidates w * per .. + per - 1, 64 per register
+    // (nregs registers); the chunk of its first candidate by binary search,
+    // then each lane walks forward over the offsets (its candidates rise by
+    // 64 per register, past a chunk or two).  Every load is issued before
+    // the first is used: one memory round trip.
+    const int per = ((C + kTopkWaves - 1) / kTopkWaves + kWave - 1) / kWave * kWave;
+    const int nregs = per / kWave;
+    const int j0 = wv * per;
+    int ch = 0;
+    {
+      int hi_c = nch;
+      while (hi_c - ch > 1) {
+        const int mid = (ch + hi_c) >> 1;
+        if (chunk_off[mid] <= j0) ch = mid; else hi_c = mid;
+      }
+    }
+    uint2 e[kRegKeys];
+    uint32_t valid = 0u;
 #pragma unroll
-    for (int r = 0; r < kPerThread; ++r) {
-      const int j = tid + r * kTopkThreads;
-      if (j < C) {
-        int lo = 0, hi = nch;
-        while (hi - lo > 1) {
-          const int mid = (lo + hi) >> 1;
-          if (chunk_off[mid] <= j) lo = mid; else hi = mid;
+    for (int r = 0; r < kRegKeys; ++r) {
+      e[r] = make_uint2(0u, 0u);
+      if (r < nregs) {
+        const int j = j0 + kWave * r + lane;
+        if (j < C) {
+          while (chunk_off[ch + 1] <= j) ++ch;
+          e[r] = ws.cand[(static_cast<size_t>(b) * ws.chunks + ch) * kChunkKeys + (j - chunk_off[ch])];
+          valid |= 1u << r;
         }
-        e[r] = ws.cand[(static_cast<size_t>(b) * ws.chunks + lo) * kChunkKeys +
-                       (j - chunk_off[lo])];
       }
     }
+    uint32_t key[kRegKeys];
+    int32_t idx[kRegKeys];
 #pragma unroll
-    for (int r = 0; r < kPerThread; ++r) {
-      const int j = tid + r * kTopkThreads;
-      if (j < C) {
-        cand_key[j] = e[r].x;
-        cand_idx[j] = static_cast<int32_t>(e[r].y);
-      }
+    for (int r = 0; r < kRegKeys; ++r) {
+      key[r] = e[r].x;
+      idx[r] = static_cast<int32_t>(e[r].y);
     }
-    __syncthreads();
-    uint32_t hi = 0u;
-#pragma unroll
-    for (int k = 0; k < kTopkWaves; ++k) hi = wave_max[k] > hi ? wave_max[k] : hi;
-    auto lds_key = [&](int i) { return cand_key[i]; };
-    auto lds_idx = [&](int i) { return cand_idx[i]; };
-    radix_select(lds_key, C, K, hist, scan_tmp, found, true, t0, hi, 0, T, kk);
-    ordered_write(lds_key, lds_idx, C, T, kk, wave_gt, wave_eq, ob);
+    radix_select_regs(key, valid, nregs, K, hist2, totals, found, T0, hi, 0, 0, T, kk);
+    ordered_write_regs(key, idx, valid, nregs, T, kk, wcount, ob);
   } else {
     auto mem_key = [&](int i) { return order_key(sb[i]); };
-    radix_select(mem_key, n, K, hist, scan_tmp, found, false, 0u, 0u, 0, T, kk);
-    ordered_write(mem_key, [](int i) { return i; }, n, T, kk, wave_gt, wave_eq, ob);
+    radix_select_mem(mem_key, n, K, hist2, scan_tmp, found, T, kk);
+    ordered_write_mem(mem_key, [](int i) { return i; }, n, T, kk, wcount, wcount + kTopkWaves, ob);
   }
   if (tid == 0) sel_lens[b] = K;
 }
@@ -652,24 +837,20 @@ extern "C" int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* 
   TopkWs ws;
   ws.chunks = topk_chunks(cap);
   char* p = static_cast<char*>(workspace);
-  const size_t t0_bytes = (static_cast<size_t>(batch) * 4 + 255) & ~size_t(255);
+  const size_t arrive_bytes = (static_cast<size_t>(batch) * 4 + 255) & ~size_t(255);
   const size_t per_chunk_bytes = (static_cast<size_t>(batch) * ws.chunks * 4 + 255) & ~size_t(255);
-  ws.t0 = reinterpret_cast<uint32_t*>(p);
-  ws.counts = reinterpret_cast<int*>(p + t0_bytes);
-  ws.cmax = reinterpret_cast<uint32_t*>(p + t0_bytes + per_chunk_bytes);
-  ws.cand = reinterpret_cast<uint2*>(p + t0_bytes + 2 * per_chunk_bytes);
+  ws.arrive = reinterpret_cast<int*>(p);
+  ws.counts = reinterpret_cast<int*>(p + arrive_bytes);
+  ws.cmax = reinterpret_cast<uint32_t*>(p + arrive_bytes + per_chunk_bytes);
+  ws.cand = reinterpret_cast<uint2*>(p + arrive_bytes + 2 * per_chunk_bytes);
   const bool vec = cap % 4 == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0;
-  const dim3 cgrid(static_cast<unsigned>(ws.chunks), static_cast<unsigned>(batch));
+  const dim3 grid(static_cast<unsigned>(ws.chunks), static_cast<unsigned>(batch));
   if (vec) {
-    hipLaunchKernelGGL(dsa_topk_compact_kernel<true>, cgrid, dim3(kTopkThreads), 0, stream,
-                       scores, lens, ws, cap, k);
+    hipLaunchKernelGGL(dsa_topk_kernel<true>, grid, dim3(kTopkThreads), 0, stream, scores, lens,
+                       ws, sel, sel_lens, cap, k);
   } else {
-    hipLaunchKernelGGL(dsa_topk_compact_kernel<false>, cgrid, dim3(kTopkThreads), 0, stream,
-                       scores, lens, ws, cap, k);
+    hipLaunchKernelGGL(dsa_topk_kernel<false>, grid, dim3(kTopkThreads), 0, stream, scores, lens,
+                       ws, sel, sel_lens, cap, k);
   }
-  int rc = VOOM_LAUNCH_CHECK("dsa_topk: threshold + compaction kernel launch");
-  if (rc) return rc;
-  hipLaunchKernelGGL(dsa_topk_select_kernel, dim3(static_cast<unsigned>(batch)),
-                     dim3(kTopkThreads), 0, stream, scores, lens, ws, sel, sel_lens, cap, k);
-  return VOOM_LAUNCH_CHECK("dsa_topk: select kernel launch");
+  return VOOM_LAUNCH_CHECK("dsa_topk: kernel launch");
 }
