@@ -604,33 +604,6 @@ void mla_group64_kernel(MlaArgs a) {
   float M[2] = {-INFINITY, -INFINITY};
   float l_run = 0.f;
 
-  if constexpr (SPARSE) {
-    if (w == 0) {
-      int pos[kPre];
-#pragma unroll
-      for (int k = 0; k < kPre; ++k) {
-        const int tok = (t_lo + k) * kTile + lane;
-        pos[k] = (t_lo + k < t_hi && tok < ctx)
-                     ? a.sel[static_cast<size_t>(b) * a.sel_stride + tok]
-                     : -1;
-      }
-#pragma unroll
-      for (int k = 0; k < kPre; ++k) {
-        // a position past the table reads from slot 0 (the slot an invalid
-        // table entry falls back to); no position: a row of zeros
-        const int page = pos[k] >> a.pt_shift;
-        int slot = (pos[k] >= 0 && page < a.max_pages) ? trow[page] : 0;
-        if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
-        pre_off[k][lane] =
-            pos[k] < 0 ? 0xFFFFFFF0u
-                       : static_cast<uint32_t>(((static_cast<long long>(slot) << a.pt_shift) +
-                                                (pos[k] & ((1 << a.pt_shift) - 1))) *
-                                               (kLat * 2));
-      }
-    }
-    lds_barrier();
-  }
-
   // LDS tile layout: nine column blocks of 8 chunks (128 bytes of a row)
   // for all 64 rows, 8 KiB each; row r of block cb holds chunks 8 cb .. 8 cb
   // + 7 of token row r at r * 128 bytes, chunk c at position c ^
@@ -642,6 +615,61 @@ void mla_group64_kernel(MlaArgs a) {
   const int ld_col = 16 * ((lane & 7) ^ group_swizzle(ld_row));
   const int ld_base0 = ld_row * (kLat * 2) + ld_col;
   const int ld_base1 = ld_base0 + 32 * (kLat * 2);
+
+  // The group's q rows (64 x 576, contiguous in memory) go through the
+  // second tile buffer in the tile layout: one coalesced stream instead of 36
+  // row-strided loads per wavefront, and the score operands are then read
+  // with the conflict-free pattern of the latent rows (row 32 hh + l32).
+  auto load_q = [&]() {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.q + (static_cast<size_t>(b) * a.H + head0) * kLat),
+        static_cast<short>(0), HG * kLat * 2, 0x00020000);
+#pragma unroll
+    for (int k = 0; k < kGLoads; ++k) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile_b + (w + kGWaves * k) * 512), 16,
+                                               ((k & 1) ? ld_base1 : ld_base0) + 128 * (k >> 1),
+                                               0, 0, 0);
+    }
+  };
+
+  if constexpr (SPARSE) {
+    // q needs no selection: its loads go out first, under the selection ->
+    // table -> row offset chain
+    load_q();
+    if (w == 0) {
+      // Both lookups load unconditionally (index 0 where there is nothing to
+      // look up), so each is one batch of loads with one wait; loads under a
+      // branch were waited for one by one.
+      int pos[kPre];
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) {
+        const int tok = (t_lo + k) * kTile + lane;
+        const bool used = t_lo + k < t_hi && tok < ctx;
+        const int p = a.sel[static_cast<size_t>(b) * a.sel_stride + (used ? tok : 0)];
+        pos[k] = used ? p : -1;
+      }
+      int tab_slot[kPre];
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) {
+        const int page = pos[k] >> a.pt_shift;
+        tab_slot[k] = trow[pos[k] >= 0 && page < a.max_pages ? page : 0];
+      }
+#pragma unroll
+      for (int k = 0; k < kPre; ++k) {
+        // a position past the table reads from slot 0 (the slot an invalid
+        // table entry falls back to); no position: a row of zeros
+        const int page = pos[k] >> a.pt_shift;
+        int slot = (pos[k] >= 0 && page < a.max_pages) ? tab_slot[k] : 0;
+        if (static_cast<unsigned>(slot) >= static_cast<unsigned>(a.num_slots)) slot = 0;
+        pre_off[k][lane] =
+            pos[k] < 0 ? 0xFFFFFFF0u
+                       : static_cast<uint32_t>(((static_cast<long long>(slot) << a.pt_shift) +
+                                                (pos[k] & ((1 << a.pt_shift) - 1))) *
+                                               (kLat * 2));
+      }
+    }
+    lds_barrier();
+  }
 
   // Source of a tile's direct-to-LDS loads: a buffer descriptor and two
   // per-lane offsets (rows 8 w + lane / 8 and 32 rows further); load k adds
@@ -894,25 +922,14 @@ void mla_group64_kernel(MlaArgs a) {
   // so the loop ends.  The accumulators are only ever zeroed or fed to MFMAs,
   // which keeps them in accumulation registers.
   //
-  // The group's q rows (64 x 576, contiguous in memory) first go through the
-  // second tile buffer in the tile layout: one coalesced stream instead of 36
-  // row-strided loads per wavefront, and the score operands are then read
-  // with the conflict-free pattern of the latent rows (row 32 hh + l32).
-  // The first tile's loads are issued right behind q's (its table lookup
-  // first: that load's wait would also wait for q), and only q is waited for
+  // The first tile's loads are issued right behind q's (dense: its table
+  // lookup first, as that load's wait would also wait for q; sparse: q went
+  // out before the row offsets were looked up), and only q is waited for
   // before its rows are read out, so the tile's latency overlaps that.
   {
     uint32_t off[2];
     const __amdgpu_buffer_rsrc_t r0 = tile_src(t_lo, off);  // empty past t_hi
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.q + (static_cast<size_t>(b) * a.H + head0) * kLat),
-        static_cast<short>(0), HG * kLat * 2, 0x00020000);
-#pragma unroll
-    for (int k = 0; k < kGLoads; ++k) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile_b + (w + kGWaves * k) * 512), 16,
-                                               ((k & 1) ? ld_base1 : ld_base0) + 128 * (k >> 1),
-                                               0, 0, 0);
-    }
+    if constexpr (!SPARSE) load_q();
 #pragma unroll
     for (int k = 0; k < kGLoads; ++k) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r0, (lds_void*)(tile_a + (w + kGWaves * k) * 512),
