@@ -1190,14 +1190,57 @@ def bench_e2e(cpu_sample: bool) -> dict:
             if a != b:
                 break
             agree += 1
+        # The random-init model's greedy stream is nearly constant, so the
+        # greedy agreement pins little: teacher-force 16 random tokens after
+        # the prompt through both models and compare every logit row (the
+        # prompt's 512 rows from the paged prefill, the 16 decode rows from
+        # the captured graph the timing replays).
+        forced = torch.randint(0, cfg.vocab_size, (16,), generator=torch.Generator().manual_seed(7))
+        with torch.no_grad():
+            out = m(prompt, use_cache=True)
+            ref_rows = [out.logits[0]]
+            past = out.past_key_values
+            for t in forced.tolist():
+                out = m(torch.tensor([[t]]), past_key_values=past, use_cache=True)
+                past = out.past_key_values
+                ref_rows.append(out.logits[0])
+        ref_l = torch.cat(ref_rows).numpy()                 # 512 + 16 rows
+        kv_t = dec.new_cache(page_positions=64)
+        got_rows = [dec.forward(prompt.cuda(), kv_t)[0].cpu()]
+        logits = torch.empty((1, cfg.vocab_size), dtype=torch.float32, device="cuda")
+        graph, tok, _ = dec.capture_decode(kv_t, 512 + 16, logits=logits)
+        # row 512 + i is the logits after forced token i; the decode input
+        # of step i is forced[i]
+        for t in forced.tolist():
+            tok.fill_(t)
+            graph.replay()
+            kv_t.advance(1)
+            got_rows.append(logits.cpu().clone())
+        got_l = torch.cat(got_rows).numpy()
+        import numpy as np
+
+        rel = np.linalg.norm(got_l - ref_l, axis=-1) / np.linalg.norm(ref_l, axis=-1)
+        res["teacher_forced_vs_cpu_fp32"] = {
+            "rows": int(ref_l.shape[0]),
+            "rel_l2_max": float(rel.max()),
+            "abs_max": float(np.abs(got_l - ref_l).max()),
+            "argmax_agreement": float((got_l.argmax(-1) == ref_l.argmax(-1)).mean()),
+            "distinct_reference_argmax": int(len(set(ref_l.argmax(-1).tolist()))),
+        }
+        del graph, kv_t
         res["cpu_baseline"] = {"value": n_cpu / dt, "unit": "tokens/s (decode)",
                                "cores": torch.get_num_threads(), "kind": "port",
                                "sample": f"{n_cpu} greedy decode steps after the same 512-token "
                                          "prompt, Hugging Face LlamaForCausalLM fp32 on the "
                                          "host CPU with its KV cache"}
         res["greedy_prefix_agreement_vs_cpu_fp32"] = agree
+        res["greedy_distinct_tokens"] = len(set(toks))
+        tf = res["teacher_forced_vs_cpu_fp32"]
         log(f"config 1: cpu baseline {n_cpu / dt:.1f} tok/s; greedy tokens agree for the first "
-            f"{agree} of {len(ref_toks)}")
+            f"{agree} of {len(ref_toks)} ({len(set(toks))} distinct tokens in the GPU stream); "
+            f"teacher-forced over {tf['rows']} rows: rel L2 max {tf['rel_l2_max']:.4f}, "
+            f"argmax agreement {tf['argmax_agreement']:.3f} "
+            f"({tf['distinct_reference_argmax']} distinct reference argmax)")
     del dec, weights, kv, kv_e
     torch.cuda.empty_cache()
     return res
