@@ -70,15 +70,14 @@ def _used_on(stream: torch.cuda.Stream | None, *tensors: torch.Tensor | None) ->
             t.record_stream(stream)
 
 
-def workspace(device: torch.device, nbytes: int, tag: int = 0, zeroed: bool = False) -> torch.Tensor:
-    """Per-device cached uint8 scratch tensor of at least ``nbytes`` bytes;
-    zeroed=True clears a newly allocated one (for kernels that keep counters
-    in it and leave them at zero)."""
+def workspace(device: torch.device, nbytes: int, tag: int = 0) -> torch.Tensor:
+    """Per-device cached uint8 scratch tensor of at least ``nbytes`` bytes,
+    zeroed when it is allocated: the DSA top-k keeps arrival counters in its
+    workspace, which must start at zero (each call leaves them zero)."""
     key = (device.index if device.index is not None else torch.cuda.current_device(), tag)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        alloc = torch.zeros if zeroed else torch.empty
-        ws = alloc(max(nbytes, 256), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 
@@ -643,7 +642,7 @@ def dsa_topk(scores: torch.Tensor, lens: torch.Tensor, k: int, *,
     _require(sel.dtype == sel_lens.dtype == torch.int32 and tuple(sel.shape) == (B, int(k))
              and tuple(sel_lens.shape) == (B,), "sel [B, k] and sel_lens [B] int32")
     need = int(_lib.lib().voom_dsa_topk_workspace_bytes(B, cap))
-    ws = workspace(dev, need, tag=4, zeroed=True)   # the row counters start at zero
+    ws = workspace(dev, need, tag=4)
     _lib.call("voom_dsa_topk", _ptr(scores), _ptr(lens), _ptr(sel), _ptr(sel_lens), _ptr(ws),
               need, B, cap, int(k), _stream(stream))
     return sel, sel_lens
