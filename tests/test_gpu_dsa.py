@@ -16,7 +16,7 @@ import torch
 
 from oracle import dsa as odsa
 from oracle import mla as omla
-from voom_amd import ops, synthetic
+from voom_amd import _lib, ops, synthetic
 
 pytestmark = pytest.mark.gpu
 
@@ -277,3 +277,38 @@ def test_topk_random_rows_lengths_and_distributions():
             rows.append(r.astype(np.float32))
         print(f"[dsa] random case {case}: k={k} cap={cap} lens={lens}", flush=True)
         _check_topk(np.stack(rows), lens, k)
+
+
+def test_topk_workspace_counters_return_to_zero():
+    """The top-k is one launch: the chunk workgroups of a row count their
+    arrival in the workspace and the last one selects.  The counters must be
+    zero again after every call (the next call relies on it), whatever the
+    rows: many rows per call, rows on each of the three paths (every key
+    selected, every key a candidate, the sampled threshold), and calls of
+    different batch sizes back to back on the same workspace."""
+    print("[dsa] topk counters", flush=True)
+    rng = np.random.default_rng(404)
+    cap, k = 70000, 512
+    need = _lib.lib().voom_dsa_topk_workspace_bytes(16, cap)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    for B in (16, 3, 16, 1):
+        lens = [int(x) for x in rng.integers(1, cap + 1, size=B)]
+        lens[0] = cap
+        if B > 2:
+            lens[1], lens[2] = 300, 9000          # every key selected; every key a candidate
+        scores = (rng.standard_normal((B, cap)) * 2).astype(np.float32)
+        sc = torch.from_numpy(scores).cuda()
+        ln = torch.tensor(lens, dtype=torch.int32, device="cuda")
+        sel = torch.empty((B, k), dtype=torch.int32, device="cuda")
+        sl = torch.empty((B,), dtype=torch.int32, device="cuda")
+        for _ in range(2):
+            _lib.call("voom_dsa_topk", sc.data_ptr(), ln.data_ptr(), sel.data_ptr(),
+                          sl.data_ptr(), ws.data_ptr(), need, B, cap, k,
+                          torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            assert int(ws[:4 * 16].view(torch.int32).abs().sum()) == 0, "counters left non-zero"
+        got, got_l = sel.cpu().numpy(), sl.cpu().numpy()
+        for b in range(B):
+            want = odsa.topk(scores[b], lens[b], k)
+            assert got_l[b] == len(want)
+            assert got[b, :got_l[b]].tolist() == want.tolist(), (B, b, lens[b])
