@@ -1125,6 +1125,59 @@ __device__ __forceinline__ void merge_ranges(const void* __restrict__ part_o,
   }
 }
 
+// At most kSmallRanges fp16 range partials (the usual case): the statistics
+// and every partial row are loaded before any is used -- one memory round
+// trip, where merge_ranges waits for the statistics before it loads a row --
+// and combined with the same arithmetic in the same order as merge_ranges
+// (weights 2^(m - M) l 2^e, lane r holding range r; rows r >= NR are copies
+// of row NR - 1 with weight 0), so both give the same bits.
+constexpr int kSmallRanges = 16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+struct SmallRanges {
+  f32x4 st;  // lane r < NR: (m, l, e, 0) of range r
+  f16x8 rows[kSmallRanges];
+};
+
+__device__ __forceinline__ void load_small_ranges(const void* __restrict__ part_o16,
+                                                  const float* __restrict__ part_ml, int b,
+                                                  int h, int H, int NR, int lane,
+                                                  SmallRanges& sr) {
+  sr.st = f32x4{-INFINITY, 0.f, 0.f, 0.f};
+  if (lane < NR) {
+    sr.st = reinterpret_cast<const f32x4*>(part_ml)[(static_cast<size_t>(b) * NR + lane) * H + h];
+  }
+#pragma unroll
+  for (int r = 0; r < kSmallRanges; ++r) {
+    const int rr = r < NR ? r : NR - 1;
+    sr.rows[r] = *reinterpret_cast<const f16x8*>(
+        static_cast<const _Float16*>(part_o16) +
+        ((static_cast<size_t>(b) * NR + rr) * H + h) * kC + lane * kDPL);
+  }
+}
+
+__device__ __forceinline__ void combine_small_ranges(const SmallRanges& sr, int NR,
+                                                     f32x4 (&acc)[kDPL / 4], float& M, float& L) {
+  const float m = sr.st[0], l = sr.st[1], e = sr.st[2];
+  M = wave_max_uniform(m);
+  const float wl = m == -INFINITY ? 0.f : fast_exp2(m - M);
+  L = wave_sum_uniform(l * wl);
+  const float wrow = wl * l * fast_exp2(e);
+  acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (M == -INFINITY) return;  // no tokens in any range
+#pragma unroll
+  for (int r = 0; r < kSmallRanges; ++r) {
+    const float wk = r < NR ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                  __builtin_bit_cast(int, wrow), r))
+                            : 0.f;
+    const f16x8& x = sr.rows[r];
+    acc[0] += f32x4{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
+                    static_cast<float>(x[3])} * wk;
+    acc[1] += f32x4{static_cast<float>(x[4]), static_cast<float>(x[5]), static_cast<float>(x[6]),
+                    static_cast<float>(x[7])} * wk;
+  }
+}
+
 // The merged row as bf16 (dims 8 lane .. + 7, one 16-byte word per lane).
 __device__ __forceinline__ u32x4 merged_row_bf16(const f32x4 (&acc)[kDPL / 4], float L) {
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -1151,7 +1204,13 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
   const int h = task - b * H;
   f32x4 acc[kDPL / 4];
   float M, L;
-  merge_ranges<F16>(part_o, part_ml, b, h, H, NR, lane, acc, M, L);
+  if (F16 && NR <= kSmallRanges) {
+    SmallRanges sr;
+    load_small_ranges(part_o, part_ml, b, h, H, NR, lane, sr);
+    combine_small_ranges(sr, NR, acc, M, L);
+  } else {
+    merge_ranges<F16>(part_o, part_ml, b, h, H, NR, lane, acc, M, L);
+  }
   *reinterpret_cast<u32x4*>(out + static_cast<size_t>(task) * kC + lane * kDPL) =
       merged_row_bf16(acc, L);
   if (lse_out != nullptr && lane == 0) lse_out[task] = merged_lse(M, L);
@@ -1187,25 +1246,13 @@ __global__ __launch_bounds__(kRpThreads) void mla_reduce_project_kernel(
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   constexpr int kWaves = kRpThreads / kWave;
-  // The merge's loads go out first (statistics and, for up to kRpRanges
+  // The merge's loads go out first (statistics and, for up to kSmallRanges
   // ranges, every partial row), then the weight stream: the merge waits only
   // for its own loads, which the wait counter drains in issue order.
-  constexpr int kRpRanges = 16;
-  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
   const int bw = w < B ? w : 0;  // wavefronts past B merge row 0 and keep nothing
-  const bool small = NR <= kRpRanges;
-  f32x4 st = f32x4{-INFINITY, 0.f, 0.f, 0.f};
-  f16x8 rows[kRpRanges];
-  if (small) {
-    if (lane < NR) st = reinterpret_cast<const f32x4*>(part_ml)[(static_cast<size_t>(bw) * NR + lane) * H + h];
-#pragma unroll
-    for (int r = 0; r < kRpRanges; ++r) {
-      const int rr = r < NR ? r : NR - 1;
-      rows[r] = *reinterpret_cast<const f16x8*>(
-          static_cast<const _Float16*>(part_o16) +
-          ((static_cast<size_t>(bw) * NR + rr) * H + h) * kC + lane * kDPL);
-    }
-  }
+  const bool small = NR <= kSmallRanges;
+  SmallRanges sr;
+  if (small) load_small_ranges(part_o16, part_ml, bw, h, H, NR, lane, sr);
   {
     // this part's tiles: blocks nt_lo * 16 .. nt_hi * 16 (1 KiB each) of the head
     const int blocks = (nt_hi - nt_lo) * kRpSteps;
@@ -1221,25 +1268,7 @@ __global__ __launch_bounds__(kRpThreads) void mla_reduce_project_kernel(
     f32x4 acc[kDPL / 4];
     float M, L;
     if (small && b == w) {
-      // all ranges at once: weights 2^(m - M) l 2^e, lane r holding range r
-      const float m = st[0], l = st[1], e = st[2];
-      M = wave_max_uniform(m);
-      const float wl_ = m == -INFINITY ? 0.f : fast_exp2(m - M);
-      L = wave_sum_uniform(l * wl_);
-      const float wrow = wl_ * l * fast_exp2(e);
-      acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (M != -INFINITY) {
-#pragma unroll
-        for (int r = 0; r < kRpRanges; ++r) {
-          const float wk = r < NR ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                        __builtin_bit_cast(int, wrow), r))
-                                  : 0.f;
-          acc[0] += f32x4{static_cast<float>(rows[r][0]), static_cast<float>(rows[r][1]),
-                          static_cast<float>(rows[r][2]), static_cast<float>(rows[r][3])} * wk;
-          acc[1] += f32x4{static_cast<float>(rows[r][4]), static_cast<float>(rows[r][5]),
-                          static_cast<float>(rows[r][6]), static_cast<float>(rows[r][7])} * wk;
-        }
-      }
+      combine_small_ranges(sr, NR, acc, M, L);  // the rows loaded at kernel start
     } else {
       merge_ranges<true>(part_o16, part_ml, b, h, H, NR, lane, acc, M, L);
     }
