@@ -140,7 +140,50 @@ def set_cpu_threads() -> dict:
     return info
 
 
-def bench_gqa(steps: int, warmup: int, cpu_sample: bool) -> dict:
+def gqa_gather_floor(inp, reps: int = 20) -> dict:
+    """Floor of config 2's page pattern: the calibration gather
+    (voom_gather_read, ordinary 16-byte loads) over exactly the partials
+    kernel's K and V bytes -- each 32-token block of each (sequence, kv head)
+    as two 4 KiB rows of each pool, in the kernel's (sequence, kv head, block)
+    order -- graph-replayed over 1024-8192 workgroups; then a linear read of
+    the same byte count.  Returns GB/s per grid."""
+    import numpy as np
+    import torch
+
+    from voom_amd import calibrate
+
+    slots, NKV, PT, D = inp.k_pool.shape
+    row = 2048  # bf16 elements per 4 KiB row
+    kr = inp.k_pool.view(-1, row)
+    vr = inp.v_pool.view(-1, row)
+    rows_per_page = PT * D // row
+    rows = []
+    for b, ctx in enumerate(inp.ctx_host):
+        j = np.arange((int(ctx) + 31) // 32)                     # 32-token blocks
+        slot = inp.table_host[b][j * 32 // PT].astype(np.int64)
+        first = (j * 32 % PT) * D // row                          # the block's first row
+        for kvh in range(NKV):
+            base = (slot * NKV + kvh) * rows_per_page + first
+            rows.append(np.stack([base, base + 1], 1).reshape(-1))
+    idx = torch.from_numpy(np.concatenate(rows).astype(np.int32)).cuda()
+    nbytes = idx.numel() * row * 2 * 2
+    sink = torch.zeros(8192, dtype=torch.int32, device="cuda")
+    res = {"bytes": nbytes}
+    for wg in (1024, 2048, 4096, 8192):
+        f = lambda wg=wg: calibrate.gather_read(kr, idx, sink, base2=vr, workgroups=wg)
+        f()
+        res[f"gather_gbs_wg{wg}"] = nbytes / graph_seconds([f] * 4, reps) / 1e9
+    lin = torch.empty(nbytes // 2, dtype=torch.int16, device="cuda")
+    for wg in (2048, 8192):
+        g = lambda wg=wg: calibrate.stream_read(lin, sink, workgroups=wg)
+        g()
+        res[f"linear_gbs_wg{wg}"] = nbytes / graph_seconds([g] * 4, reps) / 1e9
+    del lin
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_gqa(steps: int, warmup: int, cpu_sample: bool, gather_floor: bool = False) -> dict:
     import numpy as np
     import torch
 
@@ -235,6 +278,11 @@ def bench_gqa(steps: int, warmup: int, cpu_sample: bool) -> dict:
         "context_tokens": int(inp.ctx_host.sum()),
         "num_splits": splits,
     }
+    if gather_floor:
+        fl = gqa_gather_floor(inp)
+        res["page_gather_floor"] = fl
+        log("gather floor of these blocks (ordinary loads): " +
+            ", ".join(f"{k} {v:.0f}" for k, v in fl.items() if k != "bytes"))
 
     if cpu_sample:
         from oracle import paged_attention as opa
@@ -1258,6 +1306,8 @@ def main() -> int:
                          "e2e (config 1)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a known-size 1 GiB streaming kernel (PMC byte-counter calibration)")
+    ap.add_argument("--gather-floor", action="store_true",
+                    help="also time the calibration gather over config 2's own K/V blocks")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; sharding the paged-KV path over "
@@ -1271,7 +1321,8 @@ def main() -> int:
         return 1
     if args.copy_calibration:
         copy_calibration()
-    gqa = bench_gqa(args.steps, args.warmup, cpu_sample=not args.no_cpu)
+    gqa = bench_gqa(args.steps, args.warmup, cpu_sample=not args.no_cpu,
+                    gather_floor=args.gather_floor)
     line = {
         "metric": "paged decode-attn HBM GB/s (% peak) + spill/reload GB/s, Llama-3-8B shape",
         "value": round(gqa["value"], 2),
@@ -1302,6 +1353,8 @@ def main() -> int:
     }
     if "parity_max_abs_err_vs_oracle" in gqa:
         line["parity_max_abs_err_vs_oracle"] = gqa["parity_max_abs_err_vs_oracle"]
+    if "page_gather_floor" in gqa:
+        line["page_gather_floor"] = {k: round(v, 2) for k, v in gqa["page_gather_floor"].items()}
     legs = set(args.only.split(","))
     extra = {}
     if "spill" in legs:
