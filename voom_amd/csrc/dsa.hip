@@ -309,10 +309,10 @@ __device__ void radix_select_regs(const uint32_t (&key)[N], uint32_t valid, int 
 
 // Ordered selection write from registers: key[r] / idx[r] of thread (wave w,
 // lane l) is candidate w * per + 64 r + l, candidates in index order, in use
-// iff r < nregs (the same in every thread) and bit r of `valid`.  counts: 2 *
-// kTopkWaves ints of LDS, 16-byte aligned.  Every key > T and the first kk keys == T go to out[]
-// in index order: counts per wavefront, a prefix over the wavefronts, then
-// ballots place each index.  counts: 2 * kTopkWaves ints of LDS.
+// iff r < nregs (the same in every thread) and bit r of `valid`.  Every key >
+// T and the first kk keys == T go to out[] in index order: counts per
+// wavefront, a prefix over the wavefronts, then ballots place each index.
+// counts: 2 * kTopkWaves ints of LDS, 16-byte aligned.
 template <int N>
 __device__ void ordered_write_regs(const uint32_t (&key)[N], const int32_t (&idx)[N],
                                    uint32_t valid, int nregs, uint32_t T, int kk, int* counts,
@@ -525,7 +525,7 @@ __host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys -
 //    aligned row, else single keys at an even stride) -- after one pass of
 //    radix_select_regs (bins of the sample's span / 4096) when that bin holds
 //    at most 32 sample keys, else after a second (span / 2^24): about 1.5 k
-//    candidates, with margin.
+//    + 32 n / kSample candidates (4,100-4,800 for k = 2048 of 131,072 keys).
 // 2. Compaction.  The workgroup moves its keys >= T0, with their indices and
 //    in index order, to the chunk's slots, with their count and largest key.
 // 3. Selection, by the row's last workgroup to finish (an arrival counter;
