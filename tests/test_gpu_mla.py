@@ -97,6 +97,40 @@ def test_restart_after_a_late_jump(heads, jump):
             np.testing.assert_allclose(lse[b].cpu().numpy(), ref_lse, atol=1e-2, rtol=1e-3)
 
 
+@pytest.mark.parametrize("heads", [64, 128])
+def test_quarters_of_very_different_magnitude(heads):
+    # The fp16 range partials of 64-head groups scale each 128-dim quarter of
+    # a row by its own power of two (largest magnitude below 2^15).  Latent
+    # quarters scaled by 2^20, 1, 2^24 and 2^-2, with q scaled by the inverse
+    # (a power-of-two scale of a bf16 value is exact, so the scores do not
+    # change), put the outputs of some quarters far past the fp16 range; each
+    # quarter is checked relative to its own scale.
+    print(f"[mla] quarter magnitudes heads={heads}", flush=True)
+    inp = synthetic.mla_decode_inputs(batch=2, heads=heads, ctx_lens=[333, 1500])
+    shifts = (20, 0, 24, -2)
+    q_lat, _, _ = q_lat_of(inp)
+    for qi, sh in enumerate(shifts):
+        inp.lat_pool[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** sh
+        q_lat[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** -sh
+    ql = q_lat.float().cpu().numpy()
+    refs = []
+    for b in range(2):
+        lat_b = synthetic.mla_logical_latent(inp, b)
+        refs.append(omla.absorbed_weighted_c(ql[b:b + 1, :, None, :], lat_b[None], 64,
+                                             inp.scale, bf16=True)[0, :, 0])
+    assert float(np.abs(refs[1][:, :128]).max()) > 2.0 ** 16  # past the fp16 range
+    for nr in (1, 3, 16):
+        wc = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                                   scale=inp.scale, num_ranges=nr)
+        torch.cuda.synchronize()
+        got = wc.float().cpu().numpy()
+        for b in range(2):
+            for qi, sh in enumerate(shifts):
+                sl = slice(128 * qi, 128 * (qi + 1))
+                np.testing.assert_allclose(got[b][:, sl] * 2.0 ** -sh, refs[b][:, sl] * 2.0 ** -sh,
+                                           atol=ATOL, rtol=RTOL)
+
+
 @pytest.mark.parametrize("nr", [1, 3, 8])
 def test_range_splits_agree(nr):
     print(f"[mla] ranges={nr}", flush=True)

@@ -75,7 +75,7 @@ struct MlaArgs {
   const int32_t* __restrict__ ctx_lens;  // [B] (sparse: selected counts)
   float* __restrict__ part_o;            // [B, NR, H, 512] fp32 sums (32-head groups)
   void* __restrict__ part_o16;           // [B, NR, H, 512] fp16 rows (64-head groups)
-  float* __restrict__ part_ml;           // [B, NR, H, 2] (m, l); 64-head groups: [.., 4] (m, l, e, 0)
+  float* __restrict__ part_ml;           // [B, NR, H, 2] (m, l); 64-head groups: [.., 4] (m, l, e bytes, 0)
   const int32_t* __restrict__ sel;       // sparse: [B, sel_stride] positions, ascending
   int B, H, NR, max_pages, pt_shift, num_slots, sel_stride;
   uint32_t pool_bytes;                   // sparse: bytes of the latent pool (< 4 GiB)
@@ -971,9 +971,11 @@ void mla_group64_kernel(MlaArgs a) {
   }
 
   // ---- partial state of this (sequence, range, head group) ----
-  // Written as normalised rows o = acc / l in fp16, each (range, head) row
-  // scaled by 2^-e so that its largest magnitude stays below 2^15, with
-  // (m, l, e) beside it: half the bytes of fp32 sums, at 11 significant bits
+  // Written as normalised rows o = acc / l in fp16.  Wavefront w scales its
+  // dims 128 w .. 128 w + 127 of a (range, head) row by 2^-e_w so that their
+  // largest magnitude stays below 2^15 (no exchange of maxima between
+  // wavefronts); the statistics hold (m, l) and, one byte each in the third
+  // word, e_0 .. e_3: half the bytes of fp32 sums, at 11 significant bits
   // (the reduce multiplies 2^e back).  The rows go through LDS so that each
   // store instruction writes 1 KiB of one row.
   const size_t pbase = (static_cast<size_t>(b) * a.NR + range) * a.H + head0;
@@ -981,38 +983,29 @@ void mla_group64_kernel(MlaArgs a) {
   if (lh == 0) lsum_lds[th][32 * hh + l32] = lw;
   wait_vmem_all();  // the last step's (empty) next-tile loads write tile_b
   lds_barrier();
-  float inv[2], amax[2];
+  constexpr int kStageRow = kC + 8;  // fp16 elements per staged row (1040 bytes)
+  _Float16* stage = reinterpret_cast<_Float16*>(tile_a);
+  uint8_t* e_lds = reinterpret_cast<uint8_t*>(&tmax_lds[0][0][0]);  // [64 heads][4 wavefronts]
+  float lrow[2];
 #pragma unroll
   for (int ht = 0; ht < 2; ++ht) {
-    const float l = lsum_lds[0][32 * ht + l32] + lsum_lds[1][32 * ht + l32];
-    inv[ht] = l > 0.f ? 1.f / l : 0.f;
+    const int h = 32 * ht + l32;
+    const float l = lsum_lds[0][h] + lsum_lds[1][h];
+    lrow[ht] = l;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
     float mx = 0.f;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fabsf(acc[dt][ht][r]));
     }
-    mx *= inv[ht];
-    amax[ht] = fmaxf(mx, __shfl_xor(mx, 32));
-  }
-  float* amax_lds = &tmax_lds[0][0][0];  // [4 wavefronts][64 heads]; the maxima are done with
-  if (lh == 0) {
-    amax_lds[w * HG + l32] = amax[0];
-    amax_lds[w * HG + 32 + l32] = amax[1];
-  }
-  lds_barrier();
-  constexpr int kStageRow = kC + 8;  // fp16 elements per staged row (1040 bytes)
-  _Float16* stage = reinterpret_cast<_Float16*>(tile_a);
-  int ex[2];
-#pragma unroll
-  for (int ht = 0; ht < 2; ++ht) {
-    const int h = 32 * ht + l32;
-    const float rowmax = fmaxf(fmaxf(amax_lds[h], amax_lds[HG + h]),
-                               fmaxf(amax_lds[2 * HG + h], amax_lds[3 * HG + h]));
-    // e = max(0, ilogb(rowmax) - 14): rowmax 2^-e < 2^15 (finite rows only)
-    const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, rowmax) >> 23) & 0xff) - 127;
-    ex[ht] = (eb >= 15 && eb < 128) ? eb - 14 : 0;
-    const float f = inv[ht] * __builtin_bit_cast(float, static_cast<uint32_t>(127 - ex[ht]) << 23);
+    mx *= inv;
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // e = max(0, ilogb(mx) - 14): mx 2^-e < 2^15 (finite rows only)
+    const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 127;
+    const int ex = (eb >= 15 && eb < 128) ? eb - 14 : 0;
+    if (lh == 0) e_lds[4 * h + w] = static_cast<uint8_t>(ex);
+    const float f = inv * __builtin_bit_cast(float, static_cast<uint32_t>(127 - ex) << 23);
     typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
@@ -1035,11 +1028,10 @@ void mla_group64_kernel(MlaArgs a) {
         *reinterpret_cast<const u32x4*>(stage + h * kStageRow + 8 * lane);
   }
   if (w == 0) {
-    const int e = lh ? ex[1] : ex[0];
     // lane = head: heads l32 and 32 + l32 sit in lanes l32 and l32 + 32
+    const uint32_t ebits = reinterpret_cast<const uint32_t*>(e_lds)[lane];
     reinterpret_cast<f32x4*>(a.part_ml)[pbase + lane] =
-        f32x4{lh ? M[1] : M[0],
-              lsum_lds[0][lane] + lsum_lds[1][lane], static_cast<float>(e), 0.f};
+        f32x4{lh ? M[1] : M[0], lh ? lrow[1] : lrow[0], __builtin_bit_cast(float, ebits), 0.f};
   }
 }
 
@@ -1047,11 +1039,18 @@ void mla_group64_kernel(MlaArgs a) {
 // lane r holds range r's statistics; the partial rows of a batch of ranges
 // are all loaded before the first is used (one memory round trip per batch).
 // F16 = false: rows are fp32 sums relative to 2^m, stats (m, l).
-// F16 = true: rows are fp16 o 2^-e with o = sum / l, stats (m, l, e, 0); the
-// row's weight is then 2^(m - M) l 2^e.  Lane `lane` ends with dims
+// F16 = true: rows are fp16 o 2^-e with o = sum / l, stats (m, l, e bytes, 0)
+// with one e per 128-dim quarter of the row; the weight of the row's quarter
+// is then 2^(m - M) l 2^e.  Lane `lane` ends with dims
 // 8 lane .. 8 lane + 7 of sum_r weight_r row_r in acc, and M, L such that the
 // merged row is acc / L with log-sum-exp M + log2 L (log2 units).
 constexpr int kDPL = kC / 64;  // 8 dims per lane
+
+// 2^e for the byte at bit qsh of an fp16 partial's exponent word: the scale
+// of the 128-dim quarter that lane `lane` of a merge reads (qsh = 8 (lane / 16)).
+__device__ __forceinline__ float quarter_scale(uint32_t ebits, int qsh) {
+  return __builtin_bit_cast(float, (127u + ((ebits >> qsh) & 0xffu)) << 23);
+}
 template <bool F16>
 __device__ __forceinline__ void merge_ranges(const void* __restrict__ part_o,
                                              const float* __restrict__ part_ml, int b, int h,
@@ -1065,13 +1064,17 @@ __device__ __forceinline__ void merge_ranges(const void* __restrict__ part_o,
   for (int r0 = 0; r0 < NR; r0 += 64) {
     const int r = r0 + lane;
     const size_t ri = (static_cast<size_t>(b) * NR + r) * H + h;
-    float m = -INFINITY, l = 0.f, e = 0.f;
+    float m = -INFINITY, l = 0.f;
+    uint32_t ebits = 0;
     if (r < NR) {
       if constexpr (F16) {
         const f32x4 v = reinterpret_cast<const f32x4*>(part_ml)[ri];
         m = v[0];
         l = v[1];
-        e = v[2];
+        // the element goes through a scalar first: this compiler's bit cast of
+        // a vector element reads element 0
+        const float e = v[2];
+        ebits = __builtin_bit_cast(uint32_t, e);
       } else {
         const float2 v = reinterpret_cast<const float2*>(part_ml)[ri];
         m = v.x;
@@ -1089,8 +1092,9 @@ __device__ __forceinline__ void merge_ranges(const void* __restrict__ part_o,
     M = Mn;
 #pragma unroll
     for (int c = 0; c < kDPL / 4; ++c) acc[c] *= rescale;
-    // weight of a row: fp32 sums 2^(m - M); fp16 rows 2^(m - M) l 2^e
-    const float wrow = F16 ? wl * l * fast_exp2(e) : wl;
+    // weight of a row: fp32 sums 2^(m - M); fp16 rows 2^(m - M) l, times 2^e
+    // of the quarter this lane reads
+    const float wrow = F16 ? wl * l : wl;
     const int cnt = NR - r0 < 64 ? NR - r0 : 64;
     for (int k0 = 0; k0 < cnt; k0 += kBatch) {
       f32x4 v[kBatch][kDPL / 4];
@@ -1114,9 +1118,12 @@ __device__ __forceinline__ void merge_ranges(const void* __restrict__ part_o,
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const float wk = k0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                            __builtin_bit_cast(int, wrow), k0 + u))
-                                      : 0.f;
+        float wk = k0 + u < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                      __builtin_bit_cast(int, wrow), k0 + u))
+                                : 0.f;
+        if constexpr (F16) {
+          wk *= quarter_scale(__builtin_amdgcn_readlane(ebits, k0 + u), 8 * (lane >> 4));
+        }
         // a range without tokens has weight 0 and an all-zero row
 #pragma unroll
         for (int c = 0; c < kDPL / 4; ++c) acc[c] += v[u][c] * wk;
@@ -1135,7 +1142,7 @@ constexpr int kSmallRanges = 16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct SmallRanges {
-  f32x4 st;  // lane r < NR: (m, l, e, 0) of range r
+  f32x4 st;  // lane r < NR: (m, l, e bytes, 0) of range r
   f16x8 rows[kSmallRanges];
 };
 
@@ -1156,20 +1163,23 @@ __device__ __forceinline__ void load_small_ranges(const void* __restrict__ part_
   }
 }
 
-__device__ __forceinline__ void combine_small_ranges(const SmallRanges& sr, int NR,
+__device__ __forceinline__ void combine_small_ranges(const SmallRanges& sr, int NR, int lane,
                                                      f32x4 (&acc)[kDPL / 4], float& M, float& L) {
-  const float m = sr.st[0], l = sr.st[1], e = sr.st[2];
+  const float m = sr.st[0], l = sr.st[1];
+  const float e = sr.st[2];  // through a scalar, as in merge_ranges
+  const uint32_t ebits = __builtin_bit_cast(uint32_t, e);
   M = wave_max_uniform(m);
   const float wl = m == -INFINITY ? 0.f : fast_exp2(m - M);
   L = wave_sum_uniform(l * wl);
-  const float wrow = wl * l * fast_exp2(e);
+  const float wrow = wl * l;
   acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (M == -INFINITY) return;  // no tokens in any range
 #pragma unroll
   for (int r = 0; r < kSmallRanges; ++r) {
-    const float wk = r < NR ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                  __builtin_bit_cast(int, wrow), r))
-                            : 0.f;
+    const float wk =
+        r < NR ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wrow), r)) *
+                     quarter_scale(__builtin_amdgcn_readlane(ebits, r), 8 * (lane >> 4))
+               : 0.f;
     const f16x8& x = sr.rows[r];
     acc[0] += f32x4{static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
                     static_cast<float>(x[3])} * wk;
@@ -1207,7 +1217,7 @@ __global__ __launch_bounds__(kThreads) void mla_reduce_kernel(
   if (F16 && NR <= kSmallRanges) {
     SmallRanges sr;
     load_small_ranges(part_o, part_ml, b, h, H, NR, lane, sr);
-    combine_small_ranges(sr, NR, acc, M, L);
+    combine_small_ranges(sr, NR, lane, acc, M, L);
   } else {
     merge_ranges<F16>(part_o, part_ml, b, h, H, NR, lane, acc, M, L);
   }
@@ -1268,7 +1278,7 @@ __global__ __launch_bounds__(kRpThreads) void mla_reduce_project_kernel(
     f32x4 acc[kDPL / 4];
     float M, L;
     if (small && b == w) {
-      combine_small_ranges(sr, NR, acc, M, L);  // the rows loaded at kernel start
+      combine_small_ranges(sr, NR, lane, acc, M, L);  // the rows loaded at kernel start
     } else {
       merge_ranges<true>(part_o16, part_ml, b, h, H, NR, lane, acc, M, L);
     }
