@@ -70,6 +70,18 @@ def test_topk_exact(n, k):
     _check_topk(s, [n, max(1, n // 2)], k)
 
 
+@pytest.mark.parametrize("n", [40000, 131072, 200000, 500000, 600000])
+def test_topk_chunk_layouts_and_concentrated_candidates(n):
+    # Rows of 10, 32, 49, 123 and 147 chunks of 4096 keys.  Row 0: random
+    # scores, candidates spread over every chunk; row 1: ascending scores, so
+    # that every candidate sits in the last chunks and the gather's offsets
+    # are all zero but those of one or two chunks.
+    print(f"[dsa] topk chunk layouts n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    s = np.stack([rng.standard_normal(n), np.sort(rng.standard_normal(n))]).astype(np.float32)
+    _check_topk(s, [n, n], 2048)
+
+
 def test_topk_ties_negative_and_special_values():
     print("[dsa] topk ties", flush=True)
     rng = np.random.default_rng(7)
