@@ -197,9 +197,12 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* tmp, int& total)
 
 // Radix select over keys held in registers: thread t holds up to N keys,
 // key[r] in use iff r < nregs (the same in every thread) and bit r of
-// `valid`, every one within [lo, hi].  T becomes the rank-th largest key (1
-// <= rank <= the number of keys) and kk how many keys equal to T belong to
-// the top `rank`.  With max_passes > 0 the passes may stop early -- after
+// `valid`, every one within [lo, hi].  The top `rank` keys (1 <= rank <= the
+// number of keys) are then every key > T and the first kk keys equal to T:
+// T is the rank-th largest key and kk how many keys equal to it belong to
+// the top `rank`, or -- when after some pass the rank takes every key of the
+// crossing bin, which ends the select there -- T is one below that bin's
+// lower edge and kk is 0.  With max_passes > 0 the passes may stop early -- after
 // max_passes passes, or after any pass whose crossing bin holds at most
 // `enough` keys: T is then the lower edge of the bin holding the rank-th
 // largest key (at least `rank` keys are >= T, at most rank - 1 + enough) and
@@ -302,6 +305,13 @@ __device__ void radix_select_regs(const uint32_t (&key)[N], uint32_t valid, int 
     const uint32_t bin_m1 = (1u << shift) - 1u;
     span = span - off < bin_m1 ? span - off : bin_m1;
     if (max_passes > 0 && found[2] <= enough) break;
+    if (max_passes <= 0 && span != 0u && found[2] == kk && base != 0u) {
+      // the rank takes every key of the crossing bin: the selection is
+      // every key >= the bin's lower edge, and no narrower pass is needed
+      T = base - 1u;
+      kk_out = 0;
+      return;
+    }
   }
   T = base;
   kk_out = kk;
