@@ -225,24 +225,19 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* tmp, int& total)
 // barrier but costs more: sixteen wavefronts share four SIMDs.)  The two
 // buffers alternate between passes, so pass p's is cleared in pass p + 1,
 // after every wavefront has passed pass p.
-// hist2: 2 * kRadixBins ints, 16-byte aligned (cleared: both buffers are
-// already zero, behind a barrier); totals: kTopkWaves ints, 16-byte
-// aligned; found: 3 ints.  Every wavefront must have finished with them
-// since its last barrier.
+// hist2: 2 * kRadixBins ints, 16-byte aligned, both buffers zero (the
+// caller clears them before a barrier it passes anyway: a barrier of its own
+// here cost ~0.3 us per call); totals: kTopkWaves ints, 16-byte aligned;
+// found: 3 ints.  Every wavefront must have finished with them since its
+// last barrier.
 template <int N>
 __device__ void radix_select_regs(const uint32_t (&key)[N], uint32_t valid, int nregs, int rank,
                                   int* hist2, int* totals, int* found, uint32_t lo, uint32_t hi,
-                                  int max_passes, int enough, bool cleared, uint32_t& T,
-                                  int& kk_out) {
+                                  int max_passes, int enough, uint32_t& T, int& kk_out) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wv = tid / kWave;
   int4* h4 = reinterpret_cast<int4*>(hist2);
-  if (!cleared) {  // else the caller cleared both buffers before a barrier
-    h4[tid] = make_int4(0, 0, 0, 0);
-    h4[tid + kRadixBins / 4] = make_int4(0, 0, 0, 0);
-    __syncthreads();  // both buffers clear
-  }
   uint32_t base = lo;
   uint32_t span = hi - lo;
   int kk = rank;
@@ -623,6 +618,9 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
       wave_red[wv] = lo;
       wave_red[kTopkWaves + wv] = hi;
     }
+    // the select's histograms, cleared under the same barrier
+    reinterpret_cast<int4*>(hist2)[tid] = make_int4(0, 0, 0, 0);
+    reinterpret_cast<int4*>(hist2)[tid + kRadixBins / 4] = make_int4(0, 0, 0, 0);
     __syncthreads();
     lo = 0xFFFFFFFFu;
     hi = 0u;
@@ -637,7 +635,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
     int unused;
     // a second pass only when the first one's crossing bin holds more than
     // 32 sample keys (about 1,000 more candidates than the rank asks for)
-    radix_select_regs(sk, 0xFu, 4, want, hist2, totals, found, lo, hi, 2, 32, false, T0, unused);
+    radix_select_regs(sk, 0xFu, 4, want, hist2, totals, found, lo, hi, 2, 32, T0, unused);
   }
 
   // keys >= T0 in index order: a scan over the workgroup places each
@@ -784,7 +782,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
       key[r] = e[r].x;
       idx[r] = static_cast<int32_t>(e[r].y);
     }
-    radix_select_regs(key, valid, nregs, K, hist2, totals, found, T0, hi, 0, 0, true, T, kk);
+    radix_select_regs(key, valid, nregs, K, hist2, totals, found, T0, hi, 0, 0, T, kk);
     ordered_write_regs(key, idx, valid, nregs, T, kk, wcount, ob);
   } else {
     auto mem_key = [&](int i) { return order_key(sb[i]); };
