@@ -138,6 +138,11 @@ constexpr int kCandCap = 16384;                    // candidates selected from r
 constexpr int kRegKeys = kCandCap / kTopkThreads;  // candidates per thread
 constexpr int kSample = 4096;                      // keys sampled to place the threshold
 constexpr int kChunkKeys = 4096;                   // keys per chunk workgroup
+constexpr int kWaveKeys = kChunkKeys / (kTopkThreads / kWave);  // 256 keys per wavefront
+// rows of at most this many chunks (512 Ki keys) compact each wavefront's
+// keys into its own 256-slot segment: as many segments as the selection's
+// offset scan takes (two per thread)
+constexpr int kSegChunks = kChunksPerThread * kTopkThreads / (kTopkThreads / kWave);
 static_assert(kChunkKeys == 4 * kTopkThreads, "four keys of the chunk per thread");
 static_assert(kSample == 4 * kTopkThreads, "four sample keys per thread");
 
@@ -515,8 +520,8 @@ __device__ void ordered_write_mem(KeyFn key, IdxFn idx, int count, uint32_t T, i
 // candidate keys, and per-chunk candidate slots of (key, index) pairs.
 struct TopkWs {
   int* arrive;      // [B]
-  int* counts;      // [B, chunks]
-  uint32_t* cmax;   // [B, chunks]
+  int* counts;      // [B, chunks * 16]: candidates per segment (16 per chunk, or 1)
+  uint32_t* cmax;   // [B, chunks * 16]: largest candidate key per segment
   uint2* cand;      // [B, chunks, kChunkKeys]
   int chunks;
 };
@@ -553,7 +558,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
   __shared__ __align__(16) int totals[kTopkWaves];
   __shared__ __align__(16) int scan_tmp[kTopkWaves];
   __shared__ __align__(16) uint32_t wave_red[2 * kTopkWaves];
-  __shared__ int chunk_off[kChunksPerThread * kTopkThreads + 1];
+  __shared__ int slot_of[kCandCap];  // candidate j -> its slot in the row's slots
   __shared__ __align__(16) int wcount[2 * kTopkWaves];
   __shared__ int found[3];
   __shared__ int is_last;
@@ -638,8 +643,13 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
     radix_select_regs(sk, 0xFu, 4, want, hist2, totals, found, lo, hi, 2, 32, T0, unused);
   }
 
-  // keys >= T0 in index order: a scan over the workgroup places each
-  // thread's candidates; the same barrier collects the chunk's largest
+  // keys >= T0 in index order.  Rows of at most kSegChunks chunks: each
+  // wavefront moves its 256 keys' candidates into its own 256-slot segment
+  // of the chunk's slots (a wave scan, no barrier) and leaves the segment's
+  // count and largest key.  Longer rows: a scan over the workgroup places
+  // the chunk's candidates densely (one segment of 4096 slots), and the
+  // same barrier collects the chunk's largest.
+  const bool per_wave = nch <= kSegChunks;
   bool in[4];
   int cnt = 0;
   uint32_t mx = 0u;
@@ -652,36 +662,46 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
   }
   mx = wave_max_u32(mx);
   const int inc = wave_inclusive_scan(cnt, lane);
-  if (lane == kWave - 1) scan_tmp[wv] = inc;
-  if (lane == 0) wave_red[wv] = mx;
-  __syncthreads();
   int at = inc - cnt;
-  int all = 0;
-  uint32_t cmax = 0u;
+  uint2* slots = ws.cand + (static_cast<size_t>(b) * ws.chunks + chunk) * kChunkKeys;
+  // the row's segment counts and largest keys: [chunks * 16] per row
+  const size_t seg_row = static_cast<size_t>(b) * ws.chunks * kTopkWaves;
+  if (per_wave) {
+    slots += kWaveKeys * wv;
+    if (lane == kWave - 1) {  // inc: the wavefront's count; mx is uniform
+      ws.counts[seg_row + kTopkWaves * chunk + wv] = inc;
+      ws.cmax[seg_row + kTopkWaves * chunk + wv] = mx;
+    }
+  } else {
+    if (lane == kWave - 1) scan_tmp[wv] = inc;
+    if (lane == 0) wave_red[wv] = mx;
+    __syncthreads();
+    int all = 0;
+    uint32_t cmax = 0u;
 #pragma unroll
-  for (int k4 = 0; k4 < kTopkWaves / 4; ++k4) {
-    const int4 t4 = reinterpret_cast<const int4*>(scan_tmp)[k4];
-    const uint4 m4 = reinterpret_cast<const uint4*>(wave_red)[k4];
-    const int t[4] = {t4.x, t4.y, t4.z, t4.w};
-    const uint32_t m[4] = {m4.x, m4.y, m4.z, m4.w};
+    for (int k4 = 0; k4 < kTopkWaves / 4; ++k4) {
+      const int4 t4 = reinterpret_cast<const int4*>(scan_tmp)[k4];
+      const uint4 m4 = reinterpret_cast<const uint4*>(wave_red)[k4];
+      const int t[4] = {t4.x, t4.y, t4.z, t4.w};
+      const uint32_t m[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      at += 4 * k4 + e < wv ? t[e] : 0;
-      all += t[e];
-      cmax = m[e] > cmax ? m[e] : cmax;
+      for (int e = 0; e < 4; ++e) {
+        at += 4 * k4 + e < wv ? t[e] : 0;
+        all += t[e];
+        cmax = m[e] > cmax ? m[e] : cmax;
+      }
+    }
+    if (tid == 0) {
+      ws.counts[seg_row + chunk] = all;
+      ws.cmax[seg_row + chunk] = cmax;
     }
   }
-  uint2* slots = ws.cand + (static_cast<size_t>(b) * ws.chunks + chunk) * kChunkKeys;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     if (in[e]) {
       slots[at] = make_uint2(order_key(v[e]), static_cast<uint32_t>(i + e));
       ++at;
     }
-  }
-  if (tid == 0) {
-    ws.counts[static_cast<size_t>(b) * ws.chunks + chunk] = all;
-    ws.cmax[static_cast<size_t>(b) * ws.chunks + chunk] = cmax;
   }
 
   // Publish, then count the arrival: every wavefront waits for its stores to
@@ -706,61 +726,57 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
   reinterpret_cast<int4*>(hist2)[tid + kRadixBins / 4] = make_int4(0, 0, 0, 0);
 
   // ---- selection over the row's candidates ----
-  // candidate offsets of the row's chunks and the largest candidate key,
-  // which with T0 bounds every candidate
-  const int* cnt_row = ws.counts + static_cast<size_t>(b) * ws.chunks;
-  const uint32_t* cmx_row = ws.cmax + static_cast<size_t>(b) * ws.chunks;
+  // The segments' counts (in index order) give each candidate its slot: a
+  // scan over the workgroup, then the thread holding segment s writes the
+  // slots of candidates off[s] .. off[s + 1] - 1 into slot_of; the segments'
+  // largest keys give the largest candidate, which with T0 bounds them all.
+  const int nseg = per_wave ? nch * kTopkWaves : nch;
+  const int seg_keys = per_wave ? kWaveKeys : kChunkKeys;
+  const int* cnt_row = ws.counts + static_cast<size_t>(b) * ws.chunks * kTopkWaves;
+  const uint32_t* cmx_row = ws.cmax + static_cast<size_t>(b) * ws.chunks * kTopkWaves;
   int C = 0;
   uint32_t hi = 0u;
-  bool fits = nch <= kChunksPerThread * kTopkThreads;
+  bool fits = nseg <= kChunksPerThread * kTopkThreads;
   if (fits) {
     int c2[kChunksPerThread];
     int mine = 0;
     uint32_t m2 = 0u;
 #pragma unroll
     for (int e = 0; e < kChunksPerThread; ++e) {
-      const int ch = kChunksPerThread * tid + e;
-      c2[e] = ch < nch ? cnt_row[ch] : 0;
-      const uint32_t m = ch < nch ? cmx_row[ch] : 0u;
+      const int sg = kChunksPerThread * tid + e;
+      c2[e] = sg < nseg ? cnt_row[sg] : 0;
+      const uint32_t m = sg < nseg ? cmx_row[sg] : 0u;
       m2 = m > m2 ? m : m2;
       mine += c2[e];
     }
     m2 = wave_max_u32(m2);
-    if (lane == 0) wave_red[wv] = m2;  // read after the scan's barriers
+    if (lane == 0) wave_red[wv] = m2;  // read after the scan's barrier
     int total;
     int run = block_exclusive_scan(mine, scan_tmp, total);
-#pragma unroll
-    for (int e = 0; e < kChunksPerThread; ++e) {
-      const int ch = kChunksPerThread * tid + e;
-      if (ch < nch) chunk_off[ch] = run;
-      run += c2[e];
-    }
-    if (tid == 0) chunk_off[nch] = total;
 #pragma unroll
     for (int k = 0; k < kTopkWaves; ++k) hi = wave_red[k] > hi ? wave_red[k] : hi;
     C = total;
     fits = C >= K && C <= kCandCap;
-    __syncthreads();  // chunk_off complete
+    if (fits) {
+#pragma unroll
+      for (int e = 0; e < kChunksPerThread; ++e) {
+        const int base = (kChunksPerThread * tid + e) * seg_keys;
+        for (int k = 0; k < c2[e]; ++k) slot_of[run + k] = base + k;
+        run += c2[e];
+      }
+    }
+    __syncthreads();  // slot_of complete
   }
   uint32_t T;
   int kk;
   if (fits) {
     // wavefront w holds candidates w * per .. + per - 1, 64 per register
-    // (nregs registers); the chunk of its first candidate by binary search,
-    // then each lane walks forward over the offsets (its candidates rise by
-    // 64 per register, past a chunk or two).  Every load is issued before
-    // the first is used: one memory round trip.
+    // (nregs registers), each lane's slots read from slot_of.  Every load is
+    // issued before the first is used: one memory round trip.
     const int per = ((C + kTopkWaves - 1) / kTopkWaves + kWave - 1) / kWave * kWave;
     const int nregs = per / kWave;
     const int j0 = wv * per;
-    int ch = 0;
-    {
-      int hi_c = nch;
-      while (hi_c - ch > 1) {
-        const int mid = (ch + hi_c) >> 1;
-        if (chunk_off[mid] <= j0) ch = mid; else hi_c = mid;
-      }
-    }
+    const uint2* cand_row = ws.cand + static_cast<size_t>(b) * ws.chunks * kChunkKeys;
     uint2 e[kRegKeys];
     uint32_t valid = 0u;
 #pragma unroll
@@ -769,8 +785,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
       if (r < nregs) {
         const int j = j0 + kWave * r + lane;
         if (j < C) {
-          while (chunk_off[ch + 1] <= j) ++ch;
-          e[r] = ws.cand[(static_cast<size_t>(b) * ws.chunks + ch) * kChunkKeys + (j - chunk_off[ch])];
+          e[r] = cand_row[slot_of[j]];
           valid |= 1u << r;
         }
       }
@@ -835,7 +850,7 @@ extern "C" size_t voom_dsa_topk_workspace_bytes(int batch, int cap) {
   if (batch <= 0 || cap <= 0) return 0;
   const size_t chunks = static_cast<size_t>(topk_chunks(cap));
   return ((static_cast<size_t>(batch) * 4 + 255) & ~size_t(255)) +
-         2 * ((static_cast<size_t>(batch) * chunks * 4 + 255) & ~size_t(255)) +
+         2 * ((static_cast<size_t>(batch) * chunks * kTopkWaves * 4 + 255) & ~size_t(255)) +
          static_cast<size_t>(batch) * chunks * kChunkKeys * sizeof(uint2);
 }
 
@@ -854,7 +869,8 @@ extern "C" int voom_dsa_topk(const float* scores, const int32_t* lens, int32_t* 
   ws.chunks = topk_chunks(cap);
   char* p = static_cast<char*>(workspace);
   const size_t arrive_bytes = (static_cast<size_t>(batch) * 4 + 255) & ~size_t(255);
-  const size_t per_chunk_bytes = (static_cast<size_t>(batch) * ws.chunks * 4 + 255) & ~size_t(255);
+  const size_t per_chunk_bytes =
+      (static_cast<size_t>(batch) * ws.chunks * kTopkWaves * 4 + 255) & ~size_t(255);
   ws.arrive = reinterpret_cast<int*>(p);
   ws.counts = reinterpret_cast<int*>(p + arrive_bytes);
   ws.cmax = reinterpret_cast<uint32_t*>(p + arrive_bytes + per_chunk_bytes);
