@@ -82,6 +82,24 @@ def test_topk_chunk_layouts_and_concentrated_candidates(n):
     _check_topk(s, [n, n], 2048)
 
 
+def test_topk_sample_misplaced_threshold_falls_back_to_memory():
+    # The threshold comes from runs of 4 keys every n / 1024 positions.  Row 0
+    # puts the row's highest keys exactly there, so the threshold leaves
+    # fewer than k keys above it; row 1 ties 20,000 keys at the maximum, so
+    # more than 16,384 candidates pass it.  Both take the exact select over
+    # the row in memory and must still match the oracle bit for bit.
+    print("[dsa] topk memory fallback", flush=True)
+    n, k = 131072, 2048
+    rng = np.random.default_rng(11)
+    row0 = rng.standard_normal(n).astype(np.float32)
+    runs = (np.arange(1024, dtype=np.int64) * n // 1024) & ~3
+    for d in range(4):
+        row0[runs + d] = 100.0 + rng.random(1024).astype(np.float32)
+    row1 = rng.standard_normal(n).astype(np.float32)
+    row1[rng.choice(n, 20000, replace=False)] = 50.0
+    _check_topk(np.stack([row0, row1]), [n, n], k)
+
+
 def test_topk_ties_negative_and_special_values():
     print("[dsa] topk ties", flush=True)
     rng = np.random.default_rng(7)
