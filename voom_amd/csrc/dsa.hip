@@ -540,15 +540,18 @@ __host__ __device__ inline int topk_chunks(int cap) { return (cap + kChunkKeys -
 //    radix_select_regs (bins of the sample's span / 4096) when that bin holds
 //    at most 32 sample keys, else after a second (span / 2^24): about 1.5 k
 //    + 32 n / kSample candidates (4,100-4,800 for k = 2048 of 131,072 keys).
-// 2. Compaction.  The workgroup moves its keys >= T0, with their indices and
-//    in index order, to the chunk's slots, with their count and largest key.
+// 2. Compaction.  Keys >= T0 move, with their indices and in index order,
+//    to the chunk's slots, with a count and a largest key per segment: each
+//    wavefront's own 256-slot segment (rows of at most kSegChunks chunks),
+//    else one segment per chunk.
 // 3. Selection, by the row's last workgroup to finish (an arrival counter;
 //    its stores released to every XCD before the count, the others' acquired
-//    after it): between k and kCandCap candidates are gathered, in chunk (so
-//    index) order, straight into registers, kRegKeys per thread; the exact
-//    select over the range [T0, largest candidate] and the ordered write run
-//    from there.  Otherwise -- a threshold the sample misplaced -- the exact
-//    selection runs over the row in memory.
+//    after it): between k and kCandCap candidates are gathered, in segment
+//    (so index) order, straight into registers, kRegKeys per thread, through
+//    an LDS table of their slots; the exact select over the range [T0,
+//    largest candidate] and the ordered write run from there.  Otherwise --
+//    a threshold the sample misplaced -- the exact selection runs over the
+//    row in memory.
 // The counter is back at zero when the launch ends.
 template <bool VEC>
 __global__ __launch_bounds__(kTopkThreads) void dsa_topk_kernel(
