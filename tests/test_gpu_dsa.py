@@ -72,10 +72,11 @@ def test_topk_exact(n, k):
 
 @pytest.mark.parametrize("n", [40000, 131072, 200000, 500000, 600000])
 def test_topk_chunk_layouts_and_concentrated_candidates(n):
-    # Rows of 10, 32, 49, 123 and 147 chunks of 4096 keys.  Row 0: random
-    # scores, candidates spread over every chunk; row 1: ascending scores, so
-    # that every candidate sits in the last chunks and the gather's offsets
-    # are all zero but those of one or two chunks.
+    # Rows of 10, 32, 49, 123 and 147 chunks of 4096 keys (candidates in
+    # 256-slot segments per wavefront up to 128 chunks, one segment per chunk
+    # above).  Row 0: random scores, candidates spread over every segment;
+    # row 1: ascending scores, so that every candidate sits in the last
+    # chunks and every other segment is empty.
     print(f"[dsa] topk chunk layouts n={n}", flush=True)
     rng = np.random.default_rng(n)
     s = np.stack([rng.standard_normal(n), np.sort(rng.standard_normal(n))]).astype(np.float32)
@@ -140,11 +141,18 @@ def _q_lat(inp):
 
 
 @pytest.mark.parametrize("nr", [10, 16, 40])
-def test_sparse_over_all_positions_equals_dense(nr):
-    """Same range split (so the same rounding), same rows: bit for bit."""
-    print(f"[dsa] sparse == dense nr={nr}", flush=True)
+@pytest.mark.parametrize("scaled", [False, True])
+def test_sparse_over_all_positions_equals_dense(nr, scaled):
+    """Same range split (so the same rounding), same rows: bit for bit.
+    scaled: latent quarters times 2^20, 1, 2^24, 2^-2 (q times the inverse),
+    so that the fp16 range partials of some quarters carry exponents."""
+    print(f"[dsa] sparse == dense nr={nr} scaled={scaled}", flush=True)
     inp = synthetic.mla_decode_inputs(batch=2, heads=64, ctx_lens=[1000, 2500], slack_pages=2)
     q = _q_lat(inp)
+    if scaled:
+        for qi, sh in enumerate((20, 0, 24, -2)):
+            inp.lat_pool[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** sh
+            q[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** -sh
     dense, lse_d = ops.mla_latent_decode(q, inp.lat_pool, inp.block_table, inp.ctx_lens,
                                          scale=inp.scale, return_lse=True, num_ranges=nr)
     sel = torch.arange(2500, dtype=torch.int32, device="cuda").repeat(2, 1).contiguous()
