@@ -101,6 +101,42 @@ def test_topk_sample_misplaced_threshold_falls_back_to_memory():
     _check_topk(np.stack([row0, row1]), [n, n], k)
 
 
+def test_topk_seeded_sweep_across_the_segment_layouts():
+    """40 seeded batches: rows up to 700,000 keys (either side of the
+    128-chunk bound between per-wavefront segments and per-chunk packing),
+    k from 1 to 8,192, batches of 1-4 rows of mixed lengths, and score
+    distributions with wide and narrow ranges, ties, sorted runs, infinities
+    and signed zeros; every row bit-exact against the oracle."""
+    rng = np.random.default_rng(4242)
+    for case in range(40):
+        B = int(rng.integers(1, 5))
+        cap = int(rng.choice([3000, 20000, 131072, 262144, 530000, 700000]))
+        k = int(rng.choice([1, 64, 1000, 2048, 4096, 8192]))
+        lens = [int(x) for x in rng.integers(1, cap + 1, size=B)]
+        lens[int(rng.integers(0, B))] = cap
+        rows = []
+        for _ in range(B):
+            kind = int(rng.integers(0, 6))
+            if kind == 0:
+                r = rng.standard_normal(cap) * 10.0 ** rng.uniform(-3, 3)
+            elif kind == 1:
+                r = np.round(rng.standard_normal(cap) * 3)
+            elif kind == 2:
+                r = rng.exponential(1.0, cap) + 1e4
+            elif kind == 3:
+                r = np.sort(rng.standard_normal(cap))[::(1 if rng.random() < 0.5 else -1)].copy()
+            elif kind == 4:
+                r = rng.standard_normal(cap)
+                r[rng.integers(0, cap, 50)] = np.inf
+                r[rng.integers(0, cap, 50)] = -np.inf
+            else:
+                r = (np.where(rng.random(cap) < 0.5, 0.0, -0.0) +
+                     (rng.random(cap) < 0.001) * rng.standard_normal(cap))
+            rows.append(r.astype(np.float32))
+        print(f"[dsa] sweep case {case}: B={B} cap={cap} k={k}", flush=True)
+        _check_topk(np.stack(rows), lens, k)
+
+
 def test_topk_ties_negative_and_special_values():
     print("[dsa] topk ties", flush=True)
     rng = np.random.default_rng(7)

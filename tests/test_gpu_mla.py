@@ -131,6 +131,41 @@ def test_quarters_of_very_different_magnitude(heads):
                                            atol=ATOL, rtol=RTOL)
 
 
+def test_seeded_sweep_of_shapes_and_quarter_magnitudes():
+    """25 seeded cases: 1-3 sequences of 1-3,000 tokens, 64 or 128 heads,
+    pages of 64-256 tokens, 0 (default), 1, 3, 16 or 40 ranges, and each
+    latent quarter scaled by its own power of two in 2^-4 .. 2^24 (q by the
+    inverse); every quarter checked against the oracle at its own scale."""
+    rng = np.random.default_rng(777)
+    for case in range(25):
+        B = int(rng.integers(1, 4))
+        H = int(rng.choice([64, 128]))
+        pt = int(rng.choice([64, 128, 256]))
+        ctx = [int(x) for x in rng.integers(1, 3000, size=B)]
+        nr = int(rng.choice([0, 1, 3, 16, 40]))
+        print(f"[mla] sweep case {case}: B={B} H={H} pt={pt} nr={nr}", flush=True)
+        inp = synthetic.mla_decode_inputs(batch=B, heads=H, ctx_lens=ctx, page_tokens=pt,
+                                          slack_pages=1, seed=int(rng.integers(0, 1 << 30)))
+        q_lat, _, _ = q_lat_of(inp)
+        shifts = [int(x) for x in rng.integers(-4, 25, size=4)]
+        for qi, sh in enumerate(shifts):
+            inp.lat_pool[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** sh
+            q_lat[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** -sh
+        wc = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                                   scale=inp.scale, num_ranges=nr)
+        torch.cuda.synchronize()
+        got = wc.float().cpu().numpy()
+        ql = q_lat.float().cpu().numpy()
+        for b in range(B):
+            lat = synthetic.mla_logical_latent(inp, b)
+            ref = omla.absorbed_weighted_c(ql[b:b + 1, :, None, :], lat[None], 64, inp.scale,
+                                           bf16=True)[0, :, 0]
+            for qi, sh in enumerate(shifts):
+                sl = slice(128 * qi, 128 * (qi + 1))
+                np.testing.assert_allclose(got[b][:, sl] * 2.0 ** -sh, ref[:, sl] * 2.0 ** -sh,
+                                           atol=ATOL, rtol=RTOL)
+
+
 @pytest.mark.parametrize("nr", [1, 3, 8])
 def test_range_splits_agree(nr):
     print(f"[mla] ranges={nr}", flush=True)
