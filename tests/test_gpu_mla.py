@@ -97,17 +97,19 @@ def test_restart_after_a_late_jump(heads, jump):
             np.testing.assert_allclose(lse[b].cpu().numpy(), ref_lse, atol=1e-2, rtol=1e-3)
 
 
+@pytest.mark.parametrize("shifts", [(20, 0, 24, -2), (-24, 0, -30, 6)])
 @pytest.mark.parametrize("heads", [64, 128])
-def test_quarters_of_very_different_magnitude(heads):
+def test_quarters_of_very_different_magnitude(heads, shifts):
     # The fp16 range partials of 64-head groups scale each 128-dim quarter of
-    # a row by its own power of two (largest magnitude below 2^15).  Latent
-    # quarters scaled by 2^20, 1, 2^24 and 2^-2, with q scaled by the inverse
-    # (a power-of-two scale of a bf16 value is exact, so the scores do not
-    # change), put the outputs of some quarters far past the fp16 range; each
-    # quarter is checked relative to its own scale.
-    print(f"[mla] quarter magnitudes heads={heads}", flush=True)
+    # a row by its own power of two (largest magnitude in [2^14, 2^15)).
+    # Latent quarters scaled by powers of two, with q scaled by the inverse (a
+    # power-of-two scale of a bf16 value is exact, so the scores do not
+    # change), put the outputs of some quarters far past the fp16 range
+    # (2^20, 2^24) or far below its normal range (2^-24, 2^-30, where fp16
+    # holds at most a few bits); each quarter is checked relative to its own
+    # scale.
+    print(f"[mla] quarter magnitudes heads={heads} shifts={shifts}", flush=True)
     inp = synthetic.mla_decode_inputs(batch=2, heads=heads, ctx_lens=[333, 1500])
-    shifts = (20, 0, 24, -2)
     q_lat, _, _ = q_lat_of(inp)
     for qi, sh in enumerate(shifts):
         inp.lat_pool[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** sh
@@ -118,7 +120,12 @@ def test_quarters_of_very_different_magnitude(heads):
         lat_b = synthetic.mla_logical_latent(inp, b)
         refs.append(omla.absorbed_weighted_c(ql[b:b + 1, :, None, :], lat_b[None], 64,
                                              inp.scale, bf16=True)[0, :, 0])
-    assert float(np.abs(refs[1][:, :128]).max()) > 2.0 ** 16  # past the fp16 range
+    for qi, sh in enumerate(shifts):
+        top = float(np.abs(refs[1][:, 128 * qi:128 * (qi + 1)]).max())
+        if sh >= 20:
+            assert top > 2.0 ** 16  # past the fp16 range
+        if sh <= -24:
+            assert top < 2.0 ** -14  # below fp16's smallest normal
     for nr in (1, 3, 16):
         wc = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
                                    scale=inp.scale, num_ranges=nr)
@@ -134,7 +141,7 @@ def test_quarters_of_very_different_magnitude(heads):
 def test_seeded_sweep_of_shapes_and_quarter_magnitudes():
     """25 seeded cases: 1-3 sequences of 1-3,000 tokens, 64 or 128 heads,
     pages of 64-256 tokens, 0 (default), 1, 3, 16 or 40 ranges, and each
-    latent quarter scaled by its own power of two in 2^-4 .. 2^24 (q by the
+    latent quarter scaled by its own power of two in 2^-30 .. 2^24 (q by the
     inverse); every quarter checked against the oracle at its own scale."""
     rng = np.random.default_rng(777)
     for case in range(25):
@@ -147,7 +154,7 @@ def test_seeded_sweep_of_shapes_and_quarter_magnitudes():
         inp = synthetic.mla_decode_inputs(batch=B, heads=H, ctx_lens=ctx, page_tokens=pt,
                                           slack_pages=1, seed=int(rng.integers(0, 1 << 30)))
         q_lat, _, _ = q_lat_of(inp)
-        shifts = [int(x) for x in rng.integers(-4, 25, size=4)]
+        shifts = [int(x) for x in rng.integers(-30, 25, size=4)]
         for qi, sh in enumerate(shifts):
             inp.lat_pool[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** sh
             q_lat[..., 128 * qi:128 * (qi + 1)] *= 2.0 ** -sh

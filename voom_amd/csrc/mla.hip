@@ -973,9 +973,9 @@ void mla_group64_kernel(MlaArgs a) {
   // ---- partial state of this (sequence, range, head group) ----
   // Written as normalised rows o = acc / l in fp16.  Wavefront w scales its
   // dims 128 w .. 128 w + 127 of a (range, head) row by 2^-e_w so that their
-  // largest magnitude stays below 2^15 (no exchange of maxima between
-  // wavefronts); the statistics hold (m, l) and, one byte each in the third
-  // word, e_0 .. e_3: half the bytes of fp32 sums, at 11 significant bits
+  // largest magnitude lies in [2^14, 2^15) (no exchange of maxima between
+  // wavefronts); the statistics hold (m, l) and, one signed byte each in the
+  // third word, e_0 .. e_3: half the bytes of fp32 sums, at 11 significant bits
   // (the reduce multiplies 2^e back).  The rows go through LDS so that each
   // store instruction writes 1 KiB of one row.
   const size_t pbase = (static_cast<size_t>(b) * a.NR + range) * a.H + head0;
@@ -1001,10 +1001,12 @@ void mla_group64_kernel(MlaArgs a) {
     }
     mx *= inv;
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // e = max(0, ilogb(mx) - 14): mx 2^-e < 2^15 (finite rows only)
+    // e = ilogb(mx) - 14, within [-100, 113]: mx 2^-e in [2^14, 2^15), so a
+    // quarter of small values keeps 11 bits instead of falling into fp16's
+    // subnormals (a zero quarter takes -100; non-finite rows take 0)
     const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xff) - 127;
-    const int ex = (eb >= 15 && eb < 128) ? eb - 14 : 0;
-    if (lh == 0) e_lds[4 * h + w] = static_cast<uint8_t>(ex);
+    const int ex = eb == 128 ? 0 : (eb < -86 ? -100 : eb - 14);
+    if (lh == 0) e_lds[4 * h + w] = static_cast<uint8_t>(static_cast<int8_t>(ex));
     const float f = inv * __builtin_bit_cast(float, static_cast<uint32_t>(127 - ex) << 23);
     typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
@@ -1046,10 +1048,12 @@ void mla_group64_kernel(MlaArgs a) {
 // merged row is acc / L with log-sum-exp M + log2 L (log2 units).
 constexpr int kDPL = kC / 64;  // 8 dims per lane
 
-// 2^e for the byte at bit qsh of an fp16 partial's exponent word: the scale
-// of the 128-dim quarter that lane `lane` of a merge reads (qsh = 8 (lane / 16)).
+// 2^e for the signed byte at bit qsh of an fp16 partial's exponent word
+// (e in [-100, 113]): the scale of the 128-dim quarter that lane `lane` of a
+// merge reads (qsh = 8 (lane / 16)).
 __device__ __forceinline__ float quarter_scale(uint32_t ebits, int qsh) {
-  return __builtin_bit_cast(float, (127u + ((ebits >> qsh) & 0xffu)) << 23);
+  const int e = static_cast<int8_t>(static_cast<uint8_t>(ebits >> qsh));
+  return __builtin_bit_cast(float, static_cast<uint32_t>(127 + e) << 23);
 }
 template <bool F16>
 __device__ __forceinline__ void merge_ranges(const void* __restrict__ part_o,
