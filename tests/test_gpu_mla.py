@@ -243,6 +243,46 @@ def test_fused_merge_and_projection(heads, ctx):
                                    rtol=RTOL)
 
 
+@pytest.mark.parametrize("heads", [32, 64, 128])
+def test_empty_sequences_give_zeros(heads):
+    """A sequence with no cached tokens gets a zero row and a log-sum-exp of
+    -inf, as in the GQA kernels; the other rows of the batch match the oracle.
+    Dense (default and 3 ranges), merge + projection in one launch (64-head
+    groups) and the sparse contraction with a selection of length 0 alike."""
+    print(f"[mla] empty sequences H={heads}", flush=True)
+    ctx = [0, 300, 0, 65]
+    inp = synthetic.mla_decode_inputs(batch=4, heads=heads, ctx_lens=ctx, slack_pages=2)
+    q_lat, _, w_uv_t = q_lat_of(inp)
+    ql = q_lat.float().cpu().numpy()
+    refs = {b: omla.absorbed_weighted_c(ql[b:b + 1, :, None, :],
+                                        synthetic.mla_logical_latent(inp, b)[None], 64, inp.scale,
+                                        bf16=True)[0, :, 0] for b in (1, 3)}
+    sel = torch.arange(max(ctx), dtype=torch.int32, device="cuda").repeat(4, 1).contiguous()
+    for nr in (0, 3):
+        wc, lse = ops.mla_latent_decode(q_lat, inp.lat_pool, inp.block_table, inp.ctx_lens,
+                                        scale=inp.scale, return_lse=True, num_ranges=nr)
+        sp, lse_s = ops.mla_sparse_decode(q_lat, inp.lat_pool, inp.block_table, sel,
+                                          inp.ctx_lens, scale=inp.scale, return_lse=True,
+                                          num_ranges=nr)
+        torch.cuda.synchronize()
+        for out, l in ((wc, lse), (sp, lse_s)):
+            for b in (0, 2):
+                assert bool((out[b] == 0).all()), f"row {b} not zero (nr={nr})"
+                assert bool(torch.isneginf(l[b]).all()), f"lse {b} not -inf (nr={nr})"
+            got = out.float().cpu().numpy()
+            for b in (1, 3):
+                np.testing.assert_allclose(got[b], refs[b], atol=ATOL, rtol=RTOL)
+        if heads % 64 == 0:
+            y, wc2 = ops.mla_latent_decode_project(q_lat, inp.lat_pool, inp.block_table,
+                                                   inp.ctx_lens, w_uv_t, scale=inp.scale,
+                                                   num_ranges=nr, return_weighted_c=True)
+            y2 = ops.mla_project_out(wc, w_uv_t)
+            torch.cuda.synchronize()
+            assert torch.equal(wc2.view(torch.int16), wc.view(torch.int16))
+            assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+            assert bool((y[0] == 0).all()) and bool((y[2] == 0).all())
+
+
 def test_paging_invariance_is_bitwise():
     print("[mla] paging invariance", flush=True)
     inp = synthetic.mla_decode_inputs(batch=2, heads=32, ctx_lens=[700, 333], slack_pages=7)
