@@ -77,6 +77,64 @@ def test_update_returns_everything_appended_even_after_spills():
         assert kv._pages[layer][-1].resident
 
 
+@pytest.mark.parametrize("pages_per_chunk", [3, 7])
+@pytest.mark.parametrize("verify", [True, False])
+def test_staging_chunks_that_cut_a_host_record(pages_per_chunk, verify):
+    """Pages spilled in one call share one host record.  Staging chunks
+    smaller than that record, with two of its pages reloaded in between, take
+    runs of its pages that start inside it; each run moves with one copy per
+    plane (and per checksum row).  gather() returns every byte appended,
+    attend() matches the oracle, and a chunk takes a handful of copies."""
+    print(f"[kv] chunks of {pages_per_chunk} pages cut a record, verify={verify}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(31 + pages_per_chunk)
+    B, NQ, NKV, D, PT, S = 2, 8, 2, 64, 32, 32 * 23 + 5
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, page_positions=PT, resident_pages=1,
+                      prefetch=False, verify_spills=verify)
+    k = torch.randn((B, NKV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B, NKV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    kv.append(0, k, v)
+    assert kv.spill([(0, i) for i in range(20)]) == 20
+    record = kv._pages[0][0].host
+    assert all(kv._pages[0][i].host is record for i in range(20)) and record.chunk >= 20
+    assert kv.reload([(0, 5), (0, 6)]) == 2
+    # a staged page takes the record's bytes per page (checksums included)
+    kv._ring.nbytes = pages_per_chunk * record.page_bytes
+    copies = []
+    real_copy = torch.Tensor.copy_
+
+    def counting_copy(dst, src, *args, **kwargs):
+        # host -> staging-buffer copies only (index uploads go elsewhere)
+        ring = {b.untyped_storage().data_ptr() for b in kv._ring.bufs if b is not None}
+        if (src.device.type == "cpu" and dst.device.type == "cuda"
+                and dst.untyped_storage().data_ptr() in ring):
+            copies.append(src.numel())
+        return real_copy(dst, src, *args, **kwargs)
+
+    torch.Tensor.copy_ = counting_copy
+    try:
+        K, V = kv.gather(0)
+    finally:
+        torch.Tensor.copy_ = real_copy
+    torch.cuda.synchronize()
+    assert torch.equal(bits(K), bits(k)) and torch.equal(bits(V), bits(v))
+    # the 18 spilled pages in chunks of n; a run ends at a chunk's end or at
+    # the reloaded pages 5-6, and takes 2 tensors x 2 planes (+ 2 checksum
+    # rows when verified) copies; page by page it would be that many per page
+    spilled = [i for i in range(20) if i not in (5, 6)]
+    runs = 0
+    for c0 in range(0, len(spilled), pages_per_chunk):
+        cp = spilled[c0:c0 + pages_per_chunk]
+        runs += 1 + sum(1 for a, b in zip(cp, cp[1:]) if b != a + 1)
+    per_run = 6 if verify else 4
+    assert len(copies) == runs * per_run, (len(copies), runs)
+    q = torch.randn((B, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    out = kv.attend(0, q)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.float().cpu().numpy(), attn_oracle(q, k, v, D ** -0.5),
+                               atol=ATOL, rtol=RTOL)
+    kv.release()
+
+
 def attn_oracle(q, K, V, scale):
     """Reference decode over the concatenated K/V [B, NKV, S, D]."""
     B = q.shape[0]

@@ -1345,8 +1345,11 @@ class PagedKVCache:
         (low planes of every tensor, then high planes, page-major inside each,
         then the checksums when ``nsum`` > 0).
 
-        A chunk that is exactly one uncompressed host record, in order, moves
-        in a single copy; anything else is assembled page by page.
+        A chunk that is exactly one host record, in order, moves in a single
+        copy.  Otherwise each run of consecutive pages of one record moves
+        with one copy per plane and one per checksum row: page-major planes
+        keep such a run contiguous in the record and in the staging buffer
+        alike.  Pages outside any run (page files) are assembled page by page.
         """
         n = len(pages)
         p0 = pages[0]
@@ -1358,19 +1361,54 @@ class PagedKVCache:
             staging.copy_(sb.record(p0.host_j // sb.chunk), non_blocking=True)
             return
         T = len(parts)
+        B = nsum // T if nsum else 0
         dst = sums_view(staging, parts, n, nsum) if nsum else None
-        for j, p in enumerate(pages):
-            planes, sums = self._host_data(p)
-            for w, plane in enumerate(planes):
-                off = part_offset(parts, n, w) + j * parts[w % T]
-                staging[off:off + parts[w % T]].copy_(plane, non_blocking=True)
+        j = 0
+        while j < n:
+            p = pages[j]
+            sb = p.host
+            if sb is None or list(sb.parts) != list(parts):
+                self._upload_page(p, staging, parts, n, j, dst)
+                j += 1
+                continue
+            if dst is not None and not sb.nsum:
+                raise KVIntegrityError(f"layer {p.layer} page {p.index}: no checksums "
+                                       "were stored with the spilled page")
+            r, i0 = divmod(p.host_j, sb.chunk)
+            m_rec = sb.record_pages(r)
+            k = j + 1
+            while (k < n and pages[k].host is sb and pages[k].host_j == p.host_j + (k - j)
+                   and i0 + (k - j) < m_rec):
+                k += 1
+            run = k - j
+            rec = sb.record(r)
+            for w in range(2 * T):
+                size = parts[w % T]
+                src = part_offset(parts, m_rec, w) + i0 * size
+                off = part_offset(parts, n, w) + j * size
+                staging[off:off + run * size].copy_(rec[src:src + run * size], non_blocking=True)
             if dst is not None:
-                if sums is None:
-                    raise KVIntegrityError(f"layer {p.layer} page {p.index}: no checksums "
-                                           "were stored with the spilled page")
-                B = nsum // T
+                src_sums = sums_view(rec, parts, m_rec, sb.nsum)
                 for t in range(T):
-                    dst[t, j * B:(j + 1) * B].copy_(sums[t], non_blocking=True)
+                    dst[t, j * B:k * B].copy_(src_sums[t, i0 * B:(i0 + run) * B],
+                                              non_blocking=True)
+            j = k
+
+    def _upload_page(self, p: _Page, staging: torch.Tensor, parts: list[int], n: int, j: int,
+                     dst: torch.Tensor | None) -> None:
+        """Page j of an n-page staging buffer, plane by plane (see _upload_planes)."""
+        T = len(parts)
+        planes, sums = self._host_data(p)
+        for w, plane in enumerate(planes):
+            off = part_offset(parts, n, w) + j * parts[w % T]
+            staging[off:off + parts[w % T]].copy_(plane, non_blocking=True)
+        if dst is not None:
+            if sums is None:
+                raise KVIntegrityError(f"layer {p.layer} page {p.index}: no checksums "
+                                       "were stored with the spilled page")
+            B = dst.shape[1] // n
+            for t in range(T):
+                dst[t, j * B:(j + 1) * B].copy_(sums[t], non_blocking=True)
 
     def _merge_into(self, pool: DevicePagePool, staging: torch.Tensor, n: int,
                     parts: list[int], slots: list[int], cache: bool = False,
