@@ -42,7 +42,8 @@ const char* voom_last_error(void);
 
 /* ABI version, bumped on any signature or layout change (2: checksums in the
  * slot codec; 3: spill-record calls; 4: element and table types of the
- * position-free call; 5: the top-k workspace's zeroed row counters). */
+ * position-free call; 5: the top-k workspace's zeroed row counters; 6:
+ * voom_copy_rows). */
 int voom_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -519,6 +520,14 @@ int voom_reload_record(const void* record, int rec_slots, int first, void* const
                        const size_t* slot_bytes, const int* num_slots, int n_tensors,
                        const int32_t* slots, int n_slots, int tag, int32_t* status,
                        hipStream_t stream);
+/* Copies `rows` rows of `width` bytes, row r from src + r * src_pitch to
+ * dst + r * dst_pitch, as one asynchronous transfer on `stream` (the copy
+ * engine; either side pinned host or device memory; width <= both pitches).
+ * The staged reload of the reference's page load (runtime/kv_paged.py:98-113)
+ * uses it to move one byte plane of many spilled pages, each in its own host
+ * record at a constant spacing, in one transfer instead of one per page. */
+int voom_copy_rows(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t width,
+                   size_t rows, hipStream_t stream);
 
 #ifdef __cplusplus
 }

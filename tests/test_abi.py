@@ -63,7 +63,7 @@ def test_calibration_probes_live_in_their_own_library():
 
 def test_abi_version_and_workspace_query():
     lib = _lib.lib()
-    assert lib.voom_abi_version() == 5
+    assert lib.voom_abi_version() == 6
     assert lib.voom_paged_gqa_workspace_bytes(16, 32, 8, 128, 2048) > 0
     assert lib.voom_paged_gqa_workspace_bytes(0, 32, 8, 128, 2048) == 0
 

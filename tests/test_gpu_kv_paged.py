@@ -77,6 +77,38 @@ def test_update_returns_everything_appended_even_after_spills():
         assert kv._pages[layer][-1].resident
 
 
+
+class count_staged_copies:
+    """Counts the host -> staging-buffer transfers of a block: strided ones
+    (ops.copy_rows) and plain tensor copies into a staging buffer."""
+
+    def __init__(self, kv):
+        self.kv = kv
+        self.calls = []
+
+    def __enter__(self):
+        kv, calls = self.kv, self.calls
+        self.real_rows, self.real_copy = ops.copy_rows, torch.Tensor.copy_
+
+        def rows(*args, **kwargs):
+            calls.append(("rows", args[5]))
+            return self.real_rows(*args, **kwargs)
+
+        def copy(dst, src, *args, **kwargs):
+            ring = {b.untyped_storage().data_ptr() for b in kv._ring.bufs if b is not None}
+            if (src.device.type == "cpu" and dst.device.type == "cuda"
+                    and dst.untyped_storage().data_ptr() in ring):
+                calls.append(("copy", src.numel()))
+            return self.real_copy(dst, src, *args, **kwargs)
+
+        ops.copy_rows, torch.Tensor.copy_ = rows, copy
+        return calls
+
+    def __exit__(self, *exc):
+        ops.copy_rows, torch.Tensor.copy_ = self.real_rows, self.real_copy
+        return False
+
+
 @pytest.mark.parametrize("pages_per_chunk", [3, 7])
 @pytest.mark.parametrize("verify", [True, False])
 def test_staging_chunks_that_cut_a_host_record(pages_per_chunk, verify):
@@ -99,22 +131,8 @@ def test_staging_chunks_that_cut_a_host_record(pages_per_chunk, verify):
     assert kv.reload([(0, 5), (0, 6)]) == 2
     # a staged page takes the record's bytes per page (checksums included)
     kv._ring.nbytes = pages_per_chunk * record.page_bytes
-    copies = []
-    real_copy = torch.Tensor.copy_
-
-    def counting_copy(dst, src, *args, **kwargs):
-        # host -> staging-buffer copies only (index uploads go elsewhere)
-        ring = {b.untyped_storage().data_ptr() for b in kv._ring.bufs if b is not None}
-        if (src.device.type == "cpu" and dst.device.type == "cuda"
-                and dst.untyped_storage().data_ptr() in ring):
-            copies.append(src.numel())
-        return real_copy(dst, src, *args, **kwargs)
-
-    torch.Tensor.copy_ = counting_copy
-    try:
+    with count_staged_copies(kv) as copies:
         K, V = kv.gather(0)
-    finally:
-        torch.Tensor.copy_ = real_copy
     torch.cuda.synchronize()
     assert torch.equal(bits(K), bits(k)) and torch.equal(bits(V), bits(v))
     # the 18 spilled pages in chunks of n; a run ends at a chunk's end or at
@@ -127,6 +145,42 @@ def test_staging_chunks_that_cut_a_host_record(pages_per_chunk, verify):
         runs += 1 + sum(1 for a, b in zip(cp, cp[1:]) if b != a + 1)
     per_run = 6 if verify else 4
     assert len(copies) == runs * per_run, (len(copies), runs)
+    q = torch.randn((B, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    out = kv.attend(0, q)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.float().cpu().numpy(), attn_oracle(q, k, v, D ** -0.5),
+                               atol=ATOL, rtol=RTOL)
+    kv.release()
+
+
+@pytest.mark.parametrize("verify", [True, False])
+def test_pages_spilled_one_at_a_time_upload_as_strided_runs(verify):
+    """The budget spills one page at a time as a decode grows, so each spilled
+    page sits in a record of its own, one after another in the arena.  Their
+    planes lie at a constant host stride: a staged chunk moves each plane (and
+    checksum row) of such a run as one strided transfer instead of one copy
+    per page, and the bytes come back exactly."""
+    print(f"[kv] one-page records, verify={verify}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(41)
+    B, NQ, NKV, D, PT, S = 2, 8, 2, 64, 32, 32 * 34 + 9
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, page_positions=PT, resident_pages=1,
+                      prefetch=False, verify_spills=verify)
+    k = torch.randn((B, NKV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B, NKV, S, D), generator=gen, device="cuda").to(torch.bfloat16)
+    kv.append(0, k, v)
+    for i in range(30):
+        assert kv.spill([(0, i)]) == 1
+    hosts = [kv._pages[0][i].host for i in range(30)]
+    assert len({id(h) for h in hosts}) == 30  # 30 records of one page
+    with count_staged_copies(kv) as copies:
+        K, V = kv.gather(0)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(K), bits(k)) and torch.equal(bits(V), bits(v))
+    per_run = 6 if verify else 4
+    # page by page: 30 * per_run copies; evenly spaced records: one run (a
+    # new arena slab would start a second)
+    assert len(copies) <= 2 * per_run, copies
+    assert all(kind == "rows" for kind, _ in copies) and sum(n for _, n in copies) == 30 * per_run
     q = torch.randn((B, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
     out = kv.attend(0, q)
     torch.cuda.synchronize()

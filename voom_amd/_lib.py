@@ -91,6 +91,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "voom_spill_record": (c_int, [_P, _P, _P, c_int, _P, c_int, _P, c_int, c_int, c_int, _P]),
     "voom_reload_record": (c_int, [_P, c_int, c_int, _P, _P, _P, c_int, _P, c_int, c_int, _P,
                                    _P]),
+    "voom_copy_rows": (c_int, [_P, c_size_t, _P, c_size_t, c_size_t, c_size_t, _P]),
 }
 
 

@@ -48,4 +48,4 @@ int device_cu_count() {
 
 extern "C" const char* voom_last_error(void) { return voom::g_error; }
 
-extern "C" int voom_abi_version(void) { return 5; }
+extern "C" int voom_abi_version(void) { return 6; }

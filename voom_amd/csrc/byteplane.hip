@@ -681,6 +681,18 @@ extern "C" int voom_reload_record(const void* record, int rec_slots, int first,
   return VOOM_LAUNCH_CHECK("reload_record: launch");
 }
 
+extern "C" int voom_copy_rows(void* dst, size_t dst_pitch, const void* src, size_t src_pitch,
+                              size_t width, size_t rows, hipStream_t stream) {
+  if (width == 0 || rows == 0) return VOOM_OK;
+  VOOM_REQUIRE(dst && src, "copy_rows: null pointer");
+  VOOM_REQUIRE(width <= dst_pitch && width <= src_pitch,
+               "copy_rows: width %zu exceeds a pitch (dst %zu, src %zu)", width, dst_pitch,
+               src_pitch);
+  return check_hip(hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, width, rows, hipMemcpyDefault,
+                                    stream),
+                   "copy_rows: hipMemcpy2DAsync");
+}
+
 extern "C" int voom_record_prepare(void) {
   // The first launch of a kernel in a process sets up its function object on
   // the host (about a millisecond per kernel); resolving the record kernels'

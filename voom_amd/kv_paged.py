@@ -108,7 +108,7 @@ class _SpillBlock:
     """
 
     __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "rec_ready", "live", "pages",
-                 "nsum", "jobs", "last_use")
+                 "nsum", "jobs", "last_use", "_where")
 
     def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int,
                  nsum: int = 0):
@@ -121,6 +121,7 @@ class _SpillBlock:
         self.ready: torch.cuda.Event | None = None  # after the block's last record landed
         self.rec_ready: dict[int, torch.cuda.Event] = {}  # after each record landed
         self.last_use: torch.cuda.Event | None = None  # after the last direct reload from it
+        self._where: tuple | None = None  # see where()
         self.live = n_pages
         # host work queued on the spill (compression, page files), per page group
         self.jobs: list[Future] = []
@@ -130,6 +131,16 @@ class _SpillBlock:
         jobs, self.jobs = self.jobs, []
         for job in jobs:
             job.result()
+
+    def where(self) -> tuple:
+        """(host address, address of its pinned slab, chunk, pages, record
+        stride): what the staged upload needs to place this block's pages,
+        found once (a block never moves)."""
+        if self._where is None:
+            view = self.block.view
+            self._where = (view.data_ptr(), view.untyped_storage().data_ptr(), self.chunk,
+                           self.n_pages, self.rec_stride)
+        return self._where
 
     @property
     def page_bytes(self) -> int:
@@ -975,6 +986,9 @@ class PagedKVCache:
     def release(self) -> None:
         """Free device slots and host copies; offset and nbytes return to 0."""
         self._wait_host_work()
+        # uploads started ahead still read host copies and write staging buffers
+        if self._copy_stream is not None:
+            self._copy_stream.synchronize()
         # no kernel may still touch the host copies once they are given back
         for sb in self._spill_blocks:
             for ev in (sb.ready, sb.last_use):
@@ -1346,10 +1360,15 @@ class PagedKVCache:
         then the checksums when ``nsum`` > 0).
 
         A chunk that is exactly one host record, in order, moves in a single
-        copy.  Otherwise each run of consecutive pages of one record moves
-        with one copy per plane and one per checksum row: page-major planes
-        keep such a run contiguous in the record and in the staging buffer
-        alike.  Pages outside any run (page files) are assembled page by page.
+        copy.  Otherwise the pages go in runs: consecutive pages of one pinned
+        slab whose planes (and checksum rows) lie at a constant host stride
+        from one page to the next -- consecutive pages of one record (the
+        stride is the plane's page size, so each plane of the run is one
+        contiguous range), or one-page records spaced evenly in the arena, as
+        the budget's spills of one page at a time leave them.  Each plane and
+        checksum row of a run moves as one strided transfer
+        (``ops.copy_rows``).  Pages outside any run (page files) are
+        assembled page by page.
         """
         n = len(pages)
         p0 = pages[0]
@@ -1363,35 +1382,67 @@ class PagedKVCache:
         T = len(parts)
         B = nsum // T if nsum else 0
         dst = sums_view(staging, parts, n, nsum) if nsum else None
+        # Per column c (each plane, then each checksum row) the host address of
+        # page q is base(q) + m(q) * at_m[c] + i(q) * width[c]: base = its
+        # record's start, m = the record's page count, i = q's place in it.
+        width = [parts[w % T] for w in range(2 * T)] + ([4 * B] * T if nsum else [])
+        at_m = [part_offset(parts, 1, w) for w in range(2 * T)] + \
+            [2 * sum(parts) + 4 * t * B for t in range(T if nsum else 0)]
+        K = len(width)
+        # per page: block address, slab, chunk, pages, record stride, host_j
+        # (zeros and chunk 1 for a page that goes page by page)
+        none = (0, 0, 1, 0, 0)
+        rows: list[tuple] = []
+        okl: list[bool] = []
+        parts_l = list(parts)
+        for q in pages:
+            h = q.host
+            e = None
+            if h is not None:
+                if nsum and not h.nsum:
+                    raise KVIntegrityError(f"layer {q.layer} page {q.index}: no checksums "
+                                           "were stored with the spilled page")
+                if h.parts == parts_l and (not nsum or h.nsum == nsum):
+                    e = h.where()
+            okl.append(e is not None)
+            rows.append((*(e if e is not None else none), q.host_j if e is not None else 0))
+        ptr, slab, chunk, npages, stride, hj = np.array(rows, dtype=np.int64).T
+        ok = np.array(okl, dtype=bool)
+        r = hj // chunk
+        i = hj - r * chunk
+        m = np.minimum(chunk, npages - r * chunk)
+        A = (ptr + r * stride)[:, None] + m[:, None] * np.asarray(at_m, dtype=np.int64)[None, :] \
+            + i[:, None] * np.asarray(width, dtype=np.int64)[None, :]
+        D = np.diff(A, axis=0)
+        # pair (q, q + 1) may share a run: both have host rows in one slab
+        pair = (ok[:-1] & ok[1:] & (slab[:-1] == slab[1:])).tolist()
+        wide = np.all(D >= np.asarray(width, dtype=np.int64)[None, :], axis=1).tolist()
+        same = [False] + np.all(D[1:] == D[:-1], axis=1).tolist()
+        rows_at, steps = A.tolist(), D.tolist()
+
+        stream = torch.cuda.current_stream()
+        stage0 = staging.data_ptr()
+        sums0 = dst.data_ptr() if dst is not None else 0
         j = 0
         while j < n:
-            p = pages[j]
-            sb = p.host
-            if sb is None or list(sb.parts) != list(parts):
-                self._upload_page(p, staging, parts, n, j, dst)
+            if not okl[j]:
+                self._upload_page(pages[j], staging, parts, n, j, dst)
                 j += 1
                 continue
-            if dst is not None and not sb.nsum:
-                raise KVIntegrityError(f"layer {p.layer} page {p.index}: no checksums "
-                                       "were stored with the spilled page")
-            r, i0 = divmod(p.host_j, sb.chunk)
-            m_rec = sb.record_pages(r)
             k = j + 1
-            while (k < n and pages[k].host is sb and pages[k].host_j == p.host_j + (k - j)
-                   and i0 + (k - j) < m_rec):
-                k += 1
+            if k < n and pair[j] and wide[j]:
+                k = j + 2
+                while k < n and pair[k - 1] and same[k - 1]:
+                    k += 1
             run = k - j
-            rec = sb.record(r)
-            for w in range(2 * T):
-                size = parts[w % T]
-                src = part_offset(parts, m_rec, w) + i0 * size
-                off = part_offset(parts, n, w) + j * size
-                staging[off:off + run * size].copy_(rec[src:src + run * size], non_blocking=True)
-            if dst is not None:
-                src_sums = sums_view(rec, parts, m_rec, sb.nsum)
-                for t in range(T):
-                    dst[t, j * B:k * B].copy_(src_sums[t, i0 * B:(i0 + run) * B],
-                                              non_blocking=True)
+            first = rows_at[j]
+            pitch = steps[j] if run > 1 else width
+            for c in range(K):
+                if c < 2 * T:
+                    to = stage0 + part_offset(parts, n, c) + j * width[c]
+                else:
+                    to = sums0 + 4 * ((c - 2 * T) * n * B + j * B)
+                ops.copy_rows(to, width[c], first[c], pitch[c], width[c], run, stream=stream)
             j = k
 
     def _upload_page(self, p: _Page, staging: torch.Tensor, parts: list[int], n: int, j: int,

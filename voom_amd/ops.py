@@ -436,6 +436,18 @@ def page_sums_verify(expected: torch.Tensor, got: torch.Tensor, tag: int,
               _ptr(status), _stream(stream))
 
 
+def copy_rows(dst: int, dst_pitch: int, src: int, src_pitch: int, width: int, rows: int, *,
+              stream: torch.cuda.Stream | None = None) -> None:
+    """Enqueue one transfer of ``rows`` rows of ``width`` bytes, row r from
+    address src + r * src_pitch to dst + r * dst_pitch (``voom_copy_rows``;
+    pinned host or device memory on either side).  The addresses are raw
+    integers: the caller keeps both ranges alive until the stream has passed
+    the copy."""
+    _require(width >= 0 and rows >= 0, "width and rows must be non-negative")
+    _lib.call("voom_copy_rows", int(dst), int(dst_pitch), int(src), int(src_pitch), int(width),
+              int(rows), _stream(stream))
+
+
 def record_bytes(pools: list[torch.Tensor], rec_slots: int, sums: bool) -> int:
     """Bytes of a spill record of ``rec_slots`` slots of every tensor in
     ``pools``: both byte planes of each slot, plus int32 [T, rec_slots]
