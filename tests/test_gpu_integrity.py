@@ -66,10 +66,12 @@ def make_cache(gen, **kw):
     return kv, data
 
 
-def test_corrupt_host_byte_is_refused_on_reload():
-    print("[integrity] host arena byte flip", flush=True)
+@pytest.mark.parametrize("record_run_bytes", [0, 1 << 40])  # record kernels / staging ring
+def test_corrupt_host_byte_is_refused_on_reload(record_run_bytes):
+    print(f"[integrity] host arena byte flip, record_run_bytes={record_run_bytes}", flush=True)
     gen = torch.Generator(device="cuda").manual_seed(51)
     kv, _ = make_cache(gen)
+    kv.record_run_bytes = record_run_bytes
     kv.spill([(1, i) for i in (0, 1, 2, 3)])
     torch.cuda.synchronize()
     p = kv._pages[1][2]
@@ -83,10 +85,12 @@ def test_corrupt_host_byte_is_refused_on_reload():
     kv.release()
 
 
-def test_corrupt_checksum_word_is_refused():
-    print("[integrity] stored checksum changed", flush=True)
+@pytest.mark.parametrize("record_run_bytes", [0, 1 << 40])  # record kernels / staging ring
+def test_corrupt_checksum_word_is_refused(record_run_bytes):
+    print(f"[integrity] stored checksum changed, record_run_bytes={record_run_bytes}", flush=True)
     gen = torch.Generator(device="cuda").manual_seed(52)
     kv, _ = make_cache(gen)
+    kv.record_run_bytes = record_run_bytes
     kv.spill([(0, 3)])
     torch.cuda.synchronize()
     p = kv._pages[0][3]

@@ -186,6 +186,15 @@ def test_pages_spilled_one_at_a_time_upload_as_strided_runs(verify):
     torch.cuda.synchronize()
     np.testing.assert_allclose(out.float().cpu().numpy(), attn_oracle(q, k, v, D ** -0.5),
                                atol=ATOL, rtol=RTOL)
+    # reload(): runs this short go through the staging ring as well (a record
+    # kernel launch per page would move too little each)
+    with count_staged_copies(kv) as copies:
+        assert kv.reload() == 30
+    torch.cuda.synchronize()
+    assert copies and all(kind == "rows" for kind, _ in copies)
+    K, V = kv.gather(0)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(K), bits(k)) and torch.equal(bits(V), bits(v))
     kv.release()
 
 

@@ -173,6 +173,7 @@ def test_cache_record_path_equals_the_staged_path(kind):
         gen = torch.Generator(device="cuda").manual_seed(72)
         kv = PagedKVCache(num_layers=2, max_bytes=1 << 40, page_positions=64, resident_pages=1)
         kv.direct_host = direct
+        kv.record_run_bytes = 0  # every run through the record kernels when direct
         for layer in range(2):
             if kind == "kv":
                 kv.append(layer, rand_bits((2, 2, 400, 128), gen).view(torch.bfloat16),

@@ -108,7 +108,7 @@ class _SpillBlock:
     """
 
     __slots__ = ("block", "n_pages", "parts", "chunk", "ready", "rec_ready", "live", "pages",
-                 "nsum", "jobs", "last_use", "_where")
+                 "nsum", "jobs", "last_use", "_where", "ready_at")
 
     def __init__(self, block: HostBlock, n_pages: int, parts: list[int], chunk: int,
                  nsum: int = 0):
@@ -122,6 +122,9 @@ class _SpillBlock:
         self.rec_ready: dict[int, torch.cuda.Event] = {}  # after each record landed
         self.last_use: torch.cuda.Event | None = None  # after the last direct reload from it
         self._where: tuple | None = None  # see where()
+        # (stream handle, sequence number) of ``ready``: events of one stream
+        # complete in the order they were recorded
+        self.ready_at: tuple[int, int] | None = None
         self.live = n_pages
         # host work queued on the spill (compression, page files), per page group
         self.jobs: list[Future] = []
@@ -216,6 +219,29 @@ def _planes(buf: torch.Tensor, parts: list[int], m: int, t: int):
     lo = part_offset(parts, m, t)
     hi = part_offset(parts, m, T + t)
     return buf[lo:lo + m * parts[t]], buf[hi:hi + m * parts[t]]
+
+
+# A run of consecutive record pages this large or larger is reloaded by the
+# record kernel; shorter runs go through the staging ring.  One record-kernel
+# launch costs ~30 us however little it moves (measured: 100 one-page runs of
+# 256 KiB took 3.25 ms, one 100-page run 0.65 ms); 2 MiB is ~36 us at the
+# host link's rate.
+_RECORD_RUN_BYTES = 2 << 20
+
+
+def _record_runs(pages: list) -> list:
+    """[block, record, pages] runs of consecutive pages of one host record,
+    in the given order (every page must have a host copy)."""
+    runs: list = []
+    for p in pages:
+        sb, j = p.host, p.host_j
+        r = j // sb.chunk
+        last = runs[-1] if runs else None
+        if last is not None and last[0] is sb and last[1] == r and last[2][-1].host_j + 1 == j:
+            last[2].append(p)
+        else:
+            runs.append([sb, r, [p]])
+    return runs
 
 
 class _Page:
@@ -511,6 +537,11 @@ class PagedKVCache:
         # the record kernels (the split writes host memory, the merge reads
         # it); False takes the staging ring and copy-engine path instead
         self.direct_host = True
+        # a reload takes the record kernels for runs of consecutive record
+        # pages of at least this many bytes, the staging ring for the rest
+        self.record_run_bytes = _RECORD_RUN_BYTES
+        self._ready_seq = 0  # sequence of spill ready events (see _SpillBlock.ready_at)
+        self._ready_done: dict[int, int] = {}  # stream -> newest sequence known complete
         self._pending_frees: list = []  # (event, host block) freed once the event passed
         self._tags: OrderedDict = OrderedDict()  # tag -> (layer, page indices)
         self._next_tag = 1
@@ -529,7 +560,9 @@ class PagedKVCache:
         # _res[layer, i]: closed page i of the layer is resident (the budget
         # scan reads this mask instead of the page objects)
         self._res = np.zeros((L, 64), dtype=bool)
-        self._spill_blocks: list[_SpillBlock] = []  # host blocks, oldest first
+        # host blocks, oldest first (keyed by id: removal and lookup in O(1)
+        # however many one-page records a long decode leaves)
+        self._spill_blocks: dict[int, _SpillBlock] = {}
         self._pools: list[DevicePagePool | None] = [None] * L
         # one transient staging pool shared by all layers: every transient
         # merge and every read of it is ordered on the main stream
@@ -548,7 +581,7 @@ class PagedKVCache:
         return self._stats
 
     def _wait_host_work(self) -> None:
-        for sb in list(getattr(self, "_spill_blocks", ())):
+        for sb in list(getattr(self, "_spill_blocks", {}).values()):
             if sb.jobs:
                 sb.wait_jobs()
 
@@ -990,7 +1023,7 @@ class PagedKVCache:
         if self._copy_stream is not None:
             self._copy_stream.synchronize()
         # no kernel may still touch the host copies once they are given back
-        for sb in self._spill_blocks:
+        for sb in self._spill_blocks.values():
             for ev in (sb.ready, sb.last_use):
                 if ev is not None:
                     ev.synchronize()
@@ -1107,7 +1140,7 @@ class PagedKVCache:
         sb = _SpillBlock(self.arena.alloc(block_bytes(n, per_chunk, page_bytes)), n, parts,
                          per_chunk, nsum)
         sb.pages = list(pages)
-        self._spill_blocks.append(sb)
+        self._spill_blocks[id(sb)] = sb
         for j, p in enumerate(pages):
             p.host = sb
             p.host_j = j
@@ -1131,8 +1164,7 @@ class PagedKVCache:
         ev = torch.cuda.Event()
         ev.record()
         self._uploads.settle(ev)
-        sb.rec_ready[rec] = ev
-        sb.ready = ev
+        self._set_ready(sb, rec, ev, torch.cuda.current_stream())
 
     def _spill_issuer(self):
         """A function taking spill work items (pool, pages, block, record) one
@@ -1155,9 +1187,9 @@ class PagedKVCache:
                 with torch.cuda.stream(copy):
                     sb.record(rec).copy_(buf, non_blocking=True)
                 self._ring.release(idx, copy)
-                sb.ready = torch.cuda.Event()
-                sb.ready.record(copy)
-                sb.rec_ready[rec] = sb.ready
+                ev = torch.cuda.Event()
+                ev.record(copy)
+                self._set_ready(sb, rec, ev, copy)
             staged.clear()
 
         def issue(item) -> None:
@@ -1285,7 +1317,7 @@ class PagedKVCache:
         only blocks whose pages all have page files are dropped."""
         if self.host_max_bytes is None:
             return
-        for sb in list(self._spill_blocks):
+        for sb in list(self._spill_blocks.values()):
             if self.arena.used_bytes <= self.host_max_bytes:
                 break
             sb.wait_jobs()
@@ -1296,14 +1328,53 @@ class PagedKVCache:
                 p.host = None
             self._release_block(sb)
 
+    def _set_ready(self, sb: _SpillBlock, rec: int, ev: torch.cuda.Event,
+                   stream: torch.cuda.Stream) -> None:
+        """Record ``ev`` (just recorded on ``stream``) as the moment record
+        ``rec`` of ``sb``, and so the block so far, has been written."""
+        self._ready_seq += 1
+        sb.rec_ready[rec] = ev
+        sb.ready = ev
+        sb.ready_at = (int(stream.cuda_stream), self._ready_seq)
+
+    @staticmethod
+    def _newest_ready(blocks) -> list:
+        """(stream, sequence, event) of the ready events that cover ``blocks``:
+        per recording stream only the newest, which completes after every
+        earlier one of that stream (the streams outlive the spills recorded
+        on them)."""
+        newest: dict[int, tuple[int, torch.cuda.Event]] = {}
+        for sb in blocks:
+            if sb.ready is None:
+                continue
+            st, seq = sb.ready_at
+            if st not in newest or seq > newest[st][0]:
+                newest[st] = (seq, sb.ready)
+        return [(st, seq, ev) for st, (seq, ev) in newest.items()]
+
+    def _wait_ready(self, stream: torch.cuda.Stream, blocks) -> None:
+        """Make ``stream`` wait until the spills of ``blocks`` have landed (one
+        event wait per recording stream, however many blocks)."""
+        for _, _, ev in self._newest_ready(blocks):
+            stream.wait_event(ev)
+
+    def _sync_ready(self, blocks) -> None:
+        """Wait on the host until the spills of ``blocks`` have landed; events
+        known to have completed (a later one of their stream was waited for)
+        are not waited for again."""
+        for st, seq, ev in self._newest_ready(blocks):
+            if self._ready_done.get(st, 0) >= seq:
+                continue
+            ev.synchronize()
+            self._ready_done[st] = seq
+
     def _release_block(self, sb: _SpillBlock) -> None:
         """Give a spill block's host memory back.  Kernels still reading it
         (a direct reload just enqueued) keep it until they are done: it is
         freed once ``last_use`` has passed (at the next spill or release)."""
         sb.wait_jobs()
-        if sb.ready is not None:
-            sb.ready.synchronize()
-        self._spill_blocks.remove(sb)
+        self._sync_ready([sb])
+        del self._spill_blocks[id(sb)]
         if sb.last_use is not None and not sb.last_use.query():
             self._pending_frees.append((sb.last_use, sb.block))
         else:
@@ -1589,8 +1660,7 @@ class PagedKVCache:
         per_chunk = max(1, self._ring.nbytes // rec)
         cp = spilled[:per_chunk]
         copy = self._stream()
-        for sb in {id(p.host): p.host for p in cp if p.host is not None}.values():
-            copy.wait_event(sb.ready)
+        self._wait_ready(copy, [p.host for p in cp if p.host is not None])
         idx, buf = self._acquire(copy, len(cp) * rec)
         self._guarded_upload(copy, idx, buf, cp, parts, nsum)
         ev = torch.cuda.Event()
@@ -1672,11 +1742,19 @@ class PagedKVCache:
         # first copy starts before later jobs are even looked at
         for layer, pages, target, consume, transient in jobs:
             if not transient and self._direct_ok(target):
+                # runs of at least record_run_bytes go to the record kernel;
+                # shorter ones (pages spilled a few at a time) would each cost
+                # a launch that moves too little, and take the staged path,
+                # whose strided transfers move any number of them at once
                 held = [p for p in pages if p.host is not None]
-                if held:
-                    verified |= self._reload_records(layer, held, target, consume)
-                    n_pages += len(held)
-                    pages = [p for p in pages if p.host is None]
+                page_bytes = held[0].host.page_bytes if held else 0
+                direct = [p for _, _, run in _record_runs(held)
+                          if len(run) * page_bytes >= self.record_run_bytes for p in run]
+                if direct:
+                    verified |= self._reload_records(layer, direct, target, consume)
+                    n_pages += len(direct)
+                    ids = {id(p) for p in direct}
+                    pages = [p for p in pages if id(p) not in ids]
                     if not pages:
                         continue
             parts = self._plane_parts(target)
@@ -1685,8 +1763,7 @@ class PagedKVCache:
             per_chunk = max(1, self._ring.nbytes // record_page_bytes(parts, nsum))
             if transient:
                 target.ensure_capacity(nbuf * per_chunk * B)
-            for sb in {id(p.host): p.host for p in pages if p.host is not None}.values():
-                copy.wait_event(sb.ready)
+            self._wait_ready(copy, [p.host for p in pages if p.host is not None])
             for c0 in range(0, len(pages), per_chunk):
                 cp = pages[c0:c0 + per_chunk]
                 ahead = self._take_prefetch(layer, cp) if transient and c0 == 0 else None
@@ -1711,24 +1788,14 @@ class PagedKVCache:
         were compared."""
         B = self._batch
         nsum = self._nsum(target)
-        runs: list = []  # [block, record, pages]
         for p in pages:
-            sb, j = p.host, p.host_j
-            if nsum and not sb.nsum:
+            if nsum and not p.host.nsum:
                 raise KVIntegrityError(f"layer {p.layer} page {p.index}: no checksums were "
                                        "stored with the spilled page")
-            r = j // sb.chunk
-            last = runs[-1] if runs else None
-            if last is not None and last[0] is sb and last[1] == r and \
-                    last[2][-1].host_j + 1 == j:
-                last[2].append(p)
-            else:
-                runs.append([sb, r, [p]])
+        runs = _record_runs(pages)
         main = torch.cuda.current_stream()
         blocks = {id(sb): sb for sb, _, _ in runs}
-        for sb in blocks.values():
-            if sb.ready is not None:
-                main.wait_event(sb.ready)
+        self._wait_ready(main, blocks.values())
         if nsum and self._status is None:
             self._status = torch.zeros(2, dtype=torch.int32, device=self.device)
         slots = target.allocate(B * len(pages))
@@ -1797,6 +1864,8 @@ class PagedKVCache:
 
         self._pipeline_in(jobs())
         n = 0
+        self._sync_ready({id(p.host): p.host for lp in done.values() for p in lp
+                          if p.host is not None}.values())
         for layer, lp in done.items():
             self._set_table_cols(layer, {p.index: p.slots for p in lp})
             for p in lp:
@@ -1822,7 +1891,7 @@ class PagedKVCache:
         if sb is None:
             return
         sb.live -= 1
-        if sb.live == 0 and sb in self._spill_blocks:
+        if sb.live == 0 and id(sb) in self._spill_blocks:
             self._release_block(sb)
 
     def _slot_contents(self, pool: DevicePagePool, idx: torch.Tensor):
