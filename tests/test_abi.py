@@ -98,6 +98,12 @@ def test_validation_errors_raise_value_error():
     assert rc == _lib.VOOM_EINVAL and "multiple of 64" in _lib.last_error()
     rc = lib.voom_page_sums_verify(fake, fake, 4, 0, fake, None)
     assert rc == _lib.VOOM_EINVAL and "tag" in _lib.last_error()
+    rc = lib.voom_copy_rows(None, 64, fake, 64, 64, 3, None)
+    assert rc == _lib.VOOM_EINVAL and "null pointer" in _lib.last_error()
+    rc = lib.voom_copy_rows(fake, 64, fake, 32, 64, 3, None)  # rows would overlap
+    assert rc == _lib.VOOM_EINVAL and "exceeds a pitch" in _lib.last_error()
+    assert lib.voom_copy_rows(None, 0, None, 0, 0, 5, None) == 0  # nothing to copy
+    assert lib.voom_copy_rows(None, 0, None, 0, 64, 0, None) == 0
 
 
 def test_runtime_error_mapping():
