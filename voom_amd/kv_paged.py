@@ -718,9 +718,6 @@ class PagedKVCache:
         if filled:
             host[:, filled] = np.asarray([cols[page] for page in filled], np.int32).T
 
-    def _set_table(self, layer: int, page_idx: int, slots) -> None:
-        self._set_table_cols(layer, {page_idx: slots})
-
     # ---- reference protocol -------------------------------------------------
 
     @property
@@ -1124,9 +1121,6 @@ class PagedKVCache:
         if not self.verify_spills or not all(ops.slot_codec_supported(t) for t in pool.tensors):
             return 0
         return self._batch * len(pool.tensors)
-
-    def _record_bytes(self, pool: DevicePagePool) -> int:
-        return record_page_bytes(self._plane_parts(pool), self._nsum(pool))
 
     def _spill_plan(self, layer: int, pages: list[_Page]):
         """One host block for the layer's pages; returns its chunk work items."""
