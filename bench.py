@@ -438,9 +438,9 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
     best_reload = min(c[1] for c in cycles)
     # The host link measured on the arena's own pages: plain copies of the
     # same 32 record-sized blocks the spill wrote (first fit puts them where
-    # the spill's records were), in both directions.  Pinned host pages of
-    # one process do not all sustain the same DMA rate on these boxes, so
-    # this is the ceiling the spill and reload can reach with this memory.
+    # the spill's records were), in both directions: the ceiling the spill
+    # and reload can reach with this memory.  (The copy engine's first read
+    # of freshly pinned pages is slow; reserve() pays that before any spill.)
     rec_bytes = (S // PT // 2) * kv.page_nbytes + 4096
     blocks = [kv.arena.alloc(rec_bytes) for _ in range(L)]
     dev_rec = torch.empty(rec_bytes, dtype=torch.uint8, device="cuda")
@@ -683,10 +683,9 @@ def bench_long_context(steps: int, cpu_sample: bool) -> dict:
     torch.cuda.synchronize()
     copy_ms = c0.elapsed_time(c1) / 3
     del host_buf, dev_buf
-    # The same upload from where the spilled records actually sit: pinned
-    # pages of one process do not all sustain the same DMA rate, and the
-    # step's upload reads the arena's (each step's upload follows the last
-    # one on the copy stream, so this is the step's floor).
+    # The same upload from where the spilled records actually sit, the
+    # arena's pages (each step's upload follows the last one on the copy
+    # stream, so this is the step's floor).
     held = {id(p.host): p.host for p in kv._pages[0] if not p.resident and p.host is not None}
     records = [sb.record(r) for sb in held.values()
                for r in range(-(-sb.n_pages // sb.chunk))]
