@@ -1020,10 +1020,12 @@ class PagedKVCache:
         if self._copy_stream is not None:
             self._copy_stream.synchronize()
         # no kernel may still touch the host copies once they are given back
-        for sb in self._spill_blocks.values():
-            for ev in (sb.ready, sb.last_use):
-                if ev is not None:
-                    ev.synchronize()
+        # (the spills' events: one host wait per recording stream)
+        self._sync_ready(self._spill_blocks.values())
+        # a reload stamps one event on every block it read: each once
+        for ev in {id(sb.last_use): sb.last_use for sb in self._spill_blocks.values()
+                   if sb.last_use is not None}.values():
+            ev.synchronize()
         self._reap_frees(wait=True)
         if self._own_arena:
             self.arena.close()
