@@ -101,3 +101,29 @@ def test_position_free_attention_replays():
                                                   scale=D ** -0.5)]
 
     replay_matches_eager(run, lambda: run(1))
+
+
+def test_launch_stream_follows_torch_current_stream():
+    """Every op launches on the stream ops._stream(None) names: torch's current
+    stream, inside a stream context and under graph capture too (there the
+    capturing stream, or the launches would escape the graph)."""
+    print("[graph] launch stream lookup", flush=True)
+    assert ops._stream(None) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert ops._stream(None) == side.cuda_stream
+    seen = []
+    x = torch.zeros(16, device="cuda")
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            seen.append((ops._stream(None), torch.cuda.current_stream().cuda_stream))
+            x.add_(1)
+    torch.cuda.current_stream().wait_stream(cap)
+    assert seen[0][0] == seen[0][1] == cap.cuda_stream
+    graph.replay()
+    torch.cuda.synchronize()
+    assert float(x[0]) == 1.0

@@ -24,9 +24,19 @@ from .page_pool import v_slot_shape
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
+# The current stream's raw handle straight from torch (0.2 us against 2.8 us
+# through torch.cuda.current_stream(), called for every launch); the public
+# route where this torch build does not expose it.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_CUR_DEVICE = getattr(torch._C, "_cuda_getDevice", None)
+
+
 def _stream(stream: torch.cuda.Stream | None) -> int:
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return int(s.cuda_stream)
+    if stream is not None:
+        return int(stream.cuda_stream)
+    if _RAW_STREAM is not None and _CUR_DEVICE is not None:
+        return int(_RAW_STREAM(_CUR_DEVICE()))
+    return int(torch.cuda.current_stream().cuda_stream)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
