@@ -587,6 +587,62 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
     del orig
     kv.release()
     torch.cuda.empty_cache()
+    res["fragmented_spills"] = bench_fragmented_spills()
+    return res
+
+
+def bench_fragmented_spills() -> dict:
+    """Pages spilled one at a time, as the budget leaves them in a growing
+    decode: 100 pages of 256 KiB (one sequence, 8 kv heads, D = 128, 64-token
+    pages) spilled by one call (one host record) or by 100 calls (100 one-page
+    records), then attend() over the layer (the spilled pages reloaded for the
+    call) and reload() of them, on one cache; host-timed with a wait per call."""
+    import torch
+
+    from voom_amd.kv_paged import PagedKVCache
+
+    NQ, NKV, D, PT, n = 64, 8, 128, 64, 100
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    k = torch.randn((1, NKV, 200 * PT, D), generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn((1, NKV, 200 * PT, D), generator=gen, device="cuda").to(torch.bfloat16)
+    q = torch.randn((1, NQ, 1, D), generator=gen, device="cuda").to(torch.bfloat16)
+    kv = PagedKVCache(num_layers=1, max_bytes=1 << 40, page_positions=PT, resident_pages=1)
+    kv.append(0, k, v)
+    kv.arena.reserve(2 * n * kv.page_nbytes)
+    main = torch.cuda.current_stream()
+    res = {"pages": n, "page_bytes": kv.page_nbytes}
+    for mode in ("one_record", "one_page_records"):
+        att, rel = [], []
+        for cycle in range(4):
+            if mode == "one_record":
+                kv.spill([(0, i) for i in range(n)])
+            else:
+                for i in range(n):
+                    kv.spill([(0, i)])
+            torch.cuda.synchronize()
+            for rep in range(4):
+                t0 = time.perf_counter()
+                kv.attend(0, q)
+                main.synchronize()
+                if cycle and rep:
+                    att.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            kv.reload()
+            torch.cuda.synchronize()
+            if cycle:
+                rel.append(time.perf_counter() - t0)
+        res[mode] = {"attend_ms": sorted(att)[len(att) // 2] * 1e3,
+                     "reload_ms": sorted(rel)[len(rel) // 2] * 1e3}
+    K, V = kv.gather(0)
+    torch.cuda.synchronize()
+    res["exact"] = bool(torch.equal(K.view(torch.int16), k.view(torch.int16))
+                        and torch.equal(V.view(torch.int16), v.view(torch.int16)))
+    kv.release()
+    log(f"spills of one page at a time ({n} x {res['page_bytes'] >> 10} KiB): attend "
+        f"{res['one_page_records']['attend_ms']:.2f} ms, reload "
+        f"{res['one_page_records']['reload_ms']:.2f} ms (one record: "
+        f"{res['one_record']['attend_ms']:.2f} / {res['one_record']['reload_ms']:.2f} ms), "
+        f"exact={res['exact']}")
     return res
 
 
