@@ -77,7 +77,6 @@ def test_update_returns_everything_appended_even_after_spills():
         assert kv._pages[layer][-1].resident
 
 
-
 class count_staged_copies:
     """Counts the host -> staging-buffer transfers of a block: strided ones
     (ops.copy_rows) and plain tensor copies into a staging buffer."""
@@ -573,3 +572,33 @@ def test_attend_mla_prefill_of_one_token_is_attend_mla_bitwise():
                           return_weighted_c=True)
     assert torch.equal(bits(a[:, :, 0]), bits(b)) and torch.equal(bits(wa[:, :, 0]), bits(wb))
     kv.release()
+
+
+def test_side_stream_does_not_queue_behind_the_current_stream():
+    """The cache's upload stream is checked against the current stream's
+    hardware queue: whatever number of streams the process made before, a
+    marker on it completes while work enqueued earlier on the current stream
+    is still running (on a shared queue it would wait for that work)."""
+    from voom_amd.kv_paged import _side_stream_off_queue
+
+    print("[kv] side stream off the current stream's queue", flush=True)
+    dev = torch.device("cuda")
+    main = torch.cuda.current_stream()
+    scratch = torch.empty(32 << 20, dtype=torch.int32, device="cuda")
+    for extra in range(6):
+        for _ in range(extra):  # shift where the next new stream lands
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                torch.zeros(8, device="cuda").add_(1)
+        torch.cuda.synchronize()
+        side = _side_stream_off_queue(dev)
+        start, busy_end, marker = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        start.record(main)
+        for _ in range(20):
+            scratch.fill_(2)
+        busy_end.record(main)
+        marker.record(side)
+        torch.cuda.synchronize()
+        busy = start.elapsed_time(busy_end)
+        assert busy > 0.1, busy
+        assert start.elapsed_time(marker) < 0.5 * busy, (extra, start.elapsed_time(marker), busy)
