@@ -376,6 +376,9 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
     import numpy as np
     import torch
 
+    # first, before the 4 GiB of config 3 exist in this process
+    fragmented = bench_fragmented_spills()
+
     from voom_amd import ops
     from voom_amd.kv_paged import PagedKVCache
 
@@ -587,7 +590,7 @@ def bench_spill_reload(cpu_sample: bool) -> dict:
     del orig
     kv.release()
     torch.cuda.empty_cache()
-    res["fragmented_spills"] = bench_fragmented_spills()
+    res["fragmented_spills"] = fragmented
     return res
 
 
