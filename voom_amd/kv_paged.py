@@ -256,6 +256,8 @@ def _side_stream_off_queue(device: torch.device, tries: int = 8) -> torch.cuda.S
     where depends on how many streams the process made before, so each
     candidate is checked: a marker recorded on it must complete before about
     0.1 ms of fills enqueued earlier on the current stream have finished."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.cuda.Stream(device=device)  # no waits while a graph is captured
     main = torch.cuda.current_stream(device)
     scratch = torch.empty(16 << 20, dtype=torch.int32, device=device)
     cand = None
